@@ -1,0 +1,932 @@
+// Host side of the MI355X codec path: context, weight loader, the compress /
+// decompress drivers and the C ABI declared in include/boa_hip.h.
+//
+// Mirrors portability_solved_cpp/boa.cpp (compress_v2 :280-582, decompress_v2
+// :584-817) and boa_gpu.hpp (BoaPredictorGPU :944-1174) for the mambav1
+// backbone, on one HIP stream per context.  Differences by design:
+//   - bytes stay uint8 end to end (no int32 widening on the host);
+//   - the forward of a tile runs on all lanes of a batch at once
+//     (M = lanes x tile rows), the coder and the stream compaction run on
+//     the device, and only the compacted payload crosses PCIe;
+//   - errors are returned as codes, never exit().
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/boa_hip.h"
+#include "boa_kernels.h"
+#include "container.h"
+
+using namespace boa;
+
+namespace {
+
+constexpr int VOCAB = 256;
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct ProfRec {
+  int cls;
+  hipEvent_t a, b;
+  double work;
+};
+
+}  // namespace
+
+struct boa_ctx {
+  boa_config cfg{};
+  Dims D{};
+  hipStream_t own_stream = nullptr;
+  hipStream_t stream = nullptr;
+  std::string err;
+  bool loaded = false;
+  float inv_temp = 1.0f;
+
+  // weights (one device allocation)
+  float* wbuf = nullptr;
+  const float* emb = nullptr;
+  const float *hw1 = nullptr, *hb1 = nullptr, *hw2 = nullptr, *hb2 = nullptr;
+  std::vector<LayerW> layers;
+
+  // recurrent state for max_lanes lanes
+  float* conv_state = nullptr;  // [L][max_lanes][di][4]
+  float* ssm_state = nullptr;   // [L][max_lanes][di][ds]
+
+  // activations
+  int64_t rows_cap = 0;
+  float *x = nullptr, *xn = nullptr, *xz = nullptr, *cv = nullptr, *delta = nullptr, *y = nullptr,
+        *hid = nullptr, *logits = nullptr;
+  uint2* lowprob = nullptr;
+
+  // coder scratch
+  int64_t words_cap = 0;  // per-lane pitch x lanes
+  uint32_t* words = nullptr;
+  RcEnc* enc = nullptr;
+  RcDec* dec = nullptr;
+  int32_t* sizes = nullptr;
+  uint64_t* offsets = nullptr;
+  int32_t* lens = nullptr;
+  uint8_t* tok = nullptr;
+  int* t_counter = nullptr;
+  int32_t* h_sizes = nullptr;  // pinned
+
+  // profiling
+  bool prof_on = false;
+  std::vector<hipEvent_t> ev_pool;
+  std::vector<ProfRec> recs;
+  double prof_ms[BOA_K_COUNT] = {};
+  double prof_work[BOA_K_COUNT] = {};
+  int64_t prof_n[BOA_K_COUNT] = {};
+};
+
+namespace {
+
+int fail(boa_ctx* c, int code, const std::string& msg) {
+  if (c) c->err = msg;
+  return code;
+}
+
+int hip_fail(boa_ctx* c, hipError_t e, const char* where) {
+  return fail(c, BOA_E_HIP, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(c, expr)                                    \
+  do {                                                      \
+    hipError_t e_ = (expr);                                 \
+    if (e_ != hipSuccess) return hip_fail((c), e_, #expr); \
+  } while (0)
+
+template <class T>
+hipError_t dalloc(T** p, size_t count) {
+  *p = nullptr;
+  if (!count) count = 1;
+  return hipMalloc((void**)p, count * sizeof(T));
+}
+
+void dfree(void* p) {
+  if (p) (void)hipFree(p);
+}
+
+// ---- profiling -------------------------------------------------------------
+hipEvent_t take_event(boa_ctx* c) {
+  if (c->ev_pool.empty()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+  hipEvent_t e = c->ev_pool.back();
+  c->ev_pool.pop_back();
+  return e;
+}
+
+void prof_flush(boa_ctx* c) {
+  if (c->recs.empty()) return;
+  (void)hipEventSynchronize(c->recs.back().b);
+  for (auto& r : c->recs) {
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) c->prof_ms[r.cls] += ms;
+    c->prof_n[r.cls] += 1;
+    c->prof_work[r.cls] += r.work;
+    c->ev_pool.push_back(r.a);
+    c->ev_pool.push_back(r.b);
+  }
+  c->recs.clear();
+}
+
+template <class F>
+hipError_t timed(boa_ctx* c, int cls, double work, F&& f) {
+  if (!c->prof_on) return f();
+  hipEvent_t a = take_event(c), b = take_event(c);
+  if (!a || !b) return hipErrorOutOfMemory;
+  hipError_t e = hipEventRecord(a, c->stream);
+  if (e != hipSuccess) return e;
+  e = f();
+  if (e != hipSuccess) return e;
+  e = hipEventRecord(b, c->stream);
+  if (e != hipSuccess) return e;
+  c->recs.push_back({cls, a, b, work});
+  if (c->recs.size() >= 4096) prof_flush(c);
+  return hipSuccess;
+}
+
+// ---- model dims --------------------------------------------------------------
+Dims make_dims(const boa_config& cfg) {
+  Dims D{};
+  D.d = cfg.d_model;
+  D.L = cfg.n_layers;
+  D.di = 2 * cfg.d_model;
+  D.r = (cfg.d_model + 15) / 16;
+  D.ds = cfg.d_state;
+  D.R = D.r + 2 * D.ds;
+  D.ld_in = (int)round_up(2 * D.di, 128);
+  D.ld_x = (int)round_up(D.R, 128);
+  D.ld_out = (int)round_up(D.d, 128);
+  D.ld_1 = (int)round_up(4 * D.d, 128);
+  D.ld_2 = (int)round_up(D.d, 128);
+  D.ld_h1 = (int)round_up(D.d, 128);
+  D.ld_h2 = (int)round_up(VOCAB, 128);
+  return D;
+}
+
+int64_t row_bytes(const Dims& D) {
+  return 4 * (int64_t)(D.d + D.d + 2 * D.di + D.di + D.R + D.di + 4 * D.d + VOCAB) + 8;
+}
+
+int64_t pitch_words_for(int64_t chunk) { return (chunk * 10 + 4096 + 3) / 4; }
+
+int ensure_rows(boa_ctx* c, int64_t rows) {
+  if (rows <= c->rows_cap) return BOA_OK;
+  const Dims& D = c->D;
+  dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
+  dfree(c->hid); dfree(c->logits); dfree(c->lowprob);
+  c->rows_cap = 0;
+  size_t r = (size_t)rows;
+  if (dalloc(&c->x, r * D.d) || dalloc(&c->xn, r * D.d) || dalloc(&c->xz, r * 2 * D.di) ||
+      dalloc(&c->cv, r * D.di) || dalloc(&c->delta, r * D.R) || dalloc(&c->y, r * D.di) ||
+      dalloc(&c->hid, r * 4 * D.d) || dalloc(&c->logits, r * VOCAB) || dalloc(&c->lowprob, r))
+    return fail(c, BOA_E_NOMEM, "device allocation of activation buffers failed");
+  c->rows_cap = rows;
+  return BOA_OK;
+}
+
+int ensure_words(boa_ctx* c, int64_t pitch) {
+  const int64_t need = pitch * c->cfg.max_lanes;
+  if (need <= c->words_cap) return BOA_OK;
+  dfree(c->words);
+  c->words_cap = 0;
+  if (dalloc(&c->words, (size_t)need)) return fail(c, BOA_E_NOMEM, "device allocation of coder output failed");
+  c->words_cap = need;
+  return BOA_OK;
+}
+
+LayerW layer_at(const boa_ctx* c, int l) { return c->layers[l]; }
+float* conv_state_of(boa_ctx* c, int l) {
+  return c->conv_state + (size_t)l * c->cfg.max_lanes * c->D.di * 4;
+}
+float* ssm_state_of(boa_ctx* c, int l) {
+  return c->ssm_state + (size_t)l * c->cfg.max_lanes * c->D.di * c->D.ds;
+}
+
+hipError_t gemm(boa_ctx* c, const float* X, int ldx, const float* W, int ldw, float* C, int ldc,
+                const float* bias, const float* res, int ldr, int M, int N, int K, int act) {
+  GemmArgs a{X, ldx, W, ldw, C, ldc, bias, res, ldr, M, N, K, act};
+  return timed(c, BOA_K_GEMM, 2.0 * M * N * K, [&] { return gemm_f32(a, c->stream); });
+}
+
+// One mambav1 block on `rows` rows (boa_gpu.hpp:895-902 / :835-843):
+// res = x; x = LN1(x); x = Mamba(x); x = LN2(x); x = FF(x) + res.
+// x keeps the residual, LN1 writes xn, out_proj writes xn.
+hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, bool step,
+                         const TokenSrc* tok0, int t0, const uint8_t* step_tok) {
+  const Dims& D = c->D;
+  const LayerW W = layer_at(c, l);
+  hipStream_t s = c->stream;
+  hipError_t e;
+  const double ln_bytes = 3.0 * 4 * rows * D.d;
+  if (l == 0 && step) {
+    e = timed(c, BOA_K_LN, ln_bytes, [&] {
+      return launch_ln1_step(c->emb, step_tok, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, s,
+                             c->t_counter);
+    });
+  } else if (l == 0) {
+    e = timed(c, BOA_K_LN, ln_bytes, [&] {
+      return launch_ln1(c->emb, *tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, s);
+    });
+  } else {
+    e = timed(c, BOA_K_LN, ln_bytes, [&] {
+      return launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b,
+                        rows, D.d, s);
+    });
+  }
+  if (e) return e;
+  if ((e = gemm(c, c->xn, D.d, W.w_in, D.ld_in, c->xz, 2 * D.di, W.b_in, nullptr, 0, rows,
+                2 * D.di, D.d, ACT_NONE)))
+    return e;
+  const double conv_bytes = 4.0 * rows * D.di * 2;
+  e = timed(c, BOA_K_CONV, conv_bytes, [&] {
+    return step ? launch_conv_step(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes,
+                                   D.di, s)
+                : launch_conv_chunk(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes,
+                                    T, D.di, s);
+  });
+  if (e) return e;
+  if ((e = gemm(c, c->cv, D.di, W.w_x, D.ld_x, c->delta, D.R, nullptr, nullptr, 0, rows, D.R, D.di,
+                ACT_NONE)))
+    return e;
+  // algorithmic bytes: u, z, y per element, the delta row per token
+  const double scan_bytes = 4.0 * rows * (3.0 * D.di + D.R) +
+                            (step ? 8.0 * lanes * D.di * D.ds : 0.0);
+  e = timed(c, BOA_K_SCAN, scan_bytes, [&] {
+    return step ? launch_scan_step(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes, s)
+                : launch_scan_chunk(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes,
+                                    T, s);
+  });
+  if (e) return e;
+  if ((e = gemm(c, c->y, D.di, W.w_out, D.ld_out, c->xn, D.d, W.b_out, nullptr, 0, rows, D.d, D.di,
+                ACT_NONE)))
+    return e;
+  e = timed(c, BOA_K_LN, ln_bytes,
+            [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, s); });
+  if (e) return e;
+  if ((e = gemm(c, c->xn, D.d, W.w1, D.ld_1, c->hid, 4 * D.d, W.b1, nullptr, 0, rows, 4 * D.d, D.d,
+                ACT_GELU)))
+    return e;
+  return gemm(c, c->hid, 4 * D.d, W.w2, D.ld_2, c->x, D.d, W.b2, c->x, D.d, rows, D.d, 4 * D.d,
+              ACT_NONE);
+}
+
+hipError_t head_forward(boa_ctx* c, int rows, bool add_bias, float* logits) {
+  const Dims& D = c->D;
+  hipError_t e = gemm(c, c->x, D.d, c->hw1, D.ld_h1, c->xn, D.d, c->hb1, nullptr, 0, rows, D.d, D.d,
+                      ACT_RELU);
+  if (e) return e;
+  return gemm(c, c->xn, D.d, c->hw2, D.ld_h2, logits, VOCAB, add_bias ? c->hb2 : nullptr, nullptr, 0,
+              rows, VOCAB, D.d, ACT_NONE);
+}
+
+hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0, float* logits) {
+  const int rows = lanes * T;
+  for (int l = 0; l < c->D.L; ++l) {
+    hipError_t e = block_forward(c, l, rows, lanes, T, false, &tok, t0, nullptr);
+    if (e) return e;
+  }
+  return head_forward(c, rows, true, logits);
+}
+
+hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias, float* logits) {
+  for (int l = 0; l < c->D.L; ++l) {
+    hipError_t e = block_forward(c, l, lanes, lanes, 1, true, nullptr, 0, tok);
+    if (e) return e;
+  }
+  return head_forward(c, lanes, add_bias, logits);
+}
+
+int check_ready(boa_ctx* c) {
+  if (!c) return BOA_E_ARG;
+  if (!c->loaded) return fail(c, BOA_E_STATE, "no weights loaded");
+  return BOA_OK;
+}
+
+int64_t auto_tile(const boa_ctx* c, int64_t chunk, int lanes) {
+  if (c->cfg.tile > 0) return std::min<int64_t>(c->cfg.tile, chunk);
+  const int64_t budget = (int64_t)24 << 30;
+  int64_t rows = budget / row_bytes(c->D);
+  int64_t T = rows / std::max(lanes, 1);
+  T = std::max<int64_t>(64, T / 64 * 64);
+  T = std::min<int64_t>(T, 2048);
+  return std::min<int64_t>(T, chunk);
+}
+
+__global__ void gather_first_kernel(const uint8_t* base, int64_t stride, int64_t total, int lanes,
+                                    uint8_t* first) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  int64_t pos = (int64_t)b * stride;
+  first[b] = pos < total ? base[pos] : 0;
+}
+
+__global__ void neg_exp_kernel(const float* a_log, float* out, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = -expf_(a_log[i]);
+}
+
+__global__ void decode_init_kernel(const uint8_t* first, const int32_t* lens, uint8_t* tok,
+                                   uint8_t* out, int64_t out_stride, int lanes, int* t_counter) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b == 0) *t_counter = 0;
+  if (b >= lanes) return;
+  tok[b] = first[b];
+  if (lens[b] > 0) out[(size_t)b * out_stride] = first[b];
+}
+
+// ---- weight parsing ----------------------------------------------------------
+struct HostReader {
+  const uint8_t* p;
+  size_t n, pos;
+  bool fp16, bad;
+  void vec(std::vector<float>& dst, size_t count) {
+    dst.resize(count);
+    const size_t esz = fp16 ? 2 : 4;
+    if (bad || pos + count * esz > n) { bad = true; return; }
+    if (fp16) {
+      for (size_t i = 0; i < count; ++i) {
+        uint16_t h;
+        memcpy(&h, p + pos + 2 * i, 2);
+        dst[i] = boa_host_half_to_float(h);
+      }
+    } else {
+      memcpy(dst.data(), p + pos, count * 4);
+    }
+    pos += count * esz;
+  }
+};
+
+}  // namespace
+
+// ================================================================ C ABI
+extern "C" {
+
+int64_t boa_weight_file_bytes(int32_t d, int32_t L, int32_t ds, int32_t fp16) {
+  const int64_t di = 2 * (int64_t)d, r = (d + 15) / 16, R = r + 2 * (int64_t)ds;
+  const int64_t per_layer = 2 * d + 2 * di * d + 2 * di + di * 4 + di + R * di + di * r + di +
+                            di * ds + di + d * di + d + 2 * d + 4 * (int64_t)d * d + 4 * d +
+                            4 * (int64_t)d * d + d;
+  const int64_t elems = 256 * (int64_t)d + L * per_layer + (int64_t)d * d + d + 256 * (int64_t)d + 256;
+  return 4 + elems * (fp16 ? 2 : 4);
+}
+
+int boa_create(const boa_config* cfg, boa_ctx** out) {
+  if (!cfg || !out) return BOA_E_ARG;
+  *out = nullptr;
+  if (cfg->d_model < 16 || cfg->d_model % 16 || cfg->d_model > 512 || cfg->n_layers < 1 ||
+      (cfg->d_state != 16 && cfg->d_state != 32) || cfg->max_lanes < 1 || cfg->max_lanes > 65535 ||
+      cfg->precision != 0 || cfg->tile < 0)
+    return BOA_E_ARG;
+  boa_ctx* c = new boa_ctx();
+  c->cfg = *cfg;
+  if (!(c->cfg.temperature > 0.0f)) c->cfg.temperature = 1.0f;
+  c->inv_temp = 1.0f / c->cfg.temperature;
+  c->D = make_dims(*cfg);
+  hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) { delete c; return BOA_E_HIP; }
+  c->stream = c->own_stream;
+  const Dims& D = c->D;
+  const size_t L = D.L, B = cfg->max_lanes;
+  if (dalloc(&c->conv_state, L * B * D.di * 4) || dalloc(&c->ssm_state, L * B * D.di * D.ds) ||
+      dalloc(&c->enc, B) || dalloc(&c->dec, B) || dalloc(&c->sizes, B) || dalloc(&c->offsets, B) ||
+      dalloc(&c->lens, B) || dalloc(&c->tok, B) || dalloc(&c->t_counter, 1) ||
+      hipHostMalloc((void**)&c->h_sizes, sizeof(int32_t) * B) != hipSuccess) {
+    boa_destroy(c);
+    return BOA_E_NOMEM;
+  }
+  *out = c;
+  return BOA_OK;
+}
+
+void boa_destroy(boa_ctx* c) {
+  if (!c) return;
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  prof_flush(c);
+  for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
+  dfree(c->wbuf);
+  dfree(c->conv_state); dfree(c->ssm_state);
+  dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
+  dfree(c->hid); dfree(c->logits); dfree(c->lowprob);
+  dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
+  dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
+  if (c->h_sizes) (void)hipHostFree(c->h_sizes);
+  if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+const char* boa_last_error(const boa_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int boa_set_stream(boa_ctx* c, void* s) {
+  if (!c) return BOA_E_ARG;
+  c->stream = (hipStream_t)s;
+  return BOA_OK;
+}
+
+int boa_use_own_stream(boa_ctx* c) {
+  if (!c) return BOA_E_ARG;
+  c->stream = c->own_stream;
+  return BOA_OK;
+}
+
+int boa_set_temperature(boa_ctx* c, float t) {
+  if (!c || !(t > 0.0f)) return BOA_E_ARG;
+  c->cfg.temperature = t;
+  c->inv_temp = 1.0f / t;
+  return BOA_OK;
+}
+
+int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
+  if (!c || !data) return BOA_E_ARG;
+  const Dims& D = c->D;
+  const uint8_t* p = (const uint8_t*)data;
+  HostReader rd{p, n, 0, false, false};
+  // boa_gpu.hpp:994-1006: "BOA" + 0x01 is fp16, "BOA" + other byte is fp32,
+  // anything else is a headerless fp32 file.
+  const bool hdr = n >= 4 && p[0] == 'B' && p[1] == 'O' && p[2] == 'A';
+  if (hdr) { rd.fp16 = p[3] == 0x01; rd.pos = 4; }
+  const int64_t expect = boa_weight_file_bytes(D.d, D.L, D.ds, rd.fp16) - (hdr ? 0 : 4);
+  if ((int64_t)n != expect) {
+    char msg[256];
+    snprintf(msg, sizeof msg,
+             "weight file has %zu bytes, expected %lld for d_model=%d n_layers=%d d_state=%d", n,
+             (long long)expect, D.d, D.L, D.ds);
+    return fail(c, BOA_E_FORMAT, msg);
+  }
+  // device layout: Linear weights transposed to [in][ld] with ld a multiple
+  // of 128 (zero padded) so every GEMM tile load stays in bounds.
+  std::vector<std::pair<size_t, std::vector<float>>> parts;  // (offset floats, data)
+  size_t total = 0;
+  auto place = [&](std::vector<float>&& v) -> size_t {
+    size_t off = total;
+    total += round_up((int64_t)v.size(), 64);
+    parts.emplace_back(off, std::move(v));
+    return off;
+  };
+  auto linear_t = [&](int rows, int cols, int ld) -> size_t {
+    std::vector<float> w;
+    rd.vec(w, (size_t)rows * cols);
+    std::vector<float> t((size_t)cols * ld, 0.0f);
+    if (!rd.bad)
+      for (int i = 0; i < rows; ++i)
+        for (int j = 0; j < cols; ++j) t[(size_t)j * ld + i] = w[(size_t)i * cols + j];
+    return place(std::move(t));
+  };
+  auto raw = [&](size_t count) -> size_t {
+    std::vector<float> v;
+    rd.vec(v, count);
+    return place(std::move(v));
+  };
+  struct LayerOff {
+    size_t ln1_w, ln1_b, w_in, b_in, conv_w, conv_b, w_x, w_dt, b_dt, a_log, neg_a, dd, w_out, b_out,
+        ln2_w, ln2_b, w1, b1, w2, b2;
+  };
+  std::vector<LayerOff> lo(D.L);
+  const size_t emb = raw((size_t)VOCAB * D.d);
+  for (int l = 0; l < D.L; ++l) {
+    LayerOff& o = lo[l];
+    o.ln1_w = raw(D.d);
+    o.ln1_b = raw(D.d);
+    o.w_in = linear_t(2 * D.di, D.d, D.ld_in);
+    o.b_in = raw(2 * D.di);
+    o.conv_w = raw((size_t)D.di * 4);
+    o.conv_b = raw(D.di);
+    o.w_x = linear_t(D.R, D.di, D.ld_x);
+    {  // dt_proj [di][r] stored as [r][di] (no padding: read per channel)
+      std::vector<float> w;
+      rd.vec(w, (size_t)D.di * D.r);
+      std::vector<float> t((size_t)D.r * D.di, 0.0f);
+      if (!rd.bad)
+        for (int i = 0; i < D.di; ++i)
+          for (int j = 0; j < D.r; ++j) t[(size_t)j * D.di + i] = w[(size_t)i * D.r + j];
+      o.w_dt = place(std::move(t));
+    }
+    o.b_dt = raw(D.di);
+    o.a_log = raw((size_t)D.di * D.ds);
+    o.neg_a = place(std::vector<float>((size_t)D.di * D.ds, 0.0f));
+    o.dd = raw(D.di);
+    o.w_out = linear_t(D.d, D.di, D.ld_out);
+    o.b_out = raw(D.d);
+    o.ln2_w = raw(D.d);
+    o.ln2_b = raw(D.d);
+    o.w1 = linear_t(4 * D.d, D.d, D.ld_1);
+    o.b1 = raw(4 * D.d);
+    o.w2 = linear_t(D.d, 4 * D.d, D.ld_2);
+    o.b2 = raw(D.d);
+  }
+  const size_t hw1 = linear_t(D.d, D.d, D.ld_h1);
+  const size_t hb1 = raw(D.d);
+  const size_t hw2 = linear_t(VOCAB, D.d, D.ld_h2);
+  const size_t hb2 = raw(VOCAB);
+  if (rd.bad || rd.pos != n) return fail(c, BOA_E_FORMAT, "weight file truncated");
+
+  dfree(c->wbuf);
+  c->wbuf = nullptr;
+  c->loaded = false;
+  if (dalloc(&c->wbuf, total)) return fail(c, BOA_E_NOMEM, "device allocation of weights failed");
+  for (auto& pr : parts)
+    if (!pr.second.empty())
+      HIP_TRY(c, hipMemcpyAsync(c->wbuf + pr.first, pr.second.data(), pr.second.size() * 4,
+                                hipMemcpyHostToDevice, c->stream));
+  float* w = c->wbuf;
+  c->emb = w + emb;
+  c->hw1 = w + hw1; c->hb1 = w + hb1; c->hw2 = w + hw2; c->hb2 = w + hb2;
+  c->layers.resize(D.L);
+  for (int l = 0; l < D.L; ++l) {
+    const LayerOff& o = lo[l];
+    LayerW& L = c->layers[l];
+    L.ln1_w = w + o.ln1_w; L.ln1_b = w + o.ln1_b; L.w_in = w + o.w_in; L.b_in = w + o.b_in;
+    L.conv_w = w + o.conv_w; L.conv_b = w + o.conv_b; L.w_x = w + o.w_x; L.w_dt = w + o.w_dt;
+    L.b_dt = w + o.b_dt; L.neg_exp_a = w + o.neg_a; L.dd = w + o.dd; L.w_out = w + o.w_out;
+    L.b_out = w + o.b_out; L.ln2_w = w + o.ln2_w; L.ln2_b = w + o.ln2_b; L.w1 = w + o.w1;
+    L.b1 = w + o.b1; L.w2 = w + o.w2; L.b2 = w + o.b2;
+    // -exp(A_log) once per load (mamba_kernels.cu:430-437), on the device so
+    // that it is the same exp the kernels use.
+    const int nA = D.di * D.ds;
+    hipLaunchKernelGGL(neg_exp_kernel, dim3((nA + 255) / 256), dim3(256), 0, c->stream,
+                       w + o.a_log, w + o.neg_a, nA);
+    HIP_TRY(c, hipGetLastError());
+  }
+  HIP_TRY(c, hipStreamSynchronize(c->stream));
+  c->loaded = true;
+  return BOA_OK;
+}
+
+int boa_load_weights(boa_ctx* c, const char* path) {
+  if (!c || !path) return BOA_E_ARG;
+  std::vector<uint8_t> buf;
+  if (!boa_read_file(path, buf)) return fail(c, BOA_E_IO, std::string("cannot read ") + path);
+  return boa_load_weights_mem(c, buf.data(), buf.size());
+}
+
+int64_t boa_estimate_memory(const boa_config* cfg, int64_t chunk, int32_t compress) {
+  if (!cfg) return -1;
+  Dims D = make_dims(*cfg);
+  const int64_t B = cfg->max_lanes;
+  int64_t w = boa_weight_file_bytes(D.d, D.L, D.ds, 0) * 2;  // padded transposes, upper bound
+  int64_t state = 4 * (int64_t)D.L * B * D.di * (4 + D.ds);
+  int64_t rows = B;
+  int64_t words = 0;
+  if (compress) {
+    boa_ctx tmp;
+    tmp.cfg = *cfg;
+    tmp.D = D;
+    rows = B * auto_tile(&tmp, chunk, (int)B);
+    words = 4 * pitch_words_for(chunk) * B;
+  }
+  return w + state + rows * row_bytes(D) + words + (compress ? 0 : B * chunk);
+}
+
+int boa_reset_state(boa_ctx* c, int32_t lanes) {
+  if (!c || lanes < 0 || lanes > c->cfg.max_lanes) return BOA_E_ARG;
+  const Dims& D = c->D;
+  for (int l = 0; l < D.L; ++l) {
+    HIP_TRY(c, launch_fill_zero(conv_state_of(c, l), sizeof(float) * (size_t)lanes * D.di * 4, c->stream));
+    HIP_TRY(c, launch_fill_zero(ssm_state_of(c, l), sizeof(float) * (size_t)lanes * D.di * D.ds, c->stream));
+  }
+  return BOA_OK;
+}
+
+int boa_forward_chunk(boa_ctx* c, const uint8_t* d_tokens, int32_t lanes, int32_t T,
+                      float* d_logits) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!d_tokens || !d_logits || lanes < 1 || lanes > c->cfg.max_lanes || T < 1)
+    return fail(c, BOA_E_ARG, "boa_forward_chunk: bad arguments");
+  if ((rc = ensure_rows(c, (int64_t)lanes * T))) return rc;
+  TokenSrc tok{d_tokens, T, (int64_t)lanes * T};
+  HIP_TRY(c, forward_tile(c, tok, lanes, T, 0, d_logits));
+  return BOA_OK;
+}
+
+int boa_step_batch(boa_ctx* c, const uint8_t* d_tokens, int32_t lanes, float* d_logits,
+                   int32_t add_bias) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!d_tokens || !d_logits || lanes < 1 || lanes > c->cfg.max_lanes)
+    return fail(c, BOA_E_ARG, "boa_step_batch: bad arguments");
+  if ((rc = ensure_rows(c, lanes))) return rc;
+  HIP_TRY(c, step_forward(c, d_tokens, lanes, add_bias != 0, d_logits));
+  return BOA_OK;
+}
+
+int boa_cdf_from_logits(boa_ctx* c, const float* d_logits, const float* d_bias, int32_t rows,
+                        uint32_t* d_qcdf) {
+  if (!c || !d_logits || !d_qcdf || rows < 1) return BOA_E_ARG;
+  HIP_TRY(c, launch_cdf_rows(d_logits, d_bias, c->inv_temp, rows, d_qcdf, c->stream));
+  return BOA_OK;
+}
+
+int boa_rc_encode_cdf(boa_ctx* c, const uint32_t* d_cdf, const uint8_t* d_syms, int32_t n_sym,
+                      int32_t lanes, uint32_t* d_words, int64_t pitch_words, int32_t* d_sizes) {
+  if (!c || !d_cdf || !d_syms || !d_words || !d_sizes || n_sym < 0 || lanes < 1 ||
+      pitch_words < 2 * (int64_t)n_sym + 4)
+    return BOA_E_ARG;
+  HIP_TRY(c, launch_rc_encode_cdf(d_cdf, d_syms, n_sym, lanes, d_words, pitch_words, d_sizes, c->stream));
+  return BOA_OK;
+}
+
+int boa_rc_decode_cdf(boa_ctx* c, const uint32_t* d_cdf, int32_t n_sym, int32_t lanes,
+                      const uint32_t* d_words, int64_t pitch_words, const int32_t* d_sizes,
+                      uint8_t* d_syms) {
+  if (!c || !d_cdf || !d_syms || !d_words || !d_sizes || n_sym < 0 || lanes < 1) return BOA_E_ARG;
+  HIP_TRY(c, launch_rc_decode_cdf(d_cdf, n_sym, lanes, d_words, pitch_words, d_sizes, d_syms, c->stream));
+  return BOA_OK;
+}
+
+int64_t boa_num_chunks(int64_t n, int64_t chunk, int32_t max_chunks) {
+  if (chunk <= 0 || n < 0) return -1;
+  int64_t nc = (n + chunk - 1) / chunk;
+  if (max_chunks > 0 && nc > max_chunks) nc = max_chunks;
+  return nc;
+}
+
+int64_t boa_payload_bound_words(int64_t n, int64_t chunk, int32_t max_chunks) {
+  int64_t nc = boa_num_chunks(n, chunk, max_chunks);
+  if (nc < 0) return -1;
+  return nc * pitch_words_for(chunk);
+}
+
+int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t chunk,
+                        int32_t max_chunks, uint32_t* d_payload, int64_t payload_cap_words,
+                        uint64_t* h_stream_bytes, uint8_t* h_first, int64_t* h_payload_words) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!d_data || !d_payload || !h_stream_bytes || !h_first || n < 0 || chunk < 1 ||
+      chunk > (1 << 30))
+    return fail(c, BOA_E_ARG, "boa_compress_device: bad arguments");
+  const int64_t nc = boa_num_chunks(n, chunk, max_chunks);
+  const int B = c->cfg.max_lanes;
+  const int64_t pitch = pitch_words_for(chunk);
+  const int64_t T = auto_tile(c, chunk, (int)std::min<int64_t>(B, std::max<int64_t>(nc, 1)));
+  if ((rc = ensure_rows(c, (int64_t)B * T))) return rc;
+  if ((rc = ensure_words(c, pitch))) return rc;
+  uint8_t* d_first = nullptr;
+  if (dalloc(&d_first, (size_t)B)) return fail(c, BOA_E_NOMEM, "allocation failed");
+  int64_t out_words = 0;
+  hipStream_t s = c->stream;
+  for (int64_t c0 = 0; c0 < nc; c0 += B) {
+    const int lanes = (int)std::min<int64_t>(B, nc - c0);
+    const TokenSrc tok{d_data + c0 * chunk, chunk, n - c0 * chunk};
+    if ((rc = boa_reset_state(c, lanes))) { dfree(d_first); return rc; }
+    hipError_t e = launch_rc_enc_init(c->enc, lanes, s);
+    if (e) { dfree(d_first); return hip_fail(c, e, "rc init"); }
+    for (int64_t t0 = 0; t0 < chunk; t0 += T) {
+      const int Tt = (int)std::min<int64_t>(T, chunk - t0);
+      e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
+      if (!e)
+        e = timed(c, BOA_K_CDF, 1024.0 * lanes * Tt, [&] {
+          return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
+                                           c->lowprob, s);
+        });
+      if (!e)
+        e = timed(c, BOA_K_CODER, 8.0 * lanes * Tt, [&] {
+          return launch_rc_encode_tile(c->lowprob, tok, Tt, (int)t0, lanes, c->enc, c->words,
+                                       pitch, s);
+        });
+      if (e) { dfree(d_first); return hip_fail(c, e, "compress tile"); }
+    }
+    e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
+    if (!e) e = hipMemcpyAsync(c->h_sizes, c->sizes, sizeof(int32_t) * lanes, hipMemcpyDeviceToHost, s);
+    if (!e) e = hipStreamSynchronize(s);
+    if (e) { dfree(d_first); return hip_fail(c, e, "finish"); }
+    int64_t batch_words = 0;
+    for (int b = 0; b < lanes; ++b) batch_words += c->h_sizes[b];
+    if (out_words + batch_words > payload_cap_words) {
+      dfree(d_first);
+      return fail(c, BOA_E_ARG, "payload buffer too small");
+    }
+    e = timed(c, BOA_K_CODER, 8.0 * batch_words, [&] {
+      return launch_compact(c->words, pitch, c->sizes, lanes, c->offsets, d_payload + out_words, s);
+    });
+    if (!e) {
+      hipLaunchKernelGGL(gather_first_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, tok.base,
+                         tok.stride, tok.total, lanes, d_first);
+      e = hipGetLastError();
+    }
+    if (!e) e = hipMemcpyAsync(h_first + c0, d_first, lanes, hipMemcpyDeviceToHost, s);
+    if (!e) e = hipStreamSynchronize(s);
+    if (e) { dfree(d_first); return hip_fail(c, e, "compaction"); }
+    for (int b = 0; b < lanes; ++b) h_stream_bytes[c0 + b] = 4ull * (uint64_t)c->h_sizes[b];
+    out_words += batch_words;
+  }
+  dfree(d_first);
+  if (h_payload_words) *h_payload_words = out_words;
+  return BOA_OK;
+}
+
+int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t* h_offsets_words,
+                          const uint64_t* h_stream_bytes, const uint8_t* h_first, int32_t nc,
+                          int64_t chunk, int64_t last_len, uint8_t* d_out) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!d_payload || !h_offsets_words || !h_stream_bytes || !h_first || !d_out || nc < 0 ||
+      chunk < 1 || last_len < 0 || last_len > chunk)
+    return fail(c, BOA_E_ARG, "boa_decompress_device: bad arguments");
+  const int B = c->cfg.max_lanes;
+  if ((rc = ensure_rows(c, B))) return rc;
+  hipStream_t s = c->stream;
+  std::vector<uint64_t> offs(B);
+  std::vector<int32_t> nw(B), lens(B);
+  uint8_t* d_first = nullptr;
+  if (dalloc(&d_first, (size_t)B)) return fail(c, BOA_E_NOMEM, "allocation failed");
+  const int64_t pitch_bytes = pitch_words_for(chunk) * 4;
+  for (int64_t c0 = 0; c0 < nc; c0 += B) {
+    const int lanes = (int)std::min<int64_t>(B, nc - c0);
+    int32_t maxlen = 0;
+    for (int b = 0; b < lanes; ++b) {
+      const int64_t ci = c0 + b;
+      if ((int64_t)h_stream_bytes[ci] > pitch_bytes) {
+        dfree(d_first);
+        return fail(c, BOA_E_FORMAT, "stream too large for the chunk length");
+      }
+      offs[b] = h_offsets_words[ci];
+      nw[b] = (int32_t)(h_stream_bytes[ci] / 4);
+      lens[b] = (int32_t)(ci == nc - 1 ? last_len : chunk);
+      maxlen = std::max(maxlen, lens[b]);
+    }
+    hipError_t e = hipMemcpyAsync(c->offsets, offs.data(), 8 * lanes, hipMemcpyHostToDevice, s);
+    if (!e) e = hipMemcpyAsync(c->sizes, nw.data(), 4 * lanes, hipMemcpyHostToDevice, s);
+    if (!e) e = hipMemcpyAsync(c->lens, lens.data(), 4 * lanes, hipMemcpyHostToDevice, s);
+    if (!e) e = hipMemcpyAsync(d_first, h_first + c0, lanes, hipMemcpyHostToDevice, s);
+    if (e) { dfree(d_first); return hip_fail(c, e, "decode upload"); }
+    if ((rc = boa_reset_state(c, lanes))) { dfree(d_first); return rc; }
+    uint8_t* out = d_out + c0 * chunk;
+    hipLaunchKernelGGL(decode_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, d_first,
+                       c->lens, c->tok, out, chunk, lanes, c->t_counter);
+    e = hipGetLastError();
+    if (!e) e = launch_rc_dec_init(c->dec, d_payload, c->offsets, c->sizes, lanes, s);
+    if (e) { dfree(d_first); return hip_fail(c, e, "decode init"); }
+    // The step kernel of layer 0 advances the device-side t counter, the
+    // decode kernel reads it: the sequence of launches is identical for
+    // every step (graph-capturable).
+    for (int32_t t = 1; t < maxlen; ++t) {
+      e = step_forward(c, c->tok, lanes, false, c->logits);
+      if (!e)
+        e = timed(c, BOA_K_DECODE, 1024.0 * lanes, [&] {
+          return launch_decode_step(c->logits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter,
+                                    out, chunk, c->dec, d_payload, c->offsets, c->sizes, lanes, s);
+        });
+      if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }
+    }
+    e = hipStreamSynchronize(s);
+    if (e) { dfree(d_first); return hip_fail(c, e, "decode sync"); }
+  }
+  dfree(d_first);
+  return BOA_OK;
+}
+
+int boa_compress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, int64_t chunk,
+                        int32_t max_chunks, uint8_t** h_out, int64_t* out_len) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if ((!h_in && n) || !h_out || !out_len || chunk < 1) return fail(c, BOA_E_ARG, "bad arguments");
+  const int64_t nc = boa_num_chunks(n, chunk, max_chunks);
+  const int64_t processed = std::min<int64_t>(n, nc * chunk);
+  uint8_t* d_in = nullptr;
+  uint32_t* d_pay = nullptr;
+  const int64_t cap = std::max<int64_t>(boa_payload_bound_words(n, chunk, max_chunks), 1);
+  if (dalloc(&d_in, (size_t)std::max<int64_t>(n, 1)) || dalloc(&d_pay, (size_t)cap)) {
+    dfree(d_in);
+    return fail(c, BOA_E_NOMEM, "allocation failed");
+  }
+  if (n) {
+    hipError_t e = hipMemcpyAsync(d_in, h_in, (size_t)n, hipMemcpyHostToDevice, c->stream);
+    if (e) { dfree(d_in); dfree(d_pay); return hip_fail(c, e, "upload"); }
+  }
+  std::vector<uint64_t> lens((size_t)std::max<int64_t>(nc, 1));
+  std::vector<uint8_t> first((size_t)std::max<int64_t>(nc, 1));
+  int64_t words = 0;
+  rc = boa_compress_device(c, d_in, n, chunk, max_chunks, d_pay, cap, lens.data(), first.data(), &words);
+  if (rc) { dfree(d_in); dfree(d_pay); return rc; }
+  std::vector<uint8_t> payload((size_t)words * 4);
+  if (words) {
+    hipError_t e = hipMemcpy(payload.data(), d_pay, (size_t)words * 4, hipMemcpyDeviceToHost);
+    if (e) { dfree(d_in); dfree(d_pay); return hip_fail(c, e, "download"); }
+  }
+  dfree(d_in);
+  dfree(d_pay);
+  Boa2Header h;
+  h.total_size = (uint64_t)processed;
+  h.chunk_len = (uint32_t)chunk;
+  h.n_chunks = (uint32_t)nc;
+  h.last_chunk_len = (uint32_t)(nc > 1 ? processed - (nc - 1) * chunk : processed);
+  std::vector<uint8_t> blob;
+  boa2_write(h, payload, first.data(), lens.data(), (size_t)nc, blob);
+  uint8_t* o = (uint8_t*)malloc(blob.size() ? blob.size() : 1);
+  if (!o) return fail(c, BOA_E_NOMEM, "host allocation failed");
+  memcpy(o, blob.data(), blob.size());
+  *h_out = o;
+  *out_len = (int64_t)blob.size();
+  return BOA_OK;
+}
+
+int boa_decompress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, uint8_t** h_out,
+                          int64_t* out_len) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!h_in || !h_out || !out_len) return fail(c, BOA_E_ARG, "bad arguments");
+  Boa2Parsed P;
+  std::string why;
+  if (!boa2_parse(h_in, (size_t)n, P, why)) return fail(c, BOA_E_FORMAT, why);
+  if (P.hdr.flags & 1u) return fail(c, BOA_E_FORMAT, "warm-start containers are not supported");
+  const size_t nc = P.hdr.n_chunks;
+  // streams re-packed on 32-bit word boundaries
+  std::vector<uint64_t> offs(std::max<size_t>(nc, 1)), lens(std::max<size_t>(nc, 1));
+  uint64_t words = 0;
+  for (size_t i = 0; i < nc; ++i) {
+    offs[i] = words;
+    lens[i] = P.lengths[i];
+    words += (P.lengths[i] + 3) / 4;
+  }
+  std::vector<uint32_t> packed((size_t)std::max<uint64_t>(words, 1), 0u);
+  for (size_t i = 0; i < nc; ++i)
+    memcpy(packed.data() + offs[i], h_in + P.payload_off + P.offsets[i], P.lengths[i]);
+  int64_t total = 0;
+  for (size_t i = 0; i < nc; ++i) total += (i == nc - 1) ? P.hdr.last_chunk_len : P.hdr.chunk_len;
+  uint32_t* d_pay = nullptr;
+  uint8_t* d_out = nullptr;
+  if (dalloc(&d_pay, packed.size()) || dalloc(&d_out, (size_t)std::max<int64_t>(total, 1))) {
+    dfree(d_pay);
+    return fail(c, BOA_E_NOMEM, "allocation failed");
+  }
+  hipError_t e = hipMemcpy(d_pay, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
+  if (e) { dfree(d_pay); dfree(d_out); return hip_fail(c, e, "upload"); }
+  rc = boa_decompress_device(c, d_pay, offs.data(), lens.data(), P.first.data(), (int32_t)nc,
+                             P.hdr.chunk_len, nc ? P.hdr.last_chunk_len : 0, d_out);
+  if (rc) { dfree(d_pay); dfree(d_out); return rc; }
+  uint8_t* o = (uint8_t*)malloc((size_t)std::max<int64_t>(total, 1));
+  if (!o) { dfree(d_pay); dfree(d_out); return fail(c, BOA_E_NOMEM, "host allocation failed"); }
+  if (total) e = hipMemcpy(o, d_out, (size_t)total, hipMemcpyDeviceToHost);
+  dfree(d_pay);
+  dfree(d_out);
+  if (e) { free(o); return hip_fail(c, e, "download"); }
+  *h_out = o;
+  *out_len = total;
+  return BOA_OK;
+}
+
+int boa_compress_file(boa_ctx* c, const char* in_path, const char* out_path, int64_t chunk,
+                      int32_t max_chunks) {
+  if (!c || !in_path || !out_path) return BOA_E_ARG;
+  std::vector<uint8_t> in;
+  if (!boa_read_file(in_path, in)) return fail(c, BOA_E_IO, std::string("cannot read ") + in_path);
+  uint8_t* out = nullptr;
+  int64_t n = 0;
+  int rc = boa_compress_buffer(c, in.data(), (int64_t)in.size(), chunk, max_chunks, &out, &n);
+  if (rc) return rc;
+  bool ok = boa_write_file(out_path, out, (size_t)n);
+  free(out);
+  return ok ? BOA_OK : fail(c, BOA_E_IO, std::string("cannot write ") + out_path);
+}
+
+int boa_decompress_file(boa_ctx* c, const char* in_path, const char* out_path) {
+  if (!c || !in_path || !out_path) return BOA_E_ARG;
+  std::vector<uint8_t> in;
+  if (!boa_read_file(in_path, in)) return fail(c, BOA_E_IO, std::string("cannot read ") + in_path);
+  uint8_t* out = nullptr;
+  int64_t n = 0;
+  int rc = boa_decompress_buffer(c, in.data(), (int64_t)in.size(), &out, &n);
+  if (rc) return rc;
+  bool ok = boa_write_file(out_path, out, (size_t)n);
+  free(out);
+  return ok ? BOA_OK : fail(c, BOA_E_IO, std::string("cannot write ") + out_path);
+}
+
+void boa_free(void* p) { free(p); }
+
+uint32_t boa_crc32(const uint8_t* data, int64_t n) { return boa2_crc32(data, (size_t)n); }
+
+int boa_profile_enable(boa_ctx* c, int32_t on) {
+  if (!c) return BOA_E_ARG;
+  if (!on) prof_flush(c);
+  c->prof_on = on != 0;
+  return BOA_OK;
+}
+
+int boa_profile_reset(boa_ctx* c) {
+  if (!c) return BOA_E_ARG;
+  prof_flush(c);
+  for (int k = 0; k < BOA_K_COUNT; ++k) { c->prof_ms[k] = 0; c->prof_work[k] = 0; c->prof_n[k] = 0; }
+  return BOA_OK;
+}
+
+int boa_profile_read(boa_ctx* c, int32_t k, double* ms, int64_t* n, double* work) {
+  if (!c || k < 0 || k >= BOA_K_COUNT) return BOA_E_ARG;
+  prof_flush(c);
+  if (ms) *ms = c->prof_ms[k];
+  if (n) *n = c->prof_n[k];
+  if (work) *work = c->prof_work[k];
+  return BOA_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+// `boa` command-line driver over the C ABI (include/boa_hip.h).
+//
+// Same invocation as the reference driver (portability_solved_cpp/boa.cpp
+// :819-942):
+//   boa <compress|decompress> <model.bin> <input> <output> [d_model=256]
+//       [n_layers=1] [--gpu-batch B] [--max-chunks C] [--chunk-size S]
+//       [--tile T] [--temperature T] [--backbone mamba] [--show-timings]
+//       [--no-graph] [--d-state N] [--precision fp32]
+// --gpu-batch 0 (default) sizes the batch from free device memory like
+// auto_size_params (boa.cpp:109-156).  --warm-start is rejected (see the
+// design notes); --measure-energy is not provided.
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/boa_hip.h"
+
+static int usage() {
+  fprintf(stderr,
+          "Usage: boa <compress|decompress> <model> <input> <output> [d_model] [n_layers] "
+          "[--gpu-batch B] [--max-chunks C] [--chunk-size S] [--tile T] [--temperature T] "
+          "[--d-state N] [--precision fp32] [--show-timings]\n");
+  return 1;
+}
+
+static int auto_batch(boa_config cfg, int64_t chunk, bool compress) {
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return compress ? 64 : 1024;
+  const int64_t target = (int64_t)(free_b * 0.9);
+  int b = compress ? 64 : 1024;
+  cfg.max_lanes = b;
+  int64_t mem = boa_estimate_memory(&cfg, chunk, compress);
+  if (mem > target) {
+    while (b > 1 && mem > target) {
+      b /= 2;
+      cfg.max_lanes = b;
+      mem = boa_estimate_memory(&cfg, chunk, compress);
+    }
+  } else {
+    for (;;) {
+      cfg.max_lanes = b * 2;
+      int64_t m2 = boa_estimate_memory(&cfg, chunk, compress);
+      if (m2 < target && b * 2 <= 8192) b *= 2;
+      else break;
+    }
+  }
+  printf("Auto-sizing: Selected Batch=%d, Chunk=%lld\n", b, (long long)chunk);
+  return b;
+}
+
+int main(int argc, char** argv) {
+  if (argc < 5) return usage();
+  std::vector<std::string> args;
+  int gpu_batch = 0, max_chunks = -1, tile = 0, d_state = 16;
+  long long chunk = 4096;
+  float temperature = 1.0f;
+  bool show_timings = false;
+  for (int i = 1; i < argc; ++i) {
+    std::string s = argv[i];
+    auto next = [&](const char* name) -> const char* {
+      if (i + 1 >= argc) { fprintf(stderr, "missing value for %s\n", name); exit(1); }
+      return argv[++i];
+    };
+    if (s == "--gpu-batch") gpu_batch = atoi(next("--gpu-batch"));
+    else if (s == "--max-chunks") max_chunks = atoi(next("--max-chunks"));
+    else if (s == "--chunk-size") chunk = atoll(next("--chunk-size"));
+    else if (s == "--tile") tile = atoi(next("--tile"));
+    else if (s == "--temperature") temperature = (float)atof(next("--temperature"));
+    else if (s == "--d-state") d_state = atoi(next("--d-state"));
+    else if (s == "--precision") {
+      std::string p = next("--precision");
+      if (p != "fp32") { fprintf(stderr, "precision %s is not supported\n", p.c_str()); return 1; }
+    } else if (s == "--backbone") {
+      std::string b = next("--backbone");
+      if (b != "mamba" && b != "mambav1") {
+        fprintf(stderr, "backbone %s is not supported (mambav1 only)\n", b.c_str());
+        return 1;
+      }
+    } else if (s == "--show-timings") show_timings = true;
+    else if (s == "--no-graph" || s == "--gpu") continue;
+    else if (s == "--warm-start") {
+      fprintf(stderr, "--warm-start is not supported by this build\n");
+      return 1;
+    } else if (s.rfind("--", 0) == 0) fprintf(stderr, "Warning: Unknown flag '%s' ignored.\n", s.c_str());
+    else args.push_back(s);
+  }
+  if (args.size() < 4) return usage();
+  const std::string mode = args[0], model = args[1], in = args[2], out = args[3];
+  boa_config cfg{};
+  cfg.d_model = args.size() > 4 ? atoi(args[4].c_str()) : 256;
+  cfg.n_layers = args.size() > 5 ? atoi(args[5].c_str()) : 1;
+  cfg.d_state = d_state;
+  cfg.tile = tile;
+  cfg.precision = 0;
+  cfg.temperature = temperature;
+  if (chunk <= 0) chunk = 4096;
+  const bool compress = mode == "compress";
+  if (!compress && mode != "decompress") { fprintf(stderr, "Unknown mode: %s\n", mode.c_str()); return 1; }
+  cfg.max_lanes = gpu_batch > 0 ? gpu_batch : auto_batch(cfg, chunk, compress);
+  boa_ctx* ctx = nullptr;
+  int rc = boa_create(&cfg, &ctx);
+  if (rc) { fprintf(stderr, "boa_create failed (%d)\n", rc); return 1; }
+  rc = boa_load_weights(ctx, model.c_str());
+  if (rc) { fprintf(stderr, "load weights: %s\n", boa_last_error(ctx)); boa_destroy(ctx); return 1; }
+  auto t0 = std::chrono::steady_clock::now();
+  rc = compress ? boa_compress_file(ctx, in.c_str(), out.c_str(), chunk, max_chunks)
+                : boa_decompress_file(ctx, in.c_str(), out.c_str());
+  double sec = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  if (rc) { fprintf(stderr, "%s failed: %s\n", mode.c_str(), boa_last_error(ctx)); boa_destroy(ctx); return 1; }
+  FILE* f = fopen(compress ? in.c_str() : out.c_str(), "rb");
+  long long nbytes = 0;
+  if (f) { fseek(f, 0, SEEK_END); nbytes = ftell(f); fclose(f); }
+  printf("Done. Time: %.3fs, Avg Throughput: %.3f MB/s\n", sec, nbytes / 1e6 / (sec > 0 ? sec : 1));
+  if (show_timings) printf("Timing (s): total=%.3f (file I/O and PCIe included)\n", sec);
+  boa_destroy(ctx);
+  return 0;
+}

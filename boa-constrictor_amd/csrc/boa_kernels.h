@@ -1,0 +1,106 @@
+// Kernel-level interface of the MI355X codec path (internal to the library).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "boa_math.h"
+
+namespace boa {
+
+enum { ACT_NONE = 0, ACT_GELU = 1, ACT_RELU = 2 };
+
+struct GemmArgs {
+  const float* X; int ldx;        // activations [M][K]
+  const float* W; int ldw;        // weights [K][ldw], ldw >= round_up(N, 128), zero padded
+  float* C; int ldc;              // output [M][ldc]
+  const float* bias;              // [N] or null
+  const float* res; int ldr;      // residual [M][ldr] or null (may alias C)
+  int M, N, K, act;
+};
+hipError_t gemm_f32(const GemmArgs& a, hipStream_t s);
+
+// Encoder / decoder coder state (layout of RCState / RCDecState,
+// portability_solved_cpp/gemm_gpu.hpp:115-121, 212-217, padded to 8 bytes).
+struct RcEnc {
+  uint64_t lower, range;
+  int32_t inverted_num;
+  uint32_t first_inv_lower_word;
+  int32_t write_idx_words;
+  int32_t pad_;
+};
+struct RcDec {
+  uint64_t lower, range, point;
+  int32_t read_idx_words;
+  int32_t pad_;
+};
+
+// Token source for a tile: token(b, t) = base[b*stride + t0 + t] when that
+// position lies inside lane b's chunk, else 0 (the zero padding boa.cpp:412
+// gives the last, short chunk).
+struct TokenSrc {
+  const uint8_t* base;  // first byte of lane 0's chunk
+  int64_t stride;       // bytes between lanes' chunks
+  int64_t total;        // valid bytes counted from base
+};
+
+struct LayerW {
+  const float *ln1_w, *ln1_b, *w_in, *b_in, *conv_w, *conv_b, *w_x, *w_dt, *b_dt, *neg_exp_a, *dd,
+      *w_out, *b_out, *ln2_w, *ln2_b, *w1, *b1, *w2, *b2;
+};
+
+// Model dimensions and padded weight strides.
+struct Dims {
+  int d, L, di, r, ds, R;
+  int ld_in, ld_x, ld_out, ld_1, ld_2, ld_h1, ld_h2;
+};
+
+// LayerNorm of rows with the reference's 32-lane tree reduction order; when
+// `tok` is set, row b*T+t is first filled from the embedding table (and x is
+// written), which fuses the embedding lookup into layer 0's LN1.
+hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, float* xn,
+                      const float* w, const float* b, int rows, int d, hipStream_t s);
+// Decode-step variant: token per lane from a device byte array.
+hipError_t launch_ln1_step(const float* emb, const uint8_t* tok, float* x, float* xn, const float* w,
+                           const float* b, int rows, int d, hipStream_t s, int* t_counter);
+// LayerNorm with sequential per-row sums (LN2 order), in place allowed.
+hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b, int rows, int d,
+                      hipStream_t s);
+hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w, const float* cb,
+                             float* out, int lanes, int T, int di, hipStream_t s);
+hipError_t launch_conv_step(const float* xz, float* conv_state, const float* w, const float* cb,
+                            float* out, int lanes, int di, hipStream_t s);
+hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
+                             const float* delta, float* ssm_state, float* y, int lanes, int T,
+                             hipStream_t s);
+hipError_t launch_scan_step(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
+                            const float* delta, float* ssm_state, float* y, int lanes, hipStream_t s);
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
+
+// CDF + coder kernels.
+hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,
+                                     float inv_temp, uint2* lowprob, hipStream_t s);
+hipError_t launch_rc_enc_init(RcEnc* st, int lanes, hipStream_t s);
+hipError_t launch_rc_encode_tile(const uint2* lowprob, TokenSrc tok, int T, int t0, int lanes,
+                                 RcEnc* st, uint32_t* out, int64_t pitch_words, hipStream_t s);
+hipError_t launch_rc_finish(RcEnc* st, uint32_t* out, int64_t pitch_words, int32_t* sizes_words,
+                            int lanes, hipStream_t s);
+hipError_t launch_compact(const uint32_t* words, int64_t pitch_words, const int32_t* sizes_words,
+                          int lanes, uint64_t* offsets_words, uint32_t* payload, hipStream_t s);
+hipError_t launch_rc_dec_init(RcDec* st, const uint32_t* payload, const uint64_t* offsets_words,
+                              const int32_t* sizes_words, int lanes, hipStream_t s);
+hipError_t launch_decode_step(const float* logits, const float* head_b2, float inv_temp,
+                              uint8_t* tok, const int32_t* lens, const int* t_counter,
+                              uint8_t* out, int64_t out_stride, RcDec* st, const uint32_t* payload,
+                              const uint64_t* offsets_words, const int32_t* sizes_words, int lanes,
+                              hipStream_t s);
+// Test hooks: quantised CDFs of logits rows, and coder runs on explicit CDFs.
+hipError_t launch_cdf_rows(const float* logits, const float* bias, float inv_temp, int rows,
+                           uint32_t* qcdf, hipStream_t s);
+hipError_t launch_rc_encode_cdf(const uint32_t* cdf, const uint8_t* syms, int n_sym, int lanes,
+                                uint32_t* out, int64_t pitch_words, int32_t* sizes_words,
+                                hipStream_t s);
+hipError_t launch_rc_decode_cdf(const uint32_t* cdf, int n_sym, int lanes, const uint32_t* in,
+                                int64_t pitch_words, const int32_t* sizes_words, uint8_t* syms,
+                                hipStream_t s);
+
+}  // namespace boa

@@ -1,0 +1,490 @@
+// Deterministic integer CDFs and the 64-bit range coder (one chunk per lane).
+//
+// CDF (portability_solved_cpp/range_coder_kernels.cu:504-561, 856-932): a
+// 32-lane group per token, lane l owning symbols 8l..8l+7.  Max by the
+// shuffle-down tree; e_j = exp((l_j - max) / T) in fp32; per-lane sequential
+// double sum; total by the shuffle-down tree (lane 0's value broadcast);
+// exclusive lane prefix by the Hillis-Steele shuffle-up scan; s_cdf written
+// to LDS as a running double sum; then the lane-boundary monotonicity fix-up
+// (all reads happen before any write).  Symbol k's integer interval is
+// low_k = floor(s_cdf[k] (2^24-256)) + k, high_k = low_{k+1} (2^24 for 255).
+// On wave64 each wavefront carries two tokens, one per 32-lane half.
+//
+// Coder (range_coder_kernels.cu:46-60, 279-335, 572-627, 934-964): u64
+// lower/range state, 32-bit words, 24-bit precision, inverted-run carry
+// handling; decoder target q = min((point-lower)/(range>>24), 2^24-1).
+#include "boa_kernels.h"
+
+namespace boa {
+
+constexpr uint32_t TOTAL = 1u << 24;
+constexpr double CDF_SCALE = (double)((1u << 24) - 256u);
+
+// ----------------------------------------------------------------- coder
+__device__ __forceinline__ void enc_put(RcEnc& st, uint32_t left, uint32_t prob, uint32_t* out) {
+  if (prob == 0) prob = 1;
+  const uint64_t scale = st.range >> 24;
+  const uint64_t old_lower = st.lower;
+  st.range = scale * (uint64_t)prob;
+  st.lower = st.lower + scale * (uint64_t)left;
+  if (st.inverted_num > 0) {
+    const uint64_t sum = st.lower + st.range;
+    if (sum > st.lower) {
+      const bool carry = st.lower < old_lower;
+      const uint32_t first = carry ? st.first_inv_lower_word + 1u : st.first_inv_lower_word;
+      const uint32_t rest = carry ? 0u : 0xFFFFFFFFu;
+      out[st.write_idx_words++] = first;
+      for (int k = 1; k < st.inverted_num; ++k) out[st.write_idx_words++] = rest;
+      st.inverted_num = 0;
+    }
+  }
+  // range >= 2^32 before the update gives range >= 2^8 after it, so one
+  // shift always restores the invariant; the bound of two keeps a corrupted
+  // state from spinning.
+  for (int it = 0; it < 2 && st.range < (1ull << 32); ++it) {
+    const uint32_t lower_word = (uint32_t)(st.lower >> 32);
+    st.lower <<= 32;
+    st.range <<= 32;
+    if (st.inverted_num > 0) {
+      st.inverted_num++;
+    } else {
+      const uint64_t sum = st.lower + st.range;
+      if (sum > st.lower) {
+        out[st.write_idx_words++] = lower_word;
+      } else {
+        st.inverted_num = 1;
+        st.first_inv_lower_word = lower_word;
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ int32_t enc_finish(RcEnc& st, uint32_t* out) {
+  if (st.range == ~0ull) return 0;
+  const uint64_t point = st.lower + ((1ull << 32) - 1ull);
+  if (st.inverted_num > 0) {
+    const bool carry = point < st.lower;
+    const uint32_t first = carry ? st.first_inv_lower_word + 1u : st.first_inv_lower_word;
+    const uint32_t rest = carry ? 0u : 0xFFFFFFFFu;
+    out[st.write_idx_words++] = first;
+    for (int k = 1; k < st.inverted_num; ++k) out[st.write_idx_words++] = rest;
+    st.inverted_num = 0;
+  }
+  const uint32_t point_word = (uint32_t)(point >> 32);
+  out[st.write_idx_words++] = point_word;
+  const uint64_t upper = st.lower + st.range;
+  if ((uint32_t)(upper >> 32) == point_word) out[st.write_idx_words++] = 0u;
+  return st.write_idx_words;
+}
+
+__device__ __forceinline__ void dec_init(RcDec& st, const uint32_t* in, int32_t n_words) {
+  st.lower = 0;
+  st.range = ~0ull;
+  st.point = 0;
+  st.read_idx_words = 0;
+  st.pad_ = 0;
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t w = (st.read_idx_words < n_words) ? in[st.read_idx_words++] : 0u;
+    st.point = (st.point << 32) | (uint64_t)w;
+  }
+}
+
+__device__ __forceinline__ uint32_t dec_target(const RcDec& st) {
+  const uint64_t scale = st.range >> 24;
+  uint64_t q = (st.point - st.lower) / scale;
+  if (q >= TOTAL) q = TOTAL - 1;
+  return (uint32_t)q;
+}
+
+__device__ __forceinline__ void dec_advance(RcDec& st, uint32_t low, uint32_t high,
+                                            const uint32_t* in, int32_t n_words) {
+  const uint64_t scale = st.range >> 24;
+  uint32_t prob = high - low;
+  if (prob == 0) prob = 1;
+  st.lower = st.lower + scale * (uint64_t)low;
+  st.range = scale * (uint64_t)prob;
+  for (int it = 0; it < 2 && st.range < (1ull << 32); ++it) {
+    st.lower <<= 32;
+    st.range <<= 32;
+    const uint32_t w = (st.read_idx_words < n_words) ? in[st.read_idx_words++] : 0u;
+    st.point = (st.point << 32) | (uint64_t)w;
+  }
+}
+
+// ------------------------------------------------------------------- CDF
+// Every thread of the block must call this (it contains block barriers).
+// `s_cdf` is this half-wave's 257-entry LDS region; `lg` its logits row.
+__device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias, float inv_t,
+                                             double* s_cdf, int l) {
+  float v[8];
+  float mx = -1e30f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = 8 * l + i;
+    const float val = bias ? lg[c] + bias[c] : lg[c];
+    v[i] = val;
+    mx = fmaxf(mx, val);
+  }
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_down(mx, off, 32));
+  mx = __shfl(mx, 0, 32);
+  double sd = 0.0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float e = expf_((v[i] - mx) * inv_t);
+    v[i] = e;
+    sd += (double)e;
+  }
+  double tot = sd;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) tot = tot + __shfl_down(tot, off, 32);
+  tot = __shfl(tot, 0, 32);
+  const double inv = 1.0 / tot;
+  const double ts = sd * inv;
+  double pre = ts;
+#pragma unroll
+  for (int off = 1; off <= 16; off <<= 1) {
+    const double tmp = __shfl_up(pre, off, 32);
+    if (l >= off) pre = pre + tmp;
+  }
+  double run = pre - ts;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    s_cdf[8 * l + i] = run;
+    run += (double)v[i] * inv;
+  }
+  if (l == 31) s_cdf[256] = 1.0;
+  __syncthreads();
+  bool fix = false;
+  double delta = 0.0;
+  if (l > 0) {
+    const double prev_end = s_cdf[8 * l - 1];
+    const double my_start = s_cdf[8 * l];
+    if (my_start < prev_end) {
+      fix = true;
+      delta = prev_end - my_start;
+    }
+  }
+  __syncthreads();
+  if (fix) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s_cdf[8 * l + i] += delta;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t q_low(const double* s_cdf, int k) {
+  return (uint32_t)(s_cdf[k] * CDF_SCALE) + (uint32_t)k;
+}
+__device__ __forceinline__ uint32_t q_high(const double* s_cdf, int k) {
+  return k == 255 ? TOTAL : (uint32_t)(s_cdf[k + 1] * CDF_SCALE) + (uint32_t)(k + 1);
+}
+
+__device__ __forceinline__ uint32_t token_at(const TokenSrc& tok, int lane, int64_t pos_in_chunk) {
+  const int64_t pos = (int64_t)lane * tok.stride + pos_in_chunk;
+  return (pos_in_chunk < tok.stride && pos < tok.total) ? tok.base[pos] : 0u;
+}
+
+// (low, prob) of the next byte for every row (lane b, position t0+t) of a
+// tile.  8 rows per 256-thread block.
+__global__ __launch_bounds__(256) void cdf_targets_kernel(const float* __restrict__ logits,
+                                                          TokenSrc tok, int T, int t0, int rows,
+                                                          float inv_t, uint2* lowprob) {
+  __shared__ double s_cdf[8][260];
+  const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int row = blockIdx.x * 8 + half;
+  const int rr = row < rows ? row : rows - 1;
+  cdf_halfwave(logits + (size_t)rr * 256, nullptr, inv_t, s_cdf[half], l);
+  if (row < rows && l == 0) {
+    const int b = row / T, t = row % T;
+    const int sym = (int)token_at(tok, b, (int64_t)t0 + t + 1);
+    const uint32_t lo = q_low(s_cdf[half], sym), hi = q_high(s_cdf[half], sym);
+    lowprob[row] = make_uint2(lo, hi - lo);
+  }
+}
+
+hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,
+                                     float inv_temp, uint2* lowprob, hipStream_t s) {
+  const int rows = lanes * T;
+  hipLaunchKernelGGL(cdf_targets_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, tok, T, t0,
+                     rows, inv_temp, lowprob);
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void cdf_rows_kernel(const float* __restrict__ logits,
+                                                       const float* __restrict__ bias, float inv_t,
+                                                       int rows, uint32_t* qcdf) {
+  __shared__ double s_cdf[8][260];
+  const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int row = blockIdx.x * 8 + half;
+  const int rr = row < rows ? row : rows - 1;
+  cdf_halfwave(logits + (size_t)rr * 256, bias, inv_t, s_cdf[half], l);
+  if (row < rows) {
+    uint32_t* q = qcdf + (size_t)row * 257;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[8 * l + i] = q_low(s_cdf[half], 8 * l + i);
+    if (l == 0) q[256] = TOTAL;
+  }
+}
+
+hipError_t launch_cdf_rows(const float* logits, const float* bias, float inv_temp, int rows,
+                           uint32_t* qcdf, hipStream_t s) {
+  hipLaunchKernelGGL(cdf_rows_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, bias, inv_temp,
+                     rows, qcdf);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- encode
+__global__ void rc_enc_init_kernel(RcEnc* st, int lanes) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  RcEnc e;
+  e.lower = 0; e.range = ~0ull; e.inverted_num = 0; e.first_inv_lower_word = 0;
+  e.write_idx_words = 0; e.pad_ = 0;
+  st[b] = e;
+}
+
+hipError_t launch_rc_enc_init(RcEnc* st, int lanes, hipStream_t s) {
+  hipLaunchKernelGGL(rc_enc_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, lanes);
+  return hipGetLastError();
+}
+
+// One thread per lane codes positions t in [t0, min(t0+T, len_b - 1)): the
+// prediction made at t for byte t+1 (range_coder_kernels.cu:854-858 with
+// boa.cpp:463-468's per-tile bound).
+__global__ void rc_encode_tile_kernel(const uint2* __restrict__ lowprob, TokenSrc tok, int T,
+                                      int t0, int lanes, RcEnc* states, uint32_t* out,
+                                      int64_t pitch_words) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  int64_t len = tok.total - (int64_t)b * tok.stride;
+  len = len < 0 ? 0 : (len > tok.stride ? tok.stride : len);
+  int64_t end = len - 1;
+  if (end > (int64_t)t0 + T) end = (int64_t)t0 + T;
+  if (end <= t0) return;
+  RcEnc st = states[b];
+  uint32_t* o = out + (size_t)b * pitch_words;
+  const uint2* lp = lowprob + (size_t)b * T;
+  for (int64_t t = t0; t < end; ++t) {
+    const uint2 v = lp[t - t0];
+    enc_put(st, v.x, v.y, o);
+  }
+  states[b] = st;
+}
+
+hipError_t launch_rc_encode_tile(const uint2* lowprob, TokenSrc tok, int T, int t0, int lanes,
+                                 RcEnc* st, uint32_t* out, int64_t pitch_words, hipStream_t s) {
+  hipLaunchKernelGGL(rc_encode_tile_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, lowprob, tok, T,
+                     t0, lanes, st, out, pitch_words);
+  return hipGetLastError();
+}
+
+__global__ void rc_finish_kernel(RcEnc* states, uint32_t* out, int64_t pitch_words,
+                                 int32_t* sizes_words, int lanes) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  RcEnc st = states[b];
+  sizes_words[b] = enc_finish(st, out + (size_t)b * pitch_words);
+  states[b] = st;
+}
+
+hipError_t launch_rc_finish(RcEnc* st, uint32_t* out, int64_t pitch_words, int32_t* sizes_words,
+                            int lanes, hipStream_t s) {
+  hipLaunchKernelGGL(rc_finish_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, out,
+                     pitch_words, sizes_words, lanes);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------ compaction
+// Exclusive prefix sum of the per-lane word counts (one 1024-thread block:
+// wavefront inclusive scans, then a scan of the 16 wave totals, carried
+// across 1024-lane slices), followed by a copy of every lane's words to its
+// offset in the contiguous payload.
+__global__ __launch_bounds__(1024) void scan_sizes_kernel(const int32_t* sizes, int lanes,
+                                                          uint64_t* offsets) {
+  __shared__ uint64_t wave_tot[16];
+  __shared__ uint64_t carry;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < lanes; base += 1024) {
+    const int i = base + tid;
+    const uint64_t v = i < lanes ? (uint64_t)sizes[i] : 0ull;
+    uint64_t inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint64_t t = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += t;
+    }
+    if (lane == 63) wave_tot[wave] = inc;
+    __syncthreads();
+    uint64_t wbase = 0;
+    for (int w = 0; w < wave; ++w) wbase += wave_tot[w];
+    const uint64_t c = carry;
+    if (i < lanes) offsets[i] = c + wbase + inc - v;
+    __syncthreads();
+    if (tid == 1023) carry = c + wbase + inc;
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void compact_kernel(const uint32_t* __restrict__ words,
+                                                      int64_t pitch_words,
+                                                      const int32_t* __restrict__ sizes,
+                                                      const uint64_t* __restrict__ offsets,
+                                                      uint32_t* payload) {
+  const int b = blockIdx.y;
+  const int n = sizes[b];
+  const uint32_t* src = words + (size_t)b * pitch_words;
+  uint32_t* dst = payload + offsets[b];
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+hipError_t launch_compact(const uint32_t* words, int64_t pitch_words, const int32_t* sizes_words,
+                          int lanes, uint64_t* offsets_words, uint32_t* payload, hipStream_t s) {
+  if (lanes <= 0) return hipSuccess;
+  hipLaunchKernelGGL(scan_sizes_kernel, dim3(1), dim3(1024), 0, s, sizes_words, lanes,
+                     offsets_words);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(compact_kernel, dim3(16, lanes), dim3(256), 0, s, words, pitch_words,
+                     sizes_words, offsets_words, payload);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- decode
+__global__ void rc_dec_init_kernel(RcDec* st, const uint32_t* payload,
+                                   const uint64_t* offsets_words, const int32_t* sizes_words,
+                                   int lanes) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  RcDec d;
+  dec_init(d, payload + offsets_words[b], sizes_words[b]);
+  st[b] = d;
+}
+
+hipError_t launch_rc_dec_init(RcDec* st, const uint32_t* payload, const uint64_t* offsets_words,
+                              const int32_t* sizes_words, int lanes, hipStream_t s) {
+  hipLaunchKernelGGL(rc_dec_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, payload,
+                     offsets_words, sizes_words, lanes);
+  return hipGetLastError();
+}
+
+// One 32-lane half-wave per lane: head bias, CDF, the first symbol whose
+// interval holds the coder target (8 rounds of 32 candidates, ballot +
+// first-set-bit as range_coder_kernels.cu:594-610), then the state update.
+__global__ __launch_bounds__(256) void decode_step_kernel(
+    const float* __restrict__ logits, const float* __restrict__ head_b2, float inv_t, uint8_t* tok,
+    const int32_t* __restrict__ lens, const int* __restrict__ t_counter, uint8_t* out,
+    int64_t out_stride, RcDec* states, const uint32_t* __restrict__ payload,
+    const uint64_t* __restrict__ offsets_words, const int32_t* __restrict__ sizes_words,
+    int lanes) {
+  __shared__ double s_cdf[8][260];
+  __shared__ uint32_t s_target[8];
+  const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int b = blockIdx.x * 8 + half;
+  const int bb = b < lanes ? b : lanes - 1;
+  const int t = *t_counter;
+  const bool active = b < lanes && t < lens[bb];
+  cdf_halfwave(logits + (size_t)bb * 256, head_b2, inv_t, s_cdf[half], l);
+  RcDec st;
+  if (active && l == 0) {
+    st = states[b];
+    s_target[half] = dec_target(st);
+  }
+  __syncthreads();
+  if (!active) return;  // no barrier follows
+  const uint32_t target = s_target[half];
+  const double* sc = s_cdf[half];
+  int sym = 0;
+  uint32_t low_s = 0, high_s = 0;
+  const int shift = (threadIdx.x & 32);
+  for (int round = 0; round < 8; ++round) {
+    const int k = round * 32 + l;
+    const uint32_t lo = q_low(sc, k), hi = q_high(sc, k);
+    const bool match = target >= lo && target < hi;
+    const uint32_t mask = (uint32_t)(__ballot(match) >> shift);
+    if (mask != 0u) {
+      const int winner = __ffs(mask) - 1;
+      sym = __shfl(k, winner, 32);
+      low_s = __shfl(lo, winner, 32);
+      high_s = __shfl(hi, winner, 32);
+      break;
+    }
+  }
+  if (l == 0) {
+    const uint32_t* in = payload + offsets_words[b];
+    dec_advance(st, low_s, high_s, in, sizes_words[b]);
+    states[b] = st;
+    out[(size_t)b * out_stride + t] = (uint8_t)sym;
+    tok[b] = (uint8_t)sym;
+  }
+}
+
+hipError_t launch_decode_step(const float* logits, const float* head_b2, float inv_temp,
+                              uint8_t* tok, const int32_t* lens, const int* t_counter,
+                              uint8_t* out, int64_t out_stride, RcDec* st, const uint32_t* payload,
+                              const uint64_t* offsets_words, const int32_t* sizes_words, int lanes,
+                              hipStream_t s) {
+  hipLaunchKernelGGL(decode_step_kernel, dim3((lanes + 7) / 8), dim3(256), 0, s, logits, head_b2,
+                     inv_temp, tok, lens, t_counter, out, out_stride, st, payload, offsets_words,
+                     sizes_words, lanes);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------- explicit-CDF test hooks
+__global__ void rc_encode_cdf_kernel(const uint32_t* __restrict__ cdf, const uint8_t* syms,
+                                     int n_sym, int lanes, uint32_t* out, int64_t pitch_words,
+                                     int32_t* sizes_words) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  RcEnc st;
+  st.lower = 0; st.range = ~0ull; st.inverted_num = 0; st.first_inv_lower_word = 0;
+  st.write_idx_words = 0; st.pad_ = 0;
+  uint32_t* o = out + (size_t)b * pitch_words;
+  for (int i = 0; i < n_sym; ++i) {
+    const uint32_t* c = cdf + ((size_t)b * n_sym + i) * 257;
+    const uint32_t s = syms[(size_t)b * n_sym + i];
+    enc_put(st, c[s], c[s + 1] - c[s], o);
+  }
+  sizes_words[b] = enc_finish(st, o);
+}
+
+hipError_t launch_rc_encode_cdf(const uint32_t* cdf, const uint8_t* syms, int n_sym, int lanes,
+                                uint32_t* out, int64_t pitch_words, int32_t* sizes_words,
+                                hipStream_t s) {
+  hipLaunchKernelGGL(rc_encode_cdf_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, cdf, syms, n_sym,
+                     lanes, out, pitch_words, sizes_words);
+  return hipGetLastError();
+}
+
+__global__ void rc_decode_cdf_kernel(const uint32_t* __restrict__ cdf, int n_sym, int lanes,
+                                     const uint32_t* in, int64_t pitch_words,
+                                     const int32_t* sizes_words, uint8_t* syms) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= lanes) return;
+  RcDec st;
+  const uint32_t* src = in + (size_t)b * pitch_words;
+  dec_init(st, src, sizes_words[b]);
+  for (int i = 0; i < n_sym; ++i) {
+    const uint32_t* c = cdf + ((size_t)b * n_sym + i) * 257;
+    const uint32_t q = dec_target(st);
+    int s = 0;
+    uint32_t lo = 0, hi = 0;
+    for (int k = 0; k < 256; ++k)
+      if (q >= c[k] && q < c[k + 1]) { s = k; lo = c[k]; hi = c[k + 1]; break; }
+    syms[(size_t)b * n_sym + i] = (uint8_t)s;
+    dec_advance(st, lo, hi, src, sizes_words[b]);
+  }
+}
+
+hipError_t launch_rc_decode_cdf(const uint32_t* cdf, int n_sym, int lanes, const uint32_t* in,
+                                int64_t pitch_words, const int32_t* sizes_words, uint8_t* syms,
+                                hipStream_t s) {
+  hipLaunchKernelGGL(rc_decode_cdf_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, cdf, n_sym,
+                     lanes, in, pitch_words, sizes_words, syms);
+  return hipGetLastError();
+}
+
+}  // namespace boa

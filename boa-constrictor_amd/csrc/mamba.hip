@@ -1,0 +1,374 @@
+// Mamba-v1 block kernels: LayerNorms, causal depthwise conv1d + SiLU, and the
+// fused dt_proj + softplus + selective scan + D + SiLU(z) gate, each in a
+// chunk (teacher-forced tile, sequential in t) and a step (one token per
+// lane) form that share one per-element operation sequence.
+//
+// Reference semantics followed (portability_solved_cpp/):
+//   LN1  inference_kernels.cu:293-348  32-lane shuffle-down tree sums
+//   LN2  inference_kernels.cu:229-277  sequential per-row sums
+//   conv mamba_kernels.cu:158-197 (step), 370-412 (chunk)
+//   scan mamba_kernels.cu:271-352 (step), 414-470 (chunk), with the dt_proj
+//        GEMM (K = dt_rank fma chain) + softplus of boa_gpu.hpp:317-318 and
+//        the gate of mamba_kernels.cu:130-144
+// rsqrtf is replaced by 1/sqrt with IEEE-rounded division and square root.
+#include "boa_kernels.h"
+
+namespace boa {
+
+constexpr int LN_MAXE = 16;  // d_model <= 512
+
+// -------------------------------------------------------------- LayerNorm
+// One 32-lane half-wave per row: lane l accumulates elements l, l+32, ...
+// in order, then lanes combine by the shuffle-down tree 16, 8, 4, 2, 1 and
+// lane 0's totals are broadcast (the reference's warp-per-row order).
+__device__ __forceinline__ void ln_halfwave_row(const float* src, float* x_copy, float* dst,
+                                                const float* __restrict__ w,
+                                                const float* __restrict__ b, int d, int l) {
+  float v[LN_MAXE];
+  float s = 0.0f, q = 0.0f;
+#pragma unroll
+  for (int e = 0; e < LN_MAXE; ++e) {
+    int idx = l + 32 * e;
+    if (idx < d) {
+      float val = src[idx];
+      v[e] = val;
+      s = s + val;
+      q = q + val * val;
+      if (x_copy) x_copy[idx] = val;
+    }
+  }
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) {
+    s = s + __shfl_down(s, off, 32);
+    q = q + __shfl_down(q, off, 32);
+  }
+  s = __shfl(s, 0, 32);
+  q = __shfl(q, 0, 32);
+  float mean = s / (float)d;
+  float var = q / (float)d - mean * mean;
+  float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
+#pragma unroll
+  for (int e = 0; e < LN_MAXE; ++e) {
+    int idx = l + 32 * e;
+    if (idx < d) dst[idx] = ((v[e] - mean) * inv_std) * w[idx] + b[idx];
+  }
+}
+
+__global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb, TokenSrc tok,
+                                                  int use_tok, int T, int t0, float* x, float* xn,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ b, int rows, int d) {
+  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int l = threadIdx.x & 31;
+  if (row >= rows) return;  // whole half-waves exit together
+  const float* src;
+  float* xc = nullptr;
+  if (use_tok) {
+    const int lane = row / T, t = row % T;
+    const int64_t pos = (int64_t)lane * tok.stride + t0 + t;
+    const uint32_t token = (t0 + t < tok.stride && pos < tok.total) ? tok.base[pos] : 0u;
+    src = emb + (size_t)token * d;
+    xc = x + (size_t)row * d;
+  } else {
+    src = x + (size_t)row * d;
+  }
+  ln_halfwave_row(src, xc, xn + (size_t)row * d, w, b, d, l);
+}
+
+__global__ __launch_bounds__(256) void ln1_step_kernel(const float* __restrict__ emb,
+                                                       const uint8_t* tok, float* x, float* xn,
+                                                       const float* __restrict__ w,
+                                                       const float* __restrict__ b, int rows,
+                                                       int d, int* t_counter) {
+  if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
+  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int l = threadIdx.x & 31;
+  if (row >= rows) return;
+  const float* src = emb + (size_t)tok[row] * d;
+  ln_halfwave_row(src, x + (size_t)row * d, xn + (size_t)row * d, w, b, d, l);
+}
+
+hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, float* xn,
+                      const float* w, const float* b, int rows, int d, hipStream_t s) {
+  if (d > 32 * LN_MAXE) return hipErrorInvalidValue;
+  int blocks = (rows + 7) / 8;
+  hipLaunchKernelGGL(ln1_kernel, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T, t0, x, xn,
+                     w, b, rows, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_ln1_step(const float* emb, const uint8_t* tok, float* x, float* xn, const float* w,
+                           const float* b, int rows, int d, hipStream_t s, int* t_counter) {
+  if (d > 32 * LN_MAXE) return hipErrorInvalidValue;
+  int blocks = (rows + 7) / 8;
+  hipLaunchKernelGGL(ln1_step_kernel, dim3(blocks), dim3(256), 0, s, emb, tok, x, xn, w, b, rows, d,
+                     t_counter);
+  return hipGetLastError();
+}
+
+// One thread per row, sums in element order (the reference's LN2 order).
+__global__ __launch_bounds__(256) void ln2_kernel(const float* x, float* out,
+                                                  const float* __restrict__ w,
+                                                  const float* __restrict__ b, int rows, int d) {
+  const int row = blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const float* xr = x + (size_t)row * d;
+  float s = 0.0f, q = 0.0f;
+  for (int i = 0; i < d; i += 4) {
+    float4 v = *reinterpret_cast<const float4*>(xr + i);
+    s = s + v.x; q = q + v.x * v.x;
+    s = s + v.y; q = q + v.y * v.y;
+    s = s + v.z; q = q + v.z * v.z;
+    s = s + v.w; q = q + v.w * v.w;
+  }
+  float mean = s / (float)d;
+  float var = q / (float)d - mean * mean;
+  float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
+  float* o = out + (size_t)row * d;
+  for (int i = 0; i < d; i += 4) {
+    float4 v = *reinterpret_cast<const float4*>(xr + i);
+    float4 wv = *reinterpret_cast<const float4*>(w + i);
+    float4 bv = *reinterpret_cast<const float4*>(b + i);
+    v.x = ((v.x - mean) * inv_std) * wv.x + bv.x;
+    v.y = ((v.y - mean) * inv_std) * wv.y + bv.y;
+    v.z = ((v.z - mean) * inv_std) * wv.z + bv.z;
+    v.w = ((v.w - mean) * inv_std) * wv.w + bv.w;
+    *reinterpret_cast<float4*>(o + i) = v;
+  }
+}
+
+hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b, int rows, int d,
+                      hipStream_t s) {
+  if (d % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ln2_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, x, out, w, b, rows, d);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ conv1d
+// value = bias + x[t-3] w0 + x[t-2] w1 + x[t-1] w2 + x[t] w3 (unfused, k
+// order), then SiLU.  The state holds the last four inputs, most recent last.
+__device__ __forceinline__ float conv_value(float bias, float xm3, float xm2, float xm1, float x0,
+                                            const float4 w) {
+  float v = bias;
+  v = v + xm3 * w.x;
+  v = v + xm2 * w.y;
+  v = v + xm1 * w.z;
+  v = v + x0 * w.w;
+  return silu(v);
+}
+
+__global__ __launch_bounds__(256) void conv_chunk_kernel(const float* __restrict__ xz,
+                                                         float* conv_state,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ cb, float* out,
+                                                         int lanes, int T, int di) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= lanes * di) return;
+  const int c = idx % di, b = idx / di;
+  float4* st = reinterpret_cast<float4*>(conv_state) + idx;
+  float4 s0 = *st;
+  const float4 wv = reinterpret_cast<const float4*>(w)[c];
+  const float bias = cb[c];
+  float xm4 = s0.x, xm3 = s0.y, xm2 = s0.z, xm1 = s0.w;
+  const float* xp = xz + (size_t)b * T * (2 * di) + c;
+  float* op = out + (size_t)b * T * di + c;
+  for (int t = 0; t < T; ++t) {
+    float x0 = xp[(size_t)t * 2 * di];
+    op[(size_t)t * di] = conv_value(bias, xm3, xm2, xm1, x0, wv);
+    xm4 = xm3; xm3 = xm2; xm2 = xm1; xm1 = x0;
+  }
+  *st = make_float4(xm4, xm3, xm2, xm1);
+}
+
+__global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict__ xz,
+                                                        float* conv_state,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ cb, float* out,
+                                                        int lanes, int di) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= lanes * di) return;
+  const int c = idx % di, b = idx / di;
+  float4* st = reinterpret_cast<float4*>(conv_state) + idx;
+  float4 s0 = *st;
+  const float x0 = xz[(size_t)b * 2 * di + c];
+  const float4 wv = reinterpret_cast<const float4*>(w)[c];
+  out[idx] = conv_value(cb[c], s0.y, s0.z, s0.w, x0, wv);
+  *st = make_float4(s0.y, s0.z, s0.w, x0);
+}
+
+hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w, const float* cb,
+                             float* out, int lanes, int T, int di, hipStream_t s) {
+  int n = lanes * di;
+  hipLaunchKernelGGL(conv_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xz, conv_state, w,
+                     cb, out, lanes, T, di);
+  return hipGetLastError();
+}
+
+hipError_t launch_conv_step(const float* xz, float* conv_state, const float* w, const float* cb,
+                            float* out, int lanes, int di, hipStream_t s) {
+  int n = lanes * di;
+  hipLaunchKernelGGL(conv_step_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xz, conv_state, w,
+                     cb, out, lanes, di);
+  return hipGetLastError();
+}
+
+// -------------------------------------------------------- selective scan
+constexpr int RMAX = 32;  // dt_rank <= 32 (d_model <= 512)
+
+template <int DS>
+struct ScanCtx {
+  float wdt[RMAX];
+  float na[DS];
+  float h[DS];
+  float bdt, dd;
+};
+
+template <int DS>
+__device__ __forceinline__ void scan_load(ScanCtx<DS>& sc, const LayerW& Lw, const float* ssm,
+                                          int c, int di, int r) {
+#pragma unroll
+  for (int j = 0; j < RMAX; ++j) sc.wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
+#pragma unroll
+  for (int n = 0; n < DS; n += 4) {
+    float4 a = *reinterpret_cast<const float4*>(Lw.neg_exp_a + (size_t)c * DS + n);
+    sc.na[n] = a.x; sc.na[n + 1] = a.y; sc.na[n + 2] = a.z; sc.na[n + 3] = a.w;
+    float4 hv = *reinterpret_cast<const float4*>(ssm + n);
+    sc.h[n] = hv.x; sc.h[n + 1] = hv.y; sc.h[n + 2] = hv.z; sc.h[n + 3] = hv.w;
+  }
+  sc.bdt = Lw.b_dt[c];
+  sc.dd = Lw.dd[c];
+}
+
+template <int DS>
+__device__ __forceinline__ void scan_store(const ScanCtx<DS>& sc, float* ssm) {
+#pragma unroll
+  for (int n = 0; n < DS; n += 4)
+    *reinterpret_cast<float4*>(ssm + n) = make_float4(sc.h[n], sc.h[n + 1], sc.h[n + 2], sc.h[n + 3]);
+}
+
+// One token of one channel: dt = softplus(delta[0:r] . w_dt[:, c] + b_dt),
+// h_n = exp(-exp(A_log) dt) h_n + (dt B_n) u, y = sum_n h_n C_n + D u,
+// out = y * (z * sigmoid(z)).
+template <int DS>
+__device__ __forceinline__ float scan_token(ScanCtx<DS>& sc, const float* __restrict__ drow, int r,
+                                            float u, float z) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < RMAX; ++j)
+    if (j < r) acc = __builtin_fmaf(drow[j], sc.wdt[j], acc);
+  const float dt = softplus(acc + sc.bdt);
+  const float* Bv = drow + r;
+  const float* Cv = drow + r + DS;
+  float y = 0.0f;
+#pragma unroll
+  for (int n = 0; n < DS; ++n) {
+    float dA = expf_(sc.na[n] * dt);
+    float dB = dt * Bv[n];
+    sc.h[n] = dA * sc.h[n] + dB * u;
+    y = y + sc.h[n] * Cv[n];
+  }
+  y = y + sc.dd * u;
+  float sg = 1.0f / (1.0f + expf_(-z));
+  return y * (z * sg);
+}
+
+// Thread per (lane, channel); a block never straddles two lanes, so the
+// delta-row reads are uniform across it.
+template <int DS>
+__global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
+                                                         const float* __restrict__ xz,
+                                                         const float* __restrict__ conv,
+                                                         const float* __restrict__ delta,
+                                                         float* ssm_state, float* y, int lanes,
+                                                         int T) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int di = D.di;
+  if (idx >= lanes * di) return;
+  const int c = idx % di, b = idx / di;
+  float* ssm = ssm_state + (size_t)idx * DS;
+  ScanCtx<DS> sc;
+  scan_load<DS>(sc, Lw, ssm, c, di, D.r);
+  for (int t = 0; t < T; ++t) {
+    const size_t row = (size_t)b * T + t;
+    const float u = conv[row * di + c];
+    const float z = xz[row * 2 * di + di + c];
+    y[row * di + c] = scan_token<DS>(sc, delta + row * D.R, D.r, u, z);
+  }
+  scan_store<DS>(sc, ssm);
+}
+
+template <int DS>
+__global__ __launch_bounds__(256) void scan_step_kernel(Dims D, LayerW Lw,
+                                                        const float* __restrict__ xz,
+                                                        const float* __restrict__ conv,
+                                                        const float* __restrict__ delta,
+                                                        float* ssm_state, float* y, int lanes) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int di = D.di;
+  if (idx >= lanes * di) return;
+  const int c = idx % di, b = idx / di;
+  float* ssm = ssm_state + (size_t)idx * DS;
+  ScanCtx<DS> sc;
+  scan_load<DS>(sc, Lw, ssm, c, di, D.r);
+  y[idx] = scan_token<DS>(sc, delta + (size_t)b * D.R, D.r, conv[idx], xz[(size_t)b * 2 * di + di + c]);
+  scan_store<DS>(sc, ssm);
+}
+
+static int block_for(int di) {
+  for (int bs = 256; bs >= 32; bs >>= 1)
+    if (di % bs == 0) return bs;
+  return 0;
+}
+
+hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
+                             const float* delta, float* ssm_state, float* y, int lanes, int T,
+                             hipStream_t s) {
+  int bs = block_for(D.di);
+  if (!bs || D.r > RMAX) return hipErrorInvalidValue;
+  dim3 grid((lanes * D.di) / bs);
+  if (D.ds == 16)
+    hipLaunchKernelGGL(scan_chunk_kernel<16>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
+                       ssm_state, y, lanes, T);
+  else if (D.ds == 32)
+    hipLaunchKernelGGL(scan_chunk_kernel<32>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
+                       ssm_state, y, lanes, T);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_scan_step(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
+                            const float* delta, float* ssm_state, float* y, int lanes,
+                            hipStream_t s) {
+  int bs = block_for(D.di);
+  if (!bs || D.r > RMAX) return hipErrorInvalidValue;
+  dim3 grid((lanes * D.di) / bs);
+  if (D.ds == 16)
+    hipLaunchKernelGGL(scan_step_kernel<16>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
+                       ssm_state, y, lanes);
+  else if (D.ds == 32)
+    hipLaunchKernelGGL(scan_step_kernel<32>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
+                       ssm_state, y, lanes);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ misc
+__global__ void fill_zero_kernel(uint32_t* p, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = 0u;
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
+  if (bytes % 4) return hipErrorInvalidValue;
+  size_t n = bytes / 4;
+  if (!n) return hipSuccess;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (uint32_t*)p, n);
+  return hipGetLastError();
+}
+
+}  // namespace boa

@@ -1,0 +1,168 @@
+/*
+ * refcpu -- CPU restatement of BoaConstrictor's chunk-parallel codec path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity oracle and the timed
+ * CPU baseline.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only as the checker.  The product path
+ * (boa-constrictor_amd/) never links, loads or calls anything in oracle/.
+ *
+ * What it restates (reference paths relative to the reference checkout):
+ *   model     portability_solved_cpp/boa_gpu.hpp:227-330, 739-764, 834-843,
+ *             892-902, 1034-1053, 1081-1102 (mambav1 block, head)
+ *   GEMM      portability_solved_cpp/gemm_kernels.cu:283-313 (K-order FMA
+ *             chain from 0, then +bias -> activation -> +residual)
+ *   kernels   portability_solved_cpp/mamba_kernels.cu:130-197, 271-361,
+ *             370-470; inference_kernels.cu:229-348, 372-390
+ *   CDF       portability_solved_cpp/range_coder_kernels.cu:504-561, 856-932
+ *             with the 32-lane double reduction/scan of
+ *             gemm_gpu_common.cuh:87-123
+ *   coder     range_coder_kernels.cu:46-60, 279-335, 572-627, 934-964
+ *   container portability_solved_cpp/boa.cpp:85-107, 158-277, 538-581
+ *   weights   portability_solved_cpp/boa_gpu.hpp:16-43, 87-100, 212-225,
+ *             716-721, 817-832, 990-1029; convert_boa_weights.py:153-241
+ *
+ * Deliberate, documented deviations from the reference's CUDA build:
+ *   - CUDA expf/logf/__expf/rsqrtf (vendor math) are replaced by this
+ *     library's own exp/log (Cody-Waite + Taylor, atanh series) and by
+ *     1/sqrt with IEEE division and square root.
+ *   - The chunk-mode conv state update keeps the last d_conv inputs of the
+ *     concatenation (old state, tile) also for tiles shorter than d_conv.
+ *
+ * Parity pinning of every function here is listed in DESIGN.md; functions
+ * without an independent check say "parity unpinned" there.
+ */
+#ifndef BOA_REFCPU_H
+#define BOA_REFCPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- math */
+float ref_expf(float x);
+float ref_logf(float x);
+float ref_repro_exp(float x);     /* activations.hpp:33-84 (device branch) */
+float ref_repro_tanh(float x);    /* activations.hpp:87-98 */
+float ref_gelu(float x);          /* activations.hpp:105-117 */
+float ref_silu(float x);          /* mamba_kernels.cu:188-189 */
+float ref_softplus(float x);      /* inference_kernels.cu:376-382 */
+float ref_half_to_float(uint16_t h); /* boa_gpu.hpp:16-43 */
+
+/* --------------------------------------------------------------- coder */
+typedef struct {
+    uint64_t lower;
+    uint64_t range;
+    int32_t inverted_num;
+    uint32_t first_inv_lower_word;
+    int32_t write_idx_words;
+    int32_t pad_;
+} ref_rc_enc;                     /* RCState, gemm_gpu.hpp:115-121 */
+
+typedef struct {
+    uint64_t lower;
+    uint64_t range;
+    uint64_t point;
+    int32_t read_idx_words;
+    int32_t pad_;
+} ref_rc_dec;                     /* RCDecState, gemm_gpu.hpp:212-217 */
+
+void ref_rc_enc_init(ref_rc_enc* st);
+/* Encode one symbol with integer interval [left, left+prob) of 2^24.
+ * prob==0 is promoted to 1 (range_coder_kernels.cu:930-932). */
+void ref_rc_enc_put(ref_rc_enc* st, uint32_t left, uint32_t prob, uint32_t* out);
+/* Flush; returns the total number of words written (0 for an empty stream). */
+int32_t ref_rc_enc_finish(ref_rc_enc* st, uint32_t* out);
+void ref_rc_dec_init(ref_rc_dec* st, const uint32_t* in, int32_t n_words);
+uint32_t ref_rc_dec_target(const ref_rc_dec* st);
+void ref_rc_dec_advance(ref_rc_dec* st, uint32_t low, uint32_t high,
+                        const uint32_t* in, int32_t n_words);
+/* Whole-stream helpers over explicit integer CDFs: cdf is [n_sym][257]. */
+int32_t ref_rc_encode_cdf_stream(const uint32_t* cdf, const uint8_t* syms, int32_t n_sym,
+                                 uint32_t* out);
+void ref_rc_decode_cdf_stream(const uint32_t* cdf, int32_t n_sym, const uint32_t* in,
+                              int32_t n_words, uint8_t* syms_out);
+
+/* ----------------------------------------------------------------- CDF */
+/* s_cdf[257] from 256 fp32 logits (+ optional bias added first, as the
+ * decoder does), with the reference's 32-lane double reduction order and
+ * the lane-boundary monotonicity fix-up. */
+void ref_cdf_build(const float* logits, const float* bias, float inv_temperature,
+                   double* s_cdf);
+/* integer interval of symbol k: low = floor(s_cdf[k]*(2^24-256)) + k ... */
+void ref_cdf_interval(const double* s_cdf, int32_t k, uint32_t* low, uint32_t* high);
+/* all 257 integer boundaries low_0..low_255, 2^24 */
+void ref_cdf_quantize(const double* s_cdf, uint32_t* qcdf);
+/* first k with low_k <= target < high_k (0,0,0 if none) */
+int32_t ref_cdf_search(const double* s_cdf, uint32_t target, uint32_t* low, uint32_t* high);
+
+/* --------------------------------------------------------------- model */
+typedef struct ref_model ref_model;
+typedef struct ref_state ref_state;
+
+/* Loads a convert_boa_weights.py file (BOA\0 fp32, BOA\1 fp16 or headerless
+ * fp32).  Returns NULL and fills err on failure (size mismatch included). */
+ref_model* ref_model_load(const char* path, int32_t d_model, int32_t n_layers,
+                          int32_t d_state, char* err, int32_t err_len);
+void ref_model_free(ref_model* m);
+int64_t ref_model_expected_bytes(int32_t d_model, int32_t n_layers, int32_t d_state,
+                                 int32_t fp16);
+
+ref_state* ref_state_new(const ref_model* m, int32_t lanes);
+void ref_state_reset(ref_state* s);
+void ref_state_free(ref_state* s);
+
+/* Teacher-forced forward of T tokens per lane; tokens [lanes][T], logits
+ * [lanes][T][256] (head bias included).  State carries across calls. */
+void ref_forward_chunk(const ref_model* m, ref_state* s, const uint8_t* tokens,
+                       int32_t lanes, int32_t T, float* logits, int32_t n_threads);
+/* One step for every lane; logits [lanes][256]; add_bias=0 mirrors the
+ * decoder's head call (boa.cpp:728,743). */
+void ref_step(const ref_model* m, ref_state* s, const uint8_t* tokens, int32_t lanes,
+              float* logits, int32_t add_bias, int32_t n_threads);
+
+/* ------------------------------------------------------- end to end */
+typedef struct {
+    int64_t chunk_size;    /* --chunk-size (default 4096) */
+    int32_t gpu_batch;     /* lanes per batch (default 64) */
+    int32_t tile;          /* tokens per forward tile (0 = whole chunk) */
+    int32_t max_chunks;    /* <=0: all */
+    int32_t n_threads;     /* OpenMP threads (0 = default) */
+    float temperature;     /* 1.0 default */
+} ref_codec_opts;
+
+/* Returns 0 on success; *out is malloc'd (free with ref_free). */
+int32_t ref_compress(const ref_model* m, const uint8_t* data, int64_t n,
+                     const ref_codec_opts* o, uint8_t** out, int64_t* out_len);
+int32_t ref_decompress(const ref_model* m, const uint8_t* boa, int64_t n,
+                       const ref_codec_opts* o, uint8_t** out, int64_t* out_len);
+void ref_free(void* p);
+
+/* Per-chunk pieces used by tests: encode one chunk into words. */
+int32_t ref_encode_chunk(const ref_model* m, const uint8_t* chunk, int32_t len,
+                         int32_t tile, float temperature, uint32_t* words, int32_t cap_words);
+
+/* ----------------------------------------------------------- container */
+uint32_t ref_crc32(const uint8_t* data, int64_t n);
+int32_t ref_uvarint_encode(uint64_t x, uint8_t* out);
+/* parse: fills header fields; returns 0 or a negative error code */
+typedef struct {
+    uint64_t total_size;
+    uint32_t chunk_len;
+    uint32_t n_chunks;
+    uint32_t last_chunk_len;
+    uint32_t flags;
+    uint32_t interleave_batch;
+    int64_t payload_off;
+    int64_t idx_off;
+    int32_t idx_version;
+} ref_boa2_info;
+int32_t ref_boa2_parse(const uint8_t* buf, int64_t n, ref_boa2_info* info,
+                       uint8_t* first_bytes, uint64_t* offsets, uint64_t* lengths);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
