@@ -19,8 +19,8 @@ LIB_PATH = os.path.join(HERE, "libboa_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "boa_hip.h")
 
 BOA_OK = 0
-K_GEMM, K_SCAN, K_CONV, K_LN, K_CDF, K_CODER, K_DECODE = range(7)
-K_NAMES = ["gemm", "scan", "conv", "ln", "cdf", "coder", "decode"]
+K_GEMM, K_SCAN, K_CONV, K_LN, K_CDF, K_CODER, K_DECODE, K_GEMM_SMALL = range(8)
+K_NAMES = ["gemm", "scan", "conv", "ln", "cdf", "coder", "decode", "gemm_small"]
 
 
 class BoaError(RuntimeError):

@@ -163,13 +163,13 @@ Dims make_dims(const boa_config& cfg) {
   D.r = (cfg.d_model + 15) / 16;
   D.ds = cfg.d_state;
   D.R = D.r + 2 * D.ds;
-  D.ld_in = (int)round_up(2 * D.di, 128);
-  D.ld_x = (int)round_up(D.R, 128);
-  D.ld_out = (int)round_up(D.d, 128);
-  D.ld_1 = (int)round_up(4 * D.d, 128);
-  D.ld_2 = (int)round_up(D.d, 128);
-  D.ld_h1 = (int)round_up(D.d, 128);
-  D.ld_h2 = (int)round_up(VOCAB, 128);
+  D.ld_in = (int)round_up(2 * D.di, 256);
+  D.ld_x = (int)round_up(D.R, 256);
+  D.ld_out = (int)round_up(D.d, 256);
+  D.ld_1 = (int)round_up(4 * D.d, 256);
+  D.ld_2 = (int)round_up(D.d, 256);
+  D.ld_h1 = (int)round_up(D.d, 256);
+  D.ld_h2 = (int)round_up(VOCAB, 256);
   return D;
 }
 
@@ -215,7 +215,8 @@ float* ssm_state_of(boa_ctx* c, int l) {
 hipError_t gemm(boa_ctx* c, const float* X, int ldx, const float* W, int ldw, float* C, int ldc,
                 const float* bias, const float* res, int ldr, int M, int N, int K, int act) {
   GemmArgs a{X, ldx, W, ldw, C, ldc, bias, res, ldr, M, N, K, act};
-  return timed(c, BOA_K_GEMM, 2.0 * M * N * K, [&] { return gemm_f32(a, c->stream); });
+  const int cls = gemm_f32_config(a) == 0 ? BOA_K_GEMM : BOA_K_GEMM_SMALL;
+  return timed(c, cls, 2.0 * M * N * K, [&] { return gemm_f32(a, c->stream); });
 }
 
 // One mambav1 block on `rows` rows (boa_gpu.hpp:895-902 / :835-843):
@@ -463,7 +464,7 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
     return fail(c, BOA_E_FORMAT, msg);
   }
   // device layout: Linear weights transposed to [in][ld] with ld a multiple
-  // of 128 (zero padded) so every GEMM tile load stays in bounds.
+  // of 256 (zero padded) so every GEMM tile load stays in bounds.
   std::vector<std::pair<size_t, std::vector<float>>> parts;  // (offset floats, data)
   size_t total = 0;
   auto place = [&](std::vector<float>&& v) -> size_t {

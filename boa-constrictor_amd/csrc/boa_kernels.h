@@ -11,13 +11,17 @@ enum { ACT_NONE = 0, ACT_GELU = 1, ACT_RELU = 2 };
 
 struct GemmArgs {
   const float* X; int ldx;        // activations [M][K]
-  const float* W; int ldw;        // weights [K][ldw], ldw >= round_up(N, 128), zero padded
+  const float* W; int ldw;        // weights [K][ldw], ldw >= round_up(N, 256), zero padded
   float* C; int ldc;              // output [M][ldc]
   const float* bias;              // [N] or null
   const float* res; int ldr;      // residual [M][ldr] or null (may alias C)
   int M, N, K, act;
 };
 hipError_t gemm_f32(const GemmArgs& a, hipStream_t s);
+// Tile configuration gemm_f32 picks: 0 = 128x256 (bulk GEMMs of a compress
+// tile), 1 = 128x64 (narrow compress GEMMs), 2 = 32x32 (decode-step sizes).
+int gemm_f32_config(const GemmArgs& a);
+hipError_t gemm_f32_sweep(int cfg, const GemmArgs& a, hipStream_t s);
 
 // Encoder / decoder coder state (layout of RCState / RCDecState,
 // portability_solved_cpp/gemm_gpu.hpp:115-121, 212-217, padded to 8 bytes).

@@ -24,21 +24,19 @@ namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int BM, int BN, int WAVES_M, int WAVES_N>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
     const float* __restrict__ X, int ldx, const float* __restrict__ W, int ldw, float* C, int ldc,
     const float* __restrict__ bias, const float* res, int ldr, int M, int N, int K, int act,
-    int vec_store) {
-  constexpr int BK = 16;
+    int vec_store, int swizzle) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int XS = BK + 4;   // activation row stride in LDS (floats)
   constexpr int WS = BN + 16;  // weight row stride in LDS (floats)
-  constexpr int XL = BM * (BK / 4) / NT;  // float4 activation loads per thread
-  constexpr int WL = BK * (BN / 4) / NT;  // float4 weight loads per thread
-  static_assert(XL * NT == BM * (BK / 4), "activation tile load split");
-  static_assert(WL * NT == BK * (BN / 4), "weight tile load split");
+  constexpr int XQ = BM * (BK / 4), WQ = BK * (BN / 4);  // float4s per tile
+  constexpr int XL = (XQ + NT - 1) / NT;  // float4 activation loads per thread
+  constexpr int WL = (WQ + NT - 1) / NT;  // float4 weight loads per thread
   __shared__ __attribute__((aligned(16))) float xs[2][BM * XS];
   __shared__ __attribute__((aligned(16))) float ws[2][BK * WS];
 
@@ -48,7 +46,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
   const int wm0 = (wave / WAVES_N) * WM;
   const int wn0 = (wave % WAVES_N) * WN;
   const int g = lane >> 4, j = lane & 15;
-  const int m_blk = blockIdx.y * BM, n_blk = blockIdx.x * BN;
+  // Workgroup w runs on XCD w % 8.  With the swizzle, each XCD gets a
+  // contiguous range of tiles (all n-blocks of its m-blocks), so an activation
+  // row-block is fetched into one XCD's L2 instead of into all eight.
+  const int nb = (N + BN - 1) / BN;
+  int w = blockIdx.x;
+  if (swizzle) {
+    const int total = gridDim.x, per = total / 8;
+    if (w < per * 8) w = (w % 8) * per + w / 8;
+  }
+  const int m_blk = (w / nb) * BM, n_blk = (w % nb) * BN;
 
   floatx4 acc[TM][TN];
 #pragma unroll
@@ -61,6 +68,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       int q = tid + i * NT;
+      if (XQ % NT && q >= XQ) break;
       int row = q / (BK / 4), k4 = q % (BK / 4);
       int gm = m_blk + row;
       gm = gm < M ? gm : M - 1;  // rows past M are computed but never stored
@@ -69,6 +77,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
 #pragma unroll
     for (int i = 0; i < WL; ++i) {
       int q = tid + i * NT;
+      if (WQ % NT && q >= WQ) break;
       int kr = q / (BN / 4), n4 = q % (BN / 4);
       wr[i] = *reinterpret_cast<const float4*>(W + (size_t)(k0 + kr) * ldw + n_blk + 4 * n4);
     }
@@ -77,12 +86,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
 #pragma unroll
     for (int i = 0; i < XL; ++i) {
       int q = tid + i * NT;
+      if (XQ % NT && q >= XQ) break;
       int row = q / (BK / 4), k4 = q % (BK / 4);
       *reinterpret_cast<float4*>(&xs[buf][row * XS + 4 * k4]) = xr[i];
     }
 #pragma unroll
     for (int i = 0; i < WL; ++i) {
       int q = tid + i * NT;
+      if (WQ % NT && q >= WQ) break;
       int kr = q / (BN / 4), n4 = q % (BN / 4);
       *reinterpret_cast<float4*>(&ws[buf][kr * WS + 4 * n4]) = wr[i];
     }
@@ -148,26 +159,61 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
   }
 }
 
-template <int BM, int BN, int WM_, int WN_>
-static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s) {
-  dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM);
+template <int BM, int BN, int WM_, int WN_, int BK>
+static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s, int swizzle = 1) {
+  if (a.K % BK || a.ldw < (a.N + BN - 1) / BN * BN) return hipErrorInvalidValue;
+  const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+  if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
   int vec = (a.N % 4 == 0) && (a.ldc % 4 == 0) && (!a.res || a.ldr % 4 == 0);
-  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM_, WN_>), grid, dim3(64 * WM_ * WN_), 0, s, a.X,
-                     a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias, a.res, a.ldr, a.M, a.N, a.K, a.act,
-                     vec);
+  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM_, WN_, BK>), dim3((unsigned)tiles),
+                     dim3(64 * WM_ * WN_), 0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias, a.res,
+                     a.ldr, a.M, a.N, a.K, a.act, vec, swizzle);
   return hipGetLastError();
 }
 
 // Tile choice only changes the schedule, never the numerics (see above).
+// Chosen from a sweep on MI355X (fp32 MFMA): many waves per CU matter more
+// than register blocking.  Large M (a compress tile): 128x256 with 16 waves
+// (32x64 each) for N >= 256, 128x64 with 8 waves for the narrow x_proj;
+// small M (a decode step, M = lanes): 32x32 with four 16x16 waves and BK=32.
+int gemm_f32_config(const GemmArgs& a) {
+  if (a.M >= 16384) return a.N >= 256 ? 0 : 1;
+  return 2;
+}
+
 hipError_t gemm_f32(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (a.K % 16 != 0 || a.ldx % 4 != 0 || a.ldw % 4 != 0 || a.ldw < ((a.N + 127) / 128) * 128)
-    return hipErrorInvalidValue;
-  const long long tiles128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128);
-  if (a.N >= 128 && tiles128 >= 1024) return launch_cfg<128, 128, 2, 2>(a, s);
-  const long long tiles64 = (long long)((a.M + 63) / 64) * ((a.N + 63) / 64);
-  if (tiles64 >= 512) return launch_cfg<64, 64, 2, 2>(a, s);
-  return launch_cfg<32, 64, 1, 2>(a, s);
+  if (a.K % 16 != 0 || a.ldx % 4 != 0 || a.ldw % 4 != 0) return hipErrorInvalidValue;
+  switch (gemm_f32_config(a)) {
+    case 0: return launch_cfg<128, 256, 4, 4, 16>(a, s);
+    case 1: return launch_cfg<128, 64, 4, 2, 16>(a, s);
+    default:
+      return a.K % 32 == 0 ? launch_cfg<32, 32, 2, 2, 32>(a, s) : launch_cfg<32, 32, 2, 2, 16>(a, s);
+  }
+}
+
+// Explicit configurations for tile sweeps (same numerics for every entry);
+// cfg >= 100 runs cfg - 100 without the XCD swizzle.
+hipError_t gemm_f32_sweep(int cfg, const GemmArgs& a, hipStream_t s) {
+  const int sw = cfg >= 100 ? 0 : 1;
+  switch (cfg % 100) {
+    case 0: return launch_cfg<128, 128, 2, 2, 16>(a, s, sw);
+    case 2: return launch_cfg<256, 128, 4, 2, 16>(a, s, sw);
+    case 3: return launch_cfg<128, 256, 2, 4, 16>(a, s, sw);
+    case 4: return launch_cfg<64, 64, 2, 2, 16>(a, s, sw);
+    case 7: return launch_cfg<32, 32, 2, 2, 32>(a, s, sw);
+    case 14: return launch_cfg<32, 32, 2, 2, 16>(a, s, sw);
+    case 15: return launch_cfg<64, 128, 2, 2, 16>(a, s, sw);
+    case 16: return launch_cfg<128, 128, 4, 4, 16>(a, s, sw);
+    case 17: return launch_cfg<128, 64, 4, 2, 16>(a, s, sw);
+    case 18: return launch_cfg<64, 64, 4, 4, 16>(a, s, sw);
+    case 19: return launch_cfg<256, 256, 4, 4, 16>(a, s, sw);
+    case 20: return launch_cfg<128, 256, 4, 4, 16>(a, s, sw);
+    case 21: return launch_cfg<32, 64, 2, 4, 16>(a, s, sw);
+    case 22: return launch_cfg<16, 64, 1, 4, 16>(a, s, sw);
+    case 23: return launch_cfg<32, 32, 2, 2, 8>(a, s, sw);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace boa

@@ -11,6 +11,8 @@
 //        GEMM (K = dt_rank fma chain) + softplus of boa_gpu.hpp:317-318 and
 //        the gate of mamba_kernels.cu:130-144
 // rsqrtf is replaced by 1/sqrt with IEEE-rounded division and square root.
+#include <algorithm>
+
 #include "boa_kernels.h"
 
 namespace boa {
@@ -106,41 +108,65 @@ hipError_t launch_ln1_step(const float* emb, const uint8_t* tok, float* x, float
   return hipGetLastError();
 }
 
-// One thread per row, sums in element order (the reference's LN2 order).
+// LN2: per-row sums in element order (the reference's thread-per-row order).
+// A 256-thread block stages `rows_per_block` rows in LDS with coalesced
+// loads (row stride d+1 keeps the per-row sequential reads conflict-free),
+// one thread per row runs the sequential sums, then all threads normalise
+// and store coalesced.  In place is allowed.
 __global__ __launch_bounds__(256) void ln2_kernel(const float* x, float* out,
                                                   const float* __restrict__ w,
-                                                  const float* __restrict__ b, int rows, int d) {
-  const int row = blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= rows) return;
-  const float* xr = x + (size_t)row * d;
-  float s = 0.0f, q = 0.0f;
-  for (int i = 0; i < d; i += 4) {
-    float4 v = *reinterpret_cast<const float4*>(xr + i);
-    s = s + v.x; q = q + v.x * v.x;
-    s = s + v.y; q = q + v.y * v.y;
-    s = s + v.z; q = q + v.z * v.z;
-    s = s + v.w; q = q + v.w * v.w;
+                                                  const float* __restrict__ b, int rows, int d,
+                                                  int rows_per_block) {
+  extern __shared__ float lds[];
+  float* tile = lds;                                   // [rows_per_block][d+1]
+  float* stats = lds + (size_t)rows_per_block * (d + 1);  // mean, inv_std per row
+  const int r0 = blockIdx.x * rows_per_block;
+  const int nr = min(rows_per_block, rows - r0);
+  const int dq = d / 4, S = d + 1;
+  for (int q = threadIdx.x; q < nr * dq; q += blockDim.x) {
+    const int r = q / dq, c4 = q % dq;
+    const float4 v = *reinterpret_cast<const float4*>(x + (size_t)(r0 + r) * d + 4 * c4);
+    float* dst = tile + r * S + 4 * c4;
+    dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
   }
-  float mean = s / (float)d;
-  float var = q / (float)d - mean * mean;
-  float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
-  float* o = out + (size_t)row * d;
-  for (int i = 0; i < d; i += 4) {
-    float4 v = *reinterpret_cast<const float4*>(xr + i);
-    float4 wv = *reinterpret_cast<const float4*>(w + i);
-    float4 bv = *reinterpret_cast<const float4*>(b + i);
-    v.x = ((v.x - mean) * inv_std) * wv.x + bv.x;
-    v.y = ((v.y - mean) * inv_std) * wv.y + bv.y;
-    v.z = ((v.z - mean) * inv_std) * wv.z + bv.z;
-    v.w = ((v.w - mean) * inv_std) * wv.w + bv.w;
-    *reinterpret_cast<float4*>(o + i) = v;
+  __syncthreads();
+  if (threadIdx.x < nr) {
+    const float* row = tile + threadIdx.x * S;
+    float s = 0.0f, q = 0.0f;
+    for (int i = 0; i < d; ++i) {
+      const float v = row[i];
+      s = s + v;
+      q = q + v * v;
+    }
+    const float mean = s / (float)d;
+    const float var = q / (float)d - mean * mean;
+    stats[2 * threadIdx.x] = mean;
+    stats[2 * threadIdx.x + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < nr * dq; q += blockDim.x) {
+    const int r = q / dq, c4 = q % dq;
+    const float mean = stats[2 * r], inv_std = stats[2 * r + 1];
+    const float* src = tile + r * S + 4 * c4;
+    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c4);
+    const float4 bv = *reinterpret_cast<const float4*>(b + 4 * c4);
+    float4 o;
+    o.x = ((src[0] - mean) * inv_std) * wv.x + bv.x;
+    o.y = ((src[1] - mean) * inv_std) * wv.y + bv.y;
+    o.z = ((src[2] - mean) * inv_std) * wv.z + bv.z;
+    o.w = ((src[3] - mean) * inv_std) * wv.w + bv.w;
+    *reinterpret_cast<float4*>(out + (size_t)(r0 + r) * d + 4 * c4) = o;
   }
 }
 
 hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b, int rows, int d,
                       hipStream_t s) {
-  if (d % 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(ln2_kernel, dim3((rows + 255) / 256), dim3(256), 0, s, x, out, w, b, rows, d);
+  if (d % 4 || d > 512) return hipErrorInvalidValue;
+  // at most ~48 KB of LDS per block
+  const int rpb = std::min(64, (48 * 1024) / (4 * (d + 1)));
+  const size_t lds = sizeof(float) * ((size_t)rpb * (d + 1) + 2 * rpb);
+  hipLaunchKernelGGL(ln2_kernel, dim3((rows + rpb - 1) / rpb), dim3(256), lds, s, x, out, w, b,
+                     rows, d, rpb);
   return hipGetLastError();
 }
 
@@ -214,20 +240,21 @@ hipError_t launch_conv_step(const float* xz, float* conv_state, const float* w, 
 
 // -------------------------------------------------------- selective scan
 constexpr int RMAX = 32;  // dt_rank <= 32 (d_model <= 512)
+constexpr int SCAN_TB = 32;  // timesteps of delta rows staged in LDS per pass
 
-template <int DS>
+template <int DS, int RB>
 struct ScanCtx {
-  float wdt[RMAX];
+  float wdt[RB];
   float na[DS];
   float h[DS];
   float bdt, dd;
 };
 
-template <int DS>
-__device__ __forceinline__ void scan_load(ScanCtx<DS>& sc, const LayerW& Lw, const float* ssm,
+template <int DS, int RB>
+__device__ __forceinline__ void scan_load(ScanCtx<DS, RB>& sc, const LayerW& Lw, const float* ssm,
                                           int c, int di, int r) {
 #pragma unroll
-  for (int j = 0; j < RMAX; ++j) sc.wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
+  for (int j = 0; j < RB; ++j) sc.wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; n += 4) {
     float4 a = *reinterpret_cast<const float4*>(Lw.neg_exp_a + (size_t)c * DS + n);
@@ -239,8 +266,8 @@ __device__ __forceinline__ void scan_load(ScanCtx<DS>& sc, const LayerW& Lw, con
   sc.dd = Lw.dd[c];
 }
 
-template <int DS>
-__device__ __forceinline__ void scan_store(const ScanCtx<DS>& sc, float* ssm) {
+template <int DS, int RB>
+__device__ __forceinline__ void scan_store(const ScanCtx<DS, RB>& sc, float* ssm) {
 #pragma unroll
   for (int n = 0; n < DS; n += 4)
     *reinterpret_cast<float4*>(ssm + n) = make_float4(sc.h[n], sc.h[n + 1], sc.h[n + 2], sc.h[n + 3]);
@@ -249,12 +276,12 @@ __device__ __forceinline__ void scan_store(const ScanCtx<DS>& sc, float* ssm) {
 // One token of one channel: dt = softplus(delta[0:r] . w_dt[:, c] + b_dt),
 // h_n = exp(-exp(A_log) dt) h_n + (dt B_n) u, y = sum_n h_n C_n + D u,
 // out = y * (z * sigmoid(z)).
-template <int DS>
-__device__ __forceinline__ float scan_token(ScanCtx<DS>& sc, const float* __restrict__ drow, int r,
-                                            float u, float z) {
+template <int DS, int RB>
+__device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* drow, int r, float u,
+                                            float z) {
   float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < RMAX; ++j)
+  for (int j = 0; j < RB; ++j)
     if (j < r) acc = __builtin_fmaf(drow[j], sc.wdt[j], acc);
   const float dt = softplus(acc + sc.bdt);
   const float* Bv = drow + r;
@@ -273,31 +300,39 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS>& sc, const float* __rest
 }
 
 // Thread per (lane, channel); a block never straddles two lanes, so the
-// delta-row reads are uniform across it.
-template <int DS>
+// delta rows (dt_in | B | C of one token) are shared by the whole block: they
+// are staged in LDS SCAN_TB timesteps at a time and read as broadcasts.
+template <int DS, int RB>
 __global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
                                                          const float* __restrict__ xz,
                                                          const float* __restrict__ conv,
                                                          const float* __restrict__ delta,
                                                          float* ssm_state, float* y, int lanes,
                                                          int T) {
+  extern __shared__ float s_delta[];  // [SCAN_TB][R]
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  const int di = D.di;
-  if (idx >= lanes * di) return;
-  const int c = idx % di, b = idx / di;
+  const int di = D.di, R = D.R;
+  const int c = idx % di, b = idx / di;  // the grid covers lanes * di exactly
   float* ssm = ssm_state + (size_t)idx * DS;
-  ScanCtx<DS> sc;
-  scan_load<DS>(sc, Lw, ssm, c, di, D.r);
-  for (int t = 0; t < T; ++t) {
-    const size_t row = (size_t)b * T + t;
-    const float u = conv[row * di + c];
-    const float z = xz[row * 2 * di + di + c];
-    y[row * di + c] = scan_token<DS>(sc, delta + row * D.R, D.r, u, z);
+  ScanCtx<DS, RB> sc;
+  scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
+  const float* drows = delta + (size_t)b * T * R;
+  for (int t0 = 0; t0 < T; t0 += SCAN_TB) {
+    const int nt = min(SCAN_TB, T - t0);
+    __syncthreads();
+    for (int q = threadIdx.x; q < nt * R; q += blockDim.x) s_delta[q] = drows[(size_t)t0 * R + q];
+    __syncthreads();
+    for (int tt = 0; tt < nt; ++tt) {
+      const size_t row = (size_t)b * T + t0 + tt;
+      const float u = conv[row * di + c];
+      const float z = xz[row * 2 * di + di + c];
+      y[row * di + c] = scan_token<DS, RB>(sc, s_delta + tt * R, D.r, u, z);
+    }
   }
-  scan_store<DS>(sc, ssm);
+  scan_store<DS, RB>(sc, ssm);
 }
 
-template <int DS>
+template <int DS, int RB>
 __global__ __launch_bounds__(256) void scan_step_kernel(Dims D, LayerW Lw,
                                                         const float* __restrict__ xz,
                                                         const float* __restrict__ conv,
@@ -308,10 +343,11 @@ __global__ __launch_bounds__(256) void scan_step_kernel(Dims D, LayerW Lw,
   if (idx >= lanes * di) return;
   const int c = idx % di, b = idx / di;
   float* ssm = ssm_state + (size_t)idx * DS;
-  ScanCtx<DS> sc;
-  scan_load<DS>(sc, Lw, ssm, c, di, D.r);
-  y[idx] = scan_token<DS>(sc, delta + (size_t)b * D.R, D.r, conv[idx], xz[(size_t)b * 2 * di + di + c]);
-  scan_store<DS>(sc, ssm);
+  ScanCtx<DS, RB> sc;
+  scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
+  y[idx] = scan_token<DS, RB>(sc, delta + (size_t)b * D.R, D.r, conv[idx],
+                              xz[(size_t)b * 2 * di + di + c]);
+  scan_store<DS, RB>(sc, ssm);
 }
 
 static int block_for(int di) {
@@ -320,38 +356,52 @@ static int block_for(int di) {
   return 0;
 }
 
+template <int DS, int RB>
+static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
+                                const float* delta, float* ssm_state, float* y, int lanes, int T,
+                                int bs, hipStream_t s) {
+  const size_t lds = sizeof(float) * SCAN_TB * D.R;
+  hipLaunchKernelGGL((scan_chunk_kernel<DS, RB>), dim3((lanes * D.di) / bs), dim3(bs), lds, s, D,
+                     Lw, xz, conv, delta, ssm_state, y, lanes, T);
+  return hipGetLastError();
+}
+
+template <int DS, int RB>
+static hipError_t scan_step_go(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
+                               const float* delta, float* ssm_state, float* y, int lanes, int bs,
+                               hipStream_t s) {
+  hipLaunchKernelGGL((scan_step_kernel<DS, RB>), dim3((lanes * D.di) / bs), dim3(bs), 0, s, D, Lw,
+                     xz, conv, delta, ssm_state, y, lanes);
+  return hipGetLastError();
+}
+
+// dt_rank bound RB in {8, 16, 32}: the smallest that holds D.r.
+#define BOA_SCAN_DISPATCH(GO, ...)                                        \
+  do {                                                                    \
+    if (D.ds == 16) {                                                     \
+      if (D.r <= 8) return GO<16, 8>(__VA_ARGS__);                        \
+      if (D.r <= 16) return GO<16, 16>(__VA_ARGS__);                      \
+      return GO<16, 32>(__VA_ARGS__);                                     \
+    }                                                                     \
+    if (D.r <= 8) return GO<32, 8>(__VA_ARGS__);                          \
+    if (D.r <= 16) return GO<32, 16>(__VA_ARGS__);                        \
+    return GO<32, 32>(__VA_ARGS__);                                       \
+  } while (0)
+
 hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
                              const float* delta, float* ssm_state, float* y, int lanes, int T,
                              hipStream_t s) {
-  int bs = block_for(D.di);
-  if (!bs || D.r > RMAX) return hipErrorInvalidValue;
-  dim3 grid((lanes * D.di) / bs);
-  if (D.ds == 16)
-    hipLaunchKernelGGL(scan_chunk_kernel<16>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
-                       ssm_state, y, lanes, T);
-  else if (D.ds == 32)
-    hipLaunchKernelGGL(scan_chunk_kernel<32>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
-                       ssm_state, y, lanes, T);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const int bs = block_for(D.di);
+  if (!bs || D.r > RMAX || (D.ds != 16 && D.ds != 32)) return hipErrorInvalidValue;
+  BOA_SCAN_DISPATCH(scan_chunk_go, D, Lw, xz, conv, delta, ssm_state, y, lanes, T, bs, s);
 }
 
 hipError_t launch_scan_step(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
                             const float* delta, float* ssm_state, float* y, int lanes,
                             hipStream_t s) {
-  int bs = block_for(D.di);
-  if (!bs || D.r > RMAX) return hipErrorInvalidValue;
-  dim3 grid((lanes * D.di) / bs);
-  if (D.ds == 16)
-    hipLaunchKernelGGL(scan_step_kernel<16>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
-                       ssm_state, y, lanes);
-  else if (D.ds == 32)
-    hipLaunchKernelGGL(scan_step_kernel<32>, grid, dim3(bs), 0, s, D, Lw, xz, conv, delta,
-                       ssm_state, y, lanes);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  const int bs = block_for(D.di);
+  if (!bs || D.r > RMAX || (D.ds != 16 && D.ds != 32)) return hipErrorInvalidValue;
+  BOA_SCAN_DISPATCH(scan_step_go, D, Lw, xz, conv, delta, ssm_state, y, lanes, bs, s);
 }
 
 // ------------------------------------------------------------------ misc

@@ -149,14 +149,15 @@ void boa_free(void* p);
 uint32_t boa_crc32(const uint8_t* data, int64_t n);
 
 /* ---- profiling: HIP events on the context stream ------------------------ */
-#define BOA_K_GEMM 0
+#define BOA_K_GEMM 0       /* GEMMs on the 128x128 tile (compress bulk) */
 #define BOA_K_SCAN 1
 #define BOA_K_CONV 2
 #define BOA_K_LN 3
 #define BOA_K_CDF 4
 #define BOA_K_CODER 5
 #define BOA_K_DECODE 6
-#define BOA_K_COUNT 7
+#define BOA_K_GEMM_SMALL 7 /* GEMMs on the smaller tiles (x_proj, decode) */
+#define BOA_K_COUNT 8
 /* When enabled, every kernel launch is bracketed by HIP events recorded on
  * the launch stream; boa_profile_read synchronises and returns, for a
  * kernel class, the summed kernel time (ms), the launch count and the
