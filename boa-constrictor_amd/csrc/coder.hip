@@ -4,9 +4,12 @@
 // 32-lane group per token, lane l owning symbols 8l..8l+7.  Max by the
 // shuffle-down tree; e_j = exp((l_j - max) / T) in fp32; per-lane sequential
 // double sum; total by the shuffle-down tree (lane 0's value broadcast);
-// exclusive lane prefix by the Hillis-Steele shuffle-up scan; s_cdf written
-// to LDS as a running double sum; then the lane-boundary monotonicity fix-up
-// (all reads happen before any write).  Symbol k's integer interval is
+// exclusive lane prefix by the Hillis-Steele shuffle-up scan; running double
+// sums per lane; then the lane-boundary monotonicity fix-up, propagated lane
+// by lane so that every frequency stays >= 1 (the reference's lock-step
+// fix-up, :903-913, can leave a zero-frequency symbol when two adjacent lanes
+// both shift; the two agree whenever the lock-step result is monotone).
+// s_cdf is written to LDS once.  Symbol k's integer interval is
 // low_k = floor(s_cdf[k] (2^24-256)) + k, high_k = low_{k+1} (2^24 for 255).
 // On wave64 each wavefront carries two tokens, one per 32-lane half.
 //
@@ -147,29 +150,36 @@ __device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias,
     const double tmp = __shfl_up(pre, off, 32);
     if (l >= off) pre = pre + tmp;
   }
+  double r[8];
   double run = pre - ts;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    s_cdf[8 * l + i] = run;
+    r[i] = run;
     run += (double)v[i] * inv;
   }
-  if (l == 31) s_cdf[256] = 1.0;
-  __syncthreads();
-  bool fix = false;
-  double delta = 0.0;
-  if (l > 0) {
-    const double prev_end = s_cdf[8 * l - 1];
-    const double my_start = s_cdf[8 * l];
-    if (my_start < prev_end) {
-      fix = true;
-      delta = prev_end - my_start;
+  // Lane-boundary monotonicity fix-up, propagated lane by lane: lane j
+  // compares its first entry with lane j-1's already fixed last entry and
+  // shifts its eight entries up by the difference.  When no lane starts below
+  // its left neighbour's (unfixed) last entry nothing changes, which the
+  // ballot detects without running the chain.
+  double last = r[7];
+  const double left_last = __shfl_up(last, 1, 32);
+  const bool need = l > 0 && r[0] < left_last;
+  const int shift = threadIdx.x & 32;
+  if ((uint32_t)(__ballot(need) >> shift) != 0u) {
+    for (int j = 1; j < 32; ++j) {
+      const double prev_last = __shfl(last, j - 1, 32);
+      if (l == j && r[0] < prev_last) {
+        const double delta = prev_last - r[0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] += delta;
+        last = r[7];
+      }
     }
   }
-  __syncthreads();
-  if (fix) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) s_cdf[8 * l + i] += delta;
-  }
+  for (int i = 0; i < 8; ++i) s_cdf[8 * l + i] = r[i];
+  if (l == 31) s_cdf[256] = 1.0;
   __syncthreads();
 }
 

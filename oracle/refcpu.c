@@ -286,8 +286,7 @@ void ref_rc_decode_cdf_stream(const uint32_t* cdf, int32_t n_sym, const uint32_t
  * symbols 8l..8l+7; max by shuffle-down tree; per-lane sequential double
  * sum; total by warpReduceSumDouble (shuffle-down 16,8,4,2,1, lane 0's
  * value is used); exclusive lane prefix by warpScanSumDouble (Hillis-
- * Steele, offsets 1..16).  The lane-boundary fix-up reads both neighbours'
- * values before any lane writes (lock-step warp semantics).
+ * Steele, offsets 1..16); then the lane-boundary monotonicity fix-up.
  * ===================================================================== */
 static double tree_sum32(const double* v_in) {
     double v[32];
@@ -307,8 +306,15 @@ static void scan32_inclusive(const double* in, double* out) {
     memcpy(out, v, sizeof v);
 }
 
-void ref_cdf_build(const float* logits, const float* bias, float inv_temperature,
-                   double* s_cdf) {
+/* mode 0 (used everywhere): the lane-boundary fix-up propagates lane by
+ * lane, lane l comparing against lane l-1's already fixed last value, so the
+ * result is monotone.  mode 1: the reference's lock-step form, where every
+ * lane reads its neighbour before any lane writes; when two adjacent lanes
+ * both shift it can leave s_cdf[8l] < s_cdf[8l-1], a zero-frequency symbol
+ * whose encoding the decoder cannot recover.  The two modes agree bit for
+ * bit whenever mode 1's result is monotone. */
+void ref_cdf_build_mode(const float* logits, const float* bias, float inv_temperature,
+                        double* s_cdf, int32_t mode) {
     float vals[VOCAB];
     float lane_max[32];
     for (int l = 0; l < 32; ++l) {
@@ -348,19 +354,35 @@ void ref_cdf_build(const float* logits, const float* bias, float inv_temperature
         }
     }
     s_cdf[256] = 1.0;
-    double delta[32];
-    int fix[32];
-    fix[0] = 0;
-    delta[0] = 0.0;
-    for (int l = 1; l < 32; ++l) {
-        double prev_end = s_cdf[l * 8 - 1];
-        double my_start = s_cdf[l * 8];
-        fix[l] = my_start < prev_end;
-        delta[l] = fix[l] ? prev_end - my_start : 0.0;
+    if (mode == 1) {
+        double delta[32];
+        int fix[32];
+        fix[0] = 0;
+        delta[0] = 0.0;
+        for (int l = 1; l < 32; ++l) {
+            double prev_end = s_cdf[l * 8 - 1];
+            double my_start = s_cdf[l * 8];
+            fix[l] = my_start < prev_end;
+            delta[l] = fix[l] ? prev_end - my_start : 0.0;
+        }
+        for (int l = 1; l < 32; ++l)
+            if (fix[l])
+                for (int i = 0; i < 8; ++i) s_cdf[l * 8 + i] += delta[l];
+    } else {
+        for (int l = 1; l < 32; ++l) {
+            double prev_end = s_cdf[l * 8 - 1];
+            double my_start = s_cdf[l * 8];
+            if (my_start < prev_end) {
+                double delta = prev_end - my_start;
+                for (int i = 0; i < 8; ++i) s_cdf[l * 8 + i] += delta;
+            }
+        }
     }
-    for (int l = 1; l < 32; ++l)
-        if (fix[l])
-            for (int i = 0; i < 8; ++i) s_cdf[l * 8 + i] += delta[l];
+}
+
+void ref_cdf_build(const float* logits, const float* bias, float inv_temperature,
+                   double* s_cdf) {
+    ref_cdf_build_mode(logits, bias, inv_temperature, s_cdf, 0);
 }
 
 static inline uint32_t q_low(const double* s_cdf, int k) {

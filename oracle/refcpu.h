@@ -27,6 +27,9 @@
  *     1/sqrt with IEEE division and square root.
  *   - The chunk-mode conv state update keeps the last d_conv inputs of the
  *     concatenation (old state, tile) also for tiles shorter than d_conv.
+ *   - The CDF lane-boundary fix-up is propagated lane by lane, which keeps
+ *     every frequency >= 1; the reference's lock-step fix-up can leave a
+ *     zero-frequency symbol (ref_cdf_build_mode documents both).
  *
  * Parity pinning of every function here is listed in DESIGN.md; functions
  * without an independent check say "parity unpinned" there.
@@ -91,6 +94,10 @@ void ref_rc_decode_cdf_stream(const uint32_t* cdf, int32_t n_sym, const uint32_t
  * the lane-boundary monotonicity fix-up. */
 void ref_cdf_build(const float* logits, const float* bias, float inv_temperature,
                    double* s_cdf);
+/* mode 0 = ref_cdf_build (fix-up propagated lane by lane, always monotone);
+ * mode 1 = the reference's lock-step fix-up (range_coder_kernels.cu:903-913) */
+void ref_cdf_build_mode(const float* logits, const float* bias, float inv_temperature,
+                        double* s_cdf, int32_t mode);
 /* integer interval of symbol k: low = floor(s_cdf[k]*(2^24-256)) + k ... */
 void ref_cdf_interval(const double* s_cdf, int32_t k, uint32_t* low, uint32_t* high);
 /* all 257 integer boundaries low_0..low_255, 2^24 */

@@ -76,6 +76,7 @@ def lib():
             "ref_rc_encode_cdf_stream": (C.c_int32, [u32p, u8p, C.c_int32, u32p]),
             "ref_rc_decode_cdf_stream": (None, [u32p, C.c_int32, u32p, C.c_int32, u8p]),
             "ref_cdf_build": (None, [f32p, P, C.c_float, f64p]),
+            "ref_cdf_build_mode": (None, [f32p, P, C.c_float, f64p, C.c_int32]),
             "ref_cdf_interval": (None, [f64p, C.c_int32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
             "ref_cdf_quantize": (None, [f64p, u32p]),
             "ref_cdf_search": (C.c_int32, [f64p, C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
@@ -106,13 +107,14 @@ def lib():
 
 
 # ----------------------------------------------------------------- helpers
-def cdf_build(logits, bias=None, inv_temperature=1.0):
+def cdf_build(logits, bias=None, inv_temperature=1.0, mode=0):
     lg = np.ascontiguousarray(logits, dtype=np.float32)
     out = np.empty(257, np.float64)
     b = None
     if bias is not None:
         b = np.ascontiguousarray(bias, dtype=np.float32)
-    lib().ref_cdf_build(lg, b.ctypes.data if b is not None else None, inv_temperature, out)
+    lib().ref_cdf_build_mode(lg, b.ctypes.data if b is not None else None, inv_temperature, out,
+                             mode)
     return out
 
 
