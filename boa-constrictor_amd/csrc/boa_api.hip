@@ -54,8 +54,24 @@ struct boa_ctx {
   std::vector<LayerW> layers;
 
   // recurrent state for max_lanes lanes
-  float* conv_state = nullptr;  // [L][max_lanes][di][4]
-  float* ssm_state = nullptr;   // [L][max_lanes][di][ds]
+  float* conv_state = nullptr;  // [L][max_lanes][di][4]   (chunk layout)
+  float* ssm_state = nullptr;   // [L][max_lanes][di][ds]  (chunk layout)
+  // decode step: k-blocked activations and weights (decode.hip) with lane
+  // capacity ld_dec, and the recurrent state in step layout (conv
+  // [L][di][ld_dec][4], ssm [L][di/16][ds][ld_dec][16]); state_mode says
+  // which layout holds the state: 0 chunk, 1 step, 2 both (all zero)
+  struct DecW {
+    const float *w_in, *w_x, *w_out, *w1, *w2;
+  };
+  float* dwbuf = nullptr;
+  std::vector<DecW> dlayers;
+  const float *dhw1 = nullptr, *dhw2 = nullptr;
+  int ld_dec = 0;
+  float* dec_conv = nullptr;
+  float* dec_ssm = nullptr;
+  int state_mode = 2;
+  float *dxt = nullptr, *dxnt = nullptr, *dot = nullptr, *dzt = nullptr, *dcvt = nullptr,
+        *ddeltat = nullptr, *dyt = nullptr, *dhidt = nullptr, *dlogits = nullptr;
 
   // activations
   int64_t rows_cap = 0;
@@ -290,8 +306,12 @@ hipError_t head_forward(boa_ctx* c, int rows, bool add_bias, float* logits) {
               rows, VOCAB, D.d, ACT_NONE);
 }
 
+hipError_t ensure_state_layout(boa_ctx* c, int want_step);
+
 hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0, float* logits) {
   const int rows = lanes * T;
+  hipError_t es = ensure_state_layout(c, 0);
+  if (es) return es;
   for (int l = 0; l < c->D.L; ++l) {
     hipError_t e = block_forward(c, l, rows, lanes, T, false, &tok, t0, nullptr);
     if (e) return e;
@@ -299,12 +319,99 @@ hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t
   return head_forward(c, rows, true, logits);
 }
 
-hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias, float* logits) {
-  for (int l = 0; l < c->D.L; ++l) {
-    hipError_t e = block_forward(c, l, lanes, lanes, 1, true, nullptr, 0, tok);
+float* dec_conv_of(boa_ctx* c, int l) {
+  return c->dec_conv + (size_t)l * c->D.di * c->ld_dec * 4;
+}
+float* dec_ssm_of(boa_ctx* c, int l) {
+  return c->dec_ssm + (size_t)l * c->D.di * c->D.ds * c->ld_dec;
+}
+
+// W is a k-blocked decode weight with lane capacity round_up(N, 16).
+hipError_t dgemm(boa_ctx* c, const float* Xt, const float* W, float* C, int ldc,
+                 const float* bias, const float* res, int M, int N, int K, int act,
+                 int row_major = 0, int conv_l = -1) {
+  DecGemmArgs a{};
+  a.Xt = Xt; a.ldx = c->ld_dec; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ldc;
+  a.bias = bias;
+  a.res = res; a.ldr = c->ld_dec; a.M = M; a.N = N; a.K = K; a.act = act; a.row_major = row_major;
+  if (conv_l >= 0) {
+    const LayerW& L = c->layers[conv_l];
+    a.conv_di = c->D.di;
+    a.conv_state = dec_conv_of(c, conv_l);
+    a.ld_state = c->ld_dec;
+    a.conv_w = L.conv_w;
+    a.conv_b = L.conv_b;
+    a.conv_out = c->dcvt;
+  }
+  return timed(c, BOA_K_GEMM_SMALL, 2.0 * M * N * K, [&] { return dec_gemm(a, c->stream); });
+}
+
+// Move the recurrent state into the layout the next call needs.
+hipError_t ensure_state_layout(boa_ctx* c, int want_step) {
+  if (c->state_mode == 2 || c->state_mode == want_step) {
+    c->state_mode = want_step;
+    return hipSuccess;
+  }
+  const Dims& D = c->D;
+  for (int l = 0; l < D.L; ++l) {
+    hipError_t e = want_step
+        ? launch_state_relayout(conv_state_of(c, l), ssm_state_of(c, l), dec_conv_of(c, l),
+                                dec_ssm_of(c, l), c->cfg.max_lanes, D.di, D.ds, c->ld_dec, true,
+                                c->stream)
+        : launch_state_relayout(dec_conv_of(c, l), dec_ssm_of(c, l), conv_state_of(c, l),
+                                ssm_state_of(c, l), c->cfg.max_lanes, D.di, D.ds, c->ld_dec, false,
+                                c->stream);
     if (e) return e;
   }
-  return head_forward(c, lanes, add_bias, logits);
+  c->state_mode = want_step;
+  return hipSuccess;
+}
+
+// One decode step for `lanes` lanes on features-major buffers (the mambav1
+// block of boa_gpu.hpp:834-843 and the head of :1048-1052); the causal conv
+// step runs in in_proj's epilogue.  Logits are written row-major [lane][256].
+hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias, float* logits) {
+  const Dims& D = c->D;
+  const int ld = c->ld_dec;
+  hipStream_t s = c->stream;
+  hipError_t e = ensure_state_layout(c, 1);
+  if (e) return e;
+  for (int l = 0; l < D.L; ++l) {
+    const LayerW& W = c->layers[l];
+    const boa_ctx::DecW& DW = c->dlayers[l];
+    e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
+      return launch_dec_ln1(l == 0 ? c->emb : nullptr, tok, c->dxt, c->dxnt, W.ln1_w, W.ln1_b,
+                            lanes, D.d, ld, l == 0 ? c->t_counter : nullptr, s);
+    });
+    if (e) return e;
+    if ((e = dgemm(c, c->dxnt, DW.w_in, c->dzt, ld, W.b_in, nullptr, lanes, 2 * D.di, D.d,
+                   ACT_NONE, 0, l)))
+      return e;
+    if ((e = dgemm(c, c->dcvt, DW.w_x, c->ddeltat, ld, nullptr, nullptr, lanes, D.R, D.di,
+                   ACT_NONE)))
+      return e;
+    e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
+      return launch_dec_scan(D, W, c->dzt, c->dcvt, c->ddeltat, dec_ssm_of(c, l), c->dyt, lanes, ld,
+                             ld, s);
+    });
+    if (e) return e;
+    if ((e = dgemm(c, c->dyt, DW.w_out, c->dot, ld, W.b_out, nullptr, lanes, D.d, D.di,
+                   ACT_NONE)))
+      return e;
+    e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d,
+              [&] { return launch_dec_ln2(c->dot, c->dxnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
+    if (e) return e;
+    if ((e = dgemm(c, c->dxnt, DW.w1, c->dhidt, ld, W.b1, nullptr, lanes, 4 * D.d, D.d,
+                   ACT_GELU)))
+      return e;
+    if ((e = dgemm(c, c->dhidt, DW.w2, c->dxt, ld, W.b2, c->dxt, lanes, D.d, 4 * D.d,
+                   ACT_NONE)))
+      return e;
+  }
+  if ((e = dgemm(c, c->dxt, c->dhw1, c->dot, ld, c->hb1, nullptr, lanes, D.d, D.d, ACT_RELU)))
+    return e;
+  return dgemm(c, c->dot, c->dhw2, logits, VOCAB, add_bias ? c->hb2 : nullptr, nullptr,
+               lanes, VOCAB, D.d, ACT_NONE, 1);
 }
 
 int check_ready(boa_ctx* c) {
@@ -398,6 +505,16 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
   c->stream = c->own_stream;
   const Dims& D = c->D;
   const size_t L = D.L, B = cfg->max_lanes;
+  c->ld_dec = (int)round_up(cfg->max_lanes, 64);
+  const size_t ldd = c->ld_dec;
+  if (dalloc(&c->dec_conv, L * D.di * ldd * 4) || dalloc(&c->dec_ssm, L * D.di * D.ds * ldd) ||
+      dalloc(&c->dxt, D.d * ldd) || dalloc(&c->dxnt, D.d * ldd) || dalloc(&c->dot, D.d * ldd) ||
+      dalloc(&c->dzt, D.di * ldd) || dalloc(&c->dcvt, D.di * ldd) || dalloc(&c->ddeltat, round_up(D.R, 16) * ldd) ||
+      dalloc(&c->dyt, D.di * ldd) || dalloc(&c->dhidt, 4 * D.d * ldd) ||
+      dalloc(&c->dlogits, B * VOCAB)) {
+    boa_destroy(c);
+    return BOA_E_NOMEM;
+  }
   if (dalloc(&c->conv_state, L * B * D.di * 4) || dalloc(&c->ssm_state, L * B * D.di * D.ds) ||
       dalloc(&c->enc, B) || dalloc(&c->dec, B) || dalloc(&c->sizes, B) || dalloc(&c->offsets, B) ||
       dalloc(&c->lens, B) || dalloc(&c->tok, B) || dalloc(&c->t_counter, 1) ||
@@ -414,8 +531,11 @@ void boa_destroy(boa_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   prof_flush(c);
   for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
-  dfree(c->wbuf);
+  dfree(c->wbuf); dfree(c->dwbuf);
   dfree(c->conv_state); dfree(c->ssm_state);
+  dfree(c->dec_conv); dfree(c->dec_ssm);
+  dfree(c->dxt); dfree(c->dxnt); dfree(c->dot); dfree(c->dzt); dfree(c->dcvt); dfree(c->ddeltat);
+  dfree(c->dyt); dfree(c->dhidt); dfree(c->dlogits);
   dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
   dfree(c->hid); dfree(c->logits); dfree(c->lowprob);
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
@@ -557,6 +677,40 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
                        w + o.a_log, w + o.neg_a, nA);
     HIP_TRY(c, hipGetLastError());
   }
+  // k-blocked copies of the Linear weights for the decode step
+  struct DecPart {
+    const float* src;
+    int ldw_in, K, N, permute;
+    const float** dst;
+  };
+  std::vector<DecPart> dp;
+  c->dlayers.assign(D.L, boa_ctx::DecW{});
+  for (int l = 0; l < D.L; ++l) {
+    const LayerW& L = c->layers[l];
+    boa_ctx::DecW& DW = c->dlayers[l];
+    dp.push_back({L.w_in, D.ld_in, D.d, 2 * D.di, 1, &DW.w_in});
+    dp.push_back({L.w_x, D.ld_x, D.di, D.R, 1, &DW.w_x});
+    dp.push_back({L.w_out, D.ld_out, D.di, D.d, 1, &DW.w_out});
+    dp.push_back({L.w1, D.ld_1, D.d, 4 * D.d, 1, &DW.w1});
+    dp.push_back({L.w2, D.ld_2, 4 * D.d, D.d, 1, &DW.w2});
+  }
+  dp.push_back({c->hw1, D.ld_h1, D.d, D.d, 1, &c->dhw1});
+  dp.push_back({c->hw2, D.ld_h2, D.d, VOCAB, 0, &c->dhw2});
+  size_t dtotal = 0;
+  std::vector<size_t> doff;
+  for (const DecPart& q : dp) {
+    doff.push_back(dtotal);
+    dtotal += (size_t)q.K * round_up(q.N, 16);
+  }
+  dfree(c->dwbuf);
+  c->dwbuf = nullptr;
+  if (dalloc(&c->dwbuf, dtotal)) return fail(c, BOA_E_NOMEM, "device allocation of weights failed");
+  for (size_t i = 0; i < dp.size(); ++i) {
+    const DecPart& q = dp[i];
+    HIP_TRY(c, launch_dec_weight_blk(q.src, q.ldw_in, c->dwbuf + doff[i], q.K,
+                                     (int)round_up(q.N, 16), q.permute, c->stream));
+    *q.dst = c->dwbuf + doff[i];
+  }
   HIP_TRY(c, hipStreamSynchronize(c->stream));
   c->loaded = true;
   return BOA_OK;
@@ -573,7 +727,8 @@ int64_t boa_estimate_memory(const boa_config* cfg, int64_t chunk, int32_t compre
   if (!cfg) return -1;
   Dims D = make_dims(*cfg);
   const int64_t B = cfg->max_lanes;
-  int64_t w = boa_weight_file_bytes(D.d, D.L, D.ds, 0) * 2;  // padded transposes, upper bound
+  // padded transposes plus the k-blocked decode copies, upper bound
+  int64_t w = boa_weight_file_bytes(D.d, D.L, D.ds, 0) * 3;
   int64_t state = 4 * (int64_t)D.L * B * D.di * (4 + D.ds);
   int64_t rows = B;
   int64_t words = 0;
@@ -589,11 +744,15 @@ int64_t boa_estimate_memory(const boa_config* cfg, int64_t chunk, int32_t compre
 
 int boa_reset_state(boa_ctx* c, int32_t lanes) {
   if (!c || lanes < 0 || lanes > c->cfg.max_lanes) return BOA_E_ARG;
+  // Every lane is cleared (as reset_cache does for the whole batch), in both
+  // state layouts.
   const Dims& D = c->D;
-  for (int l = 0; l < D.L; ++l) {
-    HIP_TRY(c, launch_fill_zero(conv_state_of(c, l), sizeof(float) * (size_t)lanes * D.di * 4, c->stream));
-    HIP_TRY(c, launch_fill_zero(ssm_state_of(c, l), sizeof(float) * (size_t)lanes * D.di * D.ds, c->stream));
-  }
+  const size_t B = c->cfg.max_lanes, ldd = c->ld_dec, L = D.L;
+  HIP_TRY(c, launch_fill_zero(c->conv_state, sizeof(float) * L * B * D.di * 4, c->stream));
+  HIP_TRY(c, launch_fill_zero(c->ssm_state, sizeof(float) * L * B * D.di * D.ds, c->stream));
+  HIP_TRY(c, launch_fill_zero(c->dec_conv, sizeof(float) * L * D.di * ldd * 4, c->stream));
+  HIP_TRY(c, launch_fill_zero(c->dec_ssm, sizeof(float) * L * D.di * D.ds * ldd, c->stream));
+  c->state_mode = 2;
   return BOA_OK;
 }
 
@@ -615,7 +774,6 @@ int boa_step_batch(boa_ctx* c, const uint8_t* d_tokens, int32_t lanes, float* d_
   if (rc) return rc;
   if (!d_tokens || !d_logits || lanes < 1 || lanes > c->cfg.max_lanes)
     return fail(c, BOA_E_ARG, "boa_step_batch: bad arguments");
-  if ((rc = ensure_rows(c, lanes))) return rc;
   HIP_TRY(c, step_forward(c, d_tokens, lanes, add_bias != 0, d_logits));
   return BOA_OK;
 }
@@ -734,7 +892,6 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       chunk < 1 || last_len < 0 || last_len > chunk)
     return fail(c, BOA_E_ARG, "boa_decompress_device: bad arguments");
   const int B = c->cfg.max_lanes;
-  if ((rc = ensure_rows(c, B))) return rc;
   hipStream_t s = c->stream;
   std::vector<uint64_t> offs(B);
   std::vector<int32_t> nw(B), lens(B);
@@ -771,10 +928,10 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
     // decode kernel reads it: the sequence of launches is identical for
     // every step (graph-capturable).
     for (int32_t t = 1; t < maxlen; ++t) {
-      e = step_forward(c, c->tok, lanes, false, c->logits);
+      e = step_forward(c, c->tok, lanes, false, c->dlogits);
       if (!e)
         e = timed(c, BOA_K_DECODE, 1024.0 * lanes, [&] {
-          return launch_decode_step(c->logits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter,
+          return launch_decode_step(c->dlogits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter,
                                     out, chunk, c->dec, d_payload, c->offsets, c->sizes, lanes, s);
         });
       if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }

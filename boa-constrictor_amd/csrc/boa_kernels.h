@@ -80,6 +80,40 @@ hipError_t launch_scan_step(const Dims& D, const LayerW& Lw, const float* xz, co
                             const float* delta, float* ssm_state, float* y, int lanes, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
+// ---- decode step, features-major activations X^T[feature][lane] ----------
+// Activations and weights are k-blocked (element (k, m) at
+// ((k/16) ld + m) 16 + 4 (k%4) + (k%16)/4), see decode.hip.
+struct DecGemmArgs {
+  const float* Xt; int ldx;   // activations, k-blocked, lane capacity ldx
+  const float* W; int ldw;    // weights, k-blocked over N columns, ldw >= round_up(N, 16)
+  float* C; int ldc;          // output k-blocked over N (row_major = 0) or [M][ldc] (= 1)
+  const float* bias;          // [N] or null
+  const float* res; int ldr;  // residual, k-blocked, or null (may alias C)
+  int M, N, K, act, row_major;
+  // in_proj with the causal conv step fused: features n < conv_di run the
+  // conv (state [n][ld_state] float4, output conv_out k-blocked); features
+  // n >= conv_di are stored at C feature n - conv_di (the z half)
+  int conv_di;
+  float* conv_state; int ld_state;
+  const float* conv_w; const float* conv_b; float* conv_out;
+};
+hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s);
+hipError_t launch_dec_weight_blk(const float* w, int ldw_in, float* out, int K, int ldn,
+                                 int permute, hipStream_t s);
+hipError_t launch_dec_ln1(const float* emb, const uint8_t* tok, float* xt, float* xnt,
+                          const float* w, const float* b, int M, int d, int ld, int* t_counter,
+                          hipStream_t s);
+hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const float* b, int M, int d,
+                          int ld, hipStream_t s);
+hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* zt, const float* cvt,
+                           const float* deltat, float* ssm, float* yt, int M, int ld, int ld_state,
+                           hipStream_t s);
+// chunk layout: conv [lane][c][4], ssm [lane][c][n]; step layout: conv
+// [c][lane][4], ssm [c/16][n][lane][c%16] with lane stride ld_state.
+hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, float* conv_out,
+                                 float* ssm_out, int lanes, int di, int ds, int ld_state,
+                                 bool to_step, hipStream_t s);
+
 // CDF + coder kernels.
 hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,
                                      float inv_temp, uint2* lowprob, hipStream_t s);

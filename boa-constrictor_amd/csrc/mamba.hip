@@ -13,6 +13,7 @@
 // rsqrtf is replaced by 1/sqrt with IEEE-rounded division and square root.
 #include <algorithm>
 
+#include "block_device.h"
 #include "boa_kernels.h"
 
 namespace boa {
@@ -171,18 +172,6 @@ hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b
 }
 
 // ------------------------------------------------------------------ conv1d
-// value = bias + x[t-3] w0 + x[t-2] w1 + x[t-1] w2 + x[t] w3 (unfused, k
-// order), then SiLU.  The state holds the last four inputs, most recent last.
-__device__ __forceinline__ float conv_value(float bias, float xm3, float xm2, float xm1, float x0,
-                                            const float4 w) {
-  float v = bias;
-  v = v + xm3 * w.x;
-  v = v + xm2 * w.y;
-  v = v + xm1 * w.z;
-  v = v + x0 * w.w;
-  return silu(v);
-}
-
 __global__ __launch_bounds__(256) void conv_chunk_kernel(const float* __restrict__ xz,
                                                          float* conv_state,
                                                          const float* __restrict__ w,
@@ -239,66 +228,6 @@ hipError_t launch_conv_step(const float* xz, float* conv_state, const float* w, 
 }
 
 // -------------------------------------------------------- selective scan
-constexpr int RMAX = 32;  // dt_rank <= 32 (d_model <= 512)
-constexpr int SCAN_TB = 32;  // timesteps of delta rows staged in LDS per pass
-
-template <int DS, int RB>
-struct ScanCtx {
-  float wdt[RB];
-  float na[DS];
-  float h[DS];
-  float bdt, dd;
-};
-
-template <int DS, int RB>
-__device__ __forceinline__ void scan_load(ScanCtx<DS, RB>& sc, const LayerW& Lw, const float* ssm,
-                                          int c, int di, int r) {
-#pragma unroll
-  for (int j = 0; j < RB; ++j) sc.wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
-#pragma unroll
-  for (int n = 0; n < DS; n += 4) {
-    float4 a = *reinterpret_cast<const float4*>(Lw.neg_exp_a + (size_t)c * DS + n);
-    sc.na[n] = a.x; sc.na[n + 1] = a.y; sc.na[n + 2] = a.z; sc.na[n + 3] = a.w;
-    float4 hv = *reinterpret_cast<const float4*>(ssm + n);
-    sc.h[n] = hv.x; sc.h[n + 1] = hv.y; sc.h[n + 2] = hv.z; sc.h[n + 3] = hv.w;
-  }
-  sc.bdt = Lw.b_dt[c];
-  sc.dd = Lw.dd[c];
-}
-
-template <int DS, int RB>
-__device__ __forceinline__ void scan_store(const ScanCtx<DS, RB>& sc, float* ssm) {
-#pragma unroll
-  for (int n = 0; n < DS; n += 4)
-    *reinterpret_cast<float4*>(ssm + n) = make_float4(sc.h[n], sc.h[n + 1], sc.h[n + 2], sc.h[n + 3]);
-}
-
-// One token of one channel: dt = softplus(delta[0:r] . w_dt[:, c] + b_dt),
-// h_n = exp(-exp(A_log) dt) h_n + (dt B_n) u, y = sum_n h_n C_n + D u,
-// out = y * (z * sigmoid(z)).
-template <int DS, int RB>
-__device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* drow, int r, float u,
-                                            float z) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < RB; ++j)
-    if (j < r) acc = __builtin_fmaf(drow[j], sc.wdt[j], acc);
-  const float dt = softplus(acc + sc.bdt);
-  const float* Bv = drow + r;
-  const float* Cv = drow + r + DS;
-  float y = 0.0f;
-#pragma unroll
-  for (int n = 0; n < DS; ++n) {
-    float dA = expf_(sc.na[n] * dt);
-    float dB = dt * Bv[n];
-    sc.h[n] = dA * sc.h[n] + dB * u;
-    y = y + sc.h[n] * Cv[n];
-  }
-  y = y + sc.dd * u;
-  float sg = 1.0f / (1.0f + expf_(-z));
-  return y * (z * sg);
-}
-
 // Thread per (lane, channel); a block never straddles two lanes, so the
 // delta rows (dt_in | B | C of one token) are shared by the whole block: they
 // are staged in LDS SCAN_TB timesteps at a time and read as broadcasts.
@@ -326,7 +255,7 @@ __global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
       const size_t row = (size_t)b * T + t0 + tt;
       const float u = conv[row * di + c];
       const float z = xz[row * 2 * di + di + c];
-      y[row * di + c] = scan_token<DS, RB>(sc, s_delta + tt * R, D.r, u, z);
+      y[row * di + c] = scan_token<DS, RB>(sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z);
     }
   }
   scan_store<DS, RB>(sc, ssm);
@@ -345,7 +274,8 @@ __global__ __launch_bounds__(256) void scan_step_kernel(Dims D, LayerW Lw,
   float* ssm = ssm_state + (size_t)idx * DS;
   ScanCtx<DS, RB> sc;
   scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
-  y[idx] = scan_token<DS, RB>(sc, delta + (size_t)b * D.R, D.r, conv[idx],
+  const float* drow = delta + (size_t)b * D.R;
+  y[idx] = scan_token<DS, RB>(sc, drow, drow + D.r, D.r, conv[idx],
                               xz[(size_t)b * 2 * di + di + c]);
   scan_store<DS, RB>(sc, ssm);
 }

@@ -1074,8 +1074,12 @@ int32_t ref_decompress(const ref_model* m, const uint8_t* boa, int64_t n, const 
         total += (c == nc - 1) ? (int64_t)info.last_chunk_len : chunk;
     uint8_t* dst = (uint8_t*)malloc((size_t)(total ? total : 1));
     const uint8_t* payload = boa + info.payload_off;
-    enum { G = 8 };
+    enum { GMAX = 8 };
     int nt = pick_threads(o->n_threads);
+    /* lanes stepped together per thread: up to 8, fewer when that would leave
+     * threads idle */
+    int G = (int)(nc / (uint32_t)(nt > 0 ? nt : 1));
+    G = G < 1 ? 1 : (G > GMAX ? GMAX : G);
     int groups = (int)((nc + G - 1) / G);
     float inv_t = 1.0f / (o->temperature > 0 ? o->temperature : 1.0f);
 #pragma omp parallel num_threads(nt)
@@ -1083,12 +1087,12 @@ int32_t ref_decompress(const ref_model* m, const uint8_t* boa, int64_t n, const 
         scratch_t sc;
         scratch_init(&sc, m, G);
         ref_state* s = ref_state_new(m, G);
-        float* logits = (float*)malloc(sizeof(float) * G * 256);
-        uint8_t tok[G];
-        ref_rc_dec dec[G];
-        uint32_t* words[G];
-        int32_t nw[G], len[G];
-        uint8_t* o_ptr[G];
+        float* logits = (float*)malloc(sizeof(float) * GMAX * 256);
+        uint8_t tok[GMAX];
+        ref_rc_dec dec[GMAX];
+        uint32_t* words[GMAX];
+        int32_t nw[GMAX], len[GMAX];
+        uint8_t* o_ptr[GMAX];
         double s_cdf[257];
 #pragma omp for schedule(dynamic, 1)
         for (int g = 0; g < groups; ++g) {
