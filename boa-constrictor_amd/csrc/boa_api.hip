@@ -62,7 +62,10 @@ struct boa_ctx {
   // which layout holds the state: 0 chunk, 1 step, 2 both (all zero)
   struct DecW {
     const float *w_in, *w_x, *w_out, *w1, *w2;
+    const float* w_dt;  // dt_proj weights, scan quad layout (decode.hip)
+    const float* na;    // -exp(A_log), scan quad layout
   };
+  int n_xdec = 0;  // decode x_proj width: dec_rb(r) + 2 ds
   float* dwbuf = nullptr;
   std::vector<DecW> dlayers;
   const float *dhw1 = nullptr, *dhw2 = nullptr;
@@ -387,12 +390,12 @@ hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias
     if ((e = dgemm(c, c->dxnt, DW.w_in, c->dzt, ld, W.b_in, nullptr, lanes, 2 * D.di, D.d,
                    ACT_NONE, 0, l)))
       return e;
-    if ((e = dgemm(c, c->dcvt, DW.w_x, c->ddeltat, ld, nullptr, nullptr, lanes, D.R, D.di,
+    if ((e = dgemm(c, c->dcvt, DW.w_x, c->ddeltat, ld, nullptr, nullptr, lanes, c->n_xdec, D.di,
                    ACT_NONE)))
       return e;
     e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
-      return launch_dec_scan(D, W, c->dzt, c->dcvt, c->ddeltat, dec_ssm_of(c, l), c->dyt, lanes, ld,
-                             ld, s);
+      return launch_dec_scan(D, W, DW.na, DW.w_dt, c->dzt, c->dcvt, c->ddeltat, dec_ssm_of(c, l),
+                             c->dyt, lanes, ld, ld, s);
     });
     if (e) return e;
     if ((e = dgemm(c, c->dyt, DW.w_out, c->dot, ld, W.b_out, nullptr, lanes, D.d, D.di,
@@ -506,10 +509,11 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
   const Dims& D = c->D;
   const size_t L = D.L, B = cfg->max_lanes;
   c->ld_dec = (int)round_up(cfg->max_lanes, 64);
+  c->n_xdec = dec_rb(D.r) + 2 * D.ds;
   const size_t ldd = c->ld_dec;
   if (dalloc(&c->dec_conv, L * D.di * ldd * 4) || dalloc(&c->dec_ssm, L * D.di * D.ds * ldd) ||
       dalloc(&c->dxt, D.d * ldd) || dalloc(&c->dxnt, D.d * ldd) || dalloc(&c->dot, D.d * ldd) ||
-      dalloc(&c->dzt, D.di * ldd) || dalloc(&c->dcvt, D.di * ldd) || dalloc(&c->ddeltat, round_up(D.R, 16) * ldd) ||
+      dalloc(&c->dzt, D.di * ldd) || dalloc(&c->dcvt, D.di * ldd) || dalloc(&c->ddeltat, round_up(dec_rb(D.r) + 2 * D.ds, 16) * ldd) ||
       dalloc(&c->dyt, D.di * ldd) || dalloc(&c->dhidt, 4 * D.d * ldd) ||
       dalloc(&c->dlogits, B * VOCAB)) {
     boa_destroy(c);
@@ -677,39 +681,51 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
                        w + o.a_log, w + o.neg_a, nA);
     HIP_TRY(c, hipGetLastError());
   }
-  // k-blocked copies of the Linear weights for the decode step
+  // k-blocked copies of the Linear weights for the decode step; x_proj's
+  // copy inserts zero columns so that B starts at feature dec_rb(r)
   struct DecPart {
     const float* src;
-    int ldw_in, K, N, permute;
+    int ldw_in, n_src, K, N, permute, zs, ze;
     const float** dst;
   };
   std::vector<DecPart> dp;
+  const int rb = dec_rb(D.r);
   c->dlayers.assign(D.L, boa_ctx::DecW{});
   for (int l = 0; l < D.L; ++l) {
     const LayerW& L = c->layers[l];
     boa_ctx::DecW& DW = c->dlayers[l];
-    dp.push_back({L.w_in, D.ld_in, D.d, 2 * D.di, 1, &DW.w_in});
-    dp.push_back({L.w_x, D.ld_x, D.di, D.R, 1, &DW.w_x});
-    dp.push_back({L.w_out, D.ld_out, D.di, D.d, 1, &DW.w_out});
-    dp.push_back({L.w1, D.ld_1, D.d, 4 * D.d, 1, &DW.w1});
-    dp.push_back({L.w2, D.ld_2, 4 * D.d, D.d, 1, &DW.w2});
+    dp.push_back({L.w_in, D.ld_in, 2 * D.di, D.d, 2 * D.di, 1, 0, 0, &DW.w_in});
+    dp.push_back({L.w_x, D.ld_x, D.R, D.di, c->n_xdec, 1, D.r, rb, &DW.w_x});
+    dp.push_back({L.w_out, D.ld_out, D.d, D.di, D.d, 1, 0, 0, &DW.w_out});
+    dp.push_back({L.w1, D.ld_1, 4 * D.d, D.d, 4 * D.d, 1, 0, 0, &DW.w1});
+    dp.push_back({L.w2, D.ld_2, D.d, 4 * D.d, D.d, 1, 0, 0, &DW.w2});
   }
-  dp.push_back({c->hw1, D.ld_h1, D.d, D.d, 1, &c->dhw1});
-  dp.push_back({c->hw2, D.ld_h2, D.d, VOCAB, 0, &c->dhw2});
+  dp.push_back({c->hw1, D.ld_h1, D.d, D.d, D.d, 1, 0, 0, &c->dhw1});
+  dp.push_back({c->hw2, D.ld_h2, VOCAB, D.d, VOCAB, 0, 0, 0, &c->dhw2});
   size_t dtotal = 0;
   std::vector<size_t> doff;
   for (const DecPart& q : dp) {
     doff.push_back(dtotal);
     dtotal += (size_t)q.K * round_up(q.N, 16);
   }
+  const size_t wdt_off = dtotal;
+  dtotal += (size_t)D.L * D.di * (rb + D.ds);
   dfree(c->dwbuf);
   c->dwbuf = nullptr;
   if (dalloc(&c->dwbuf, dtotal)) return fail(c, BOA_E_NOMEM, "device allocation of weights failed");
   for (size_t i = 0; i < dp.size(); ++i) {
     const DecPart& q = dp[i];
-    HIP_TRY(c, launch_dec_weight_blk(q.src, q.ldw_in, c->dwbuf + doff[i], q.K,
-                                     (int)round_up(q.N, 16), q.permute, c->stream));
+    HIP_TRY(c, launch_dec_weight_blk(q.src, q.ldw_in, q.n_src, c->dwbuf + doff[i], q.K,
+                                     (int)round_up(q.N, 16), q.permute, q.zs, q.ze, c->stream));
     *q.dst = c->dwbuf + doff[i];
+  }
+  for (int l = 0; l < D.L; ++l) {
+    float* wq = c->dwbuf + wdt_off + (size_t)l * D.di * (rb + D.ds);
+    float* nq = wq + (size_t)D.di * rb;
+    HIP_TRY(c, launch_dec_scan_params(c->layers[l].w_dt, c->layers[l].neg_exp_a, wq, nq, D.r, rb,
+                                      D.ds, D.di, c->stream));
+    c->dlayers[l].w_dt = wq;
+    c->dlayers[l].na = nq;
   }
   HIP_TRY(c, hipStreamSynchronize(c->stream));
   c->loaded = true;

@@ -98,18 +98,24 @@ struct DecGemmArgs {
   const float* conv_w; const float* conv_b; float* conv_out;
 };
 hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s);
-hipError_t launch_dec_weight_blk(const float* w, int ldw_in, float* out, int K, int ldn,
-                                 int permute, hipStream_t s);
+// explicit wave-tile configuration (tile sweeps)
+hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s);
+hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* out, int K, int ldn,
+                                 int permute, int zs, int ze, hipStream_t s);
+hipError_t launch_dec_scan_params(const float* w_dt, const float* na, float* wdt_q, float* na_q,
+                                  int r, int rb, int ds, int di, hipStream_t s);
+// dt_rank slots of the decode scan's row (features [0, dec_rb) hold dt_in)
+inline int dec_rb(int r) { return r <= 8 ? 8 : (r <= 16 ? 16 : 32); }
 hipError_t launch_dec_ln1(const float* emb, const uint8_t* tok, float* xt, float* xnt,
                           const float* w, const float* b, int M, int d, int ld, int* t_counter,
                           hipStream_t s);
 hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const float* b, int M, int d,
                           int ld, hipStream_t s);
-hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* zt, const float* cvt,
-                           const float* deltat, float* ssm, float* yt, int M, int ld, int ld_state,
-                           hipStream_t s);
+hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
+                           const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
+                           int M, int ld, int ld_state, hipStream_t s);
 // chunk layout: conv [lane][c][4], ssm [lane][c][n]; step layout: conv
-// [c][lane][4], ssm [c/16][n][lane][c%16] with lane stride ld_state.
+// [c][lane][4], ssm [c/16][n/4][lane][c%16][n%4] with lane stride ld_state.
 hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, float* conv_out,
                                  float* ssm_out, int lanes, int di, int ds, int ld_state,
                                  bool to_step, hipStream_t s);

@@ -12,9 +12,10 @@
 //     load per operand per four MFMAs, issued two groups ahead, with no LDS
 //     and no barriers (the vector memory pipeline, not the loads' latency,
 //     bounded the feature-per-load form);
-//   - LayerNorm stages a 16-lane slab (contiguous in this layout) in LDS;
+//   - LayerNorm stages 16 lanes' rows (64 contiguous bytes per lane and
+//     block) in LDS;
 //   - the scan runs 16 consecutive threads on the 16 channels of one lane
-//     block, so activations and the k-blocked state are read coalesced.
+//     and loads whole feature blocks and state rows as float4.
 // The per-element operation sequences are those of the chunk kernels
 // (boa_math.h, mamba.hip), and every GEMM output is the same K-ordered fma
 // chain, so decode logits are bit-identical to the compress logits.
@@ -34,63 +35,19 @@ __device__ __forceinline__ size_t dblk(int k, int m, int ld) {
 }
 
 // ------------------------------------------------------------------- GEMM
-// Wave tile: 16 output features x 16 lanes.  Lane (i = lane & 15,
-// g = lane >> 4) loads the float4 at W[q][n0+i][4g..4g+3] and
-// X[q][m0+i][4g..4g+3] (k-blocked), whose component e is its operand for
-// k-step 4q+e; the accumulated k order is 0, 1, 2, ... (one fma chain).
-// Accumulator v of lane (i, g) holds tile row 4g+v for lane m0+i.  For
-// k-blocked outputs the weights' tile rows are stored permuted (row j holds
-// feature n0 + dperm(j)), so row 4g+v is feature n0 + 4v + g and lands at
-// in-block position 4g+v: each lane stores one float4.  Row-major outputs
-// (the logits) use unpermuted weights: row 4g+v is feature n0 + 4g + v.
-template <int KS>
-__global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
-  constexpr int UQ = 2;             // 16-k blocks per prefetch group
-  constexpr int QB = KS / 4;        // 16-k blocks in K
-  constexpr int G = QB / UQ;        // groups
-  static_assert(QB % UQ == 0, "K must be a multiple of 32");
-  const int lane = threadIdx.x & 63;
-  const int i = lane & 15, g = lane >> 4;
-  const int n_tiles = (a.N + 15) / 16;
-  const int m_tiles = (a.M + 15) / 16;
-  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (wid >= n_tiles * m_tiles) return;  // whole waves exit; no barriers below
-  const int n0 = (wid % n_tiles) * 16;
-  const int m0 = (wid / n_tiles) * 16;
-  const int mrow = min(m0 + i, a.M - 1);
-  const float4* wp = reinterpret_cast<const float4*>(a.W) + (size_t)(n0 + i) * 4 + g;
-  const float4* xp = reinterpret_cast<const float4*>(a.Xt) + (size_t)mrow * 4 + g;
-  const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // float4s per 16-k block
-
-  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-  float4 af[3][UQ], bf[3][UQ];
-#define BOA_DEC_LOAD(BUF, Q0)                                      \
-  _Pragma("unroll") for (int q = 0; q < UQ; ++q) {                 \
-    af[BUF][q] = wp[(size_t)((Q0) + q) * wq];                      \
-    bf[BUF][q] = xp[(size_t)((Q0) + q) * xq];                      \
-  }                                                                \
-  __builtin_amdgcn_sched_barrier(0);
-  BOA_DEC_LOAD(0, 0)
-  if (G > 1) { BOA_DEC_LOAD(1, UQ) }
-#pragma unroll
-  for (int gi = 0; gi < G; ++gi) {
-    if (gi + 2 < G) { BOA_DEC_LOAD((gi + 2) % 3, (gi + 2) * UQ) }
-#pragma unroll
-    for (int q = 0; q < UQ; ++q) {
-      const float4 av = af[gi % 3][q], bv = bf[gi % 3][q];
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-#undef BOA_DEC_LOAD
-
-  // Epilogue: acc + bias, activation, + residual.  CONV mode runs the causal
-  // conv step on the x half of in_proj and stores the z half.
-  const int m = m0 + i;
-  if (m >= a.M) return;
+// A wave computes TN x TM MFMA tiles of 16 output features x 16 lanes.  Lane
+// (i = lane & 15, g = lane >> 4) loads, per 16-k block q, the float4s at
+// W[q][n0+16tn+i][4g..4g+3] and X[q][m0+16tm+i][4g..4g+3] (k-blocked), whose
+// component e is its operand for k-step 4q+e; every accumulator sees k in
+// order 0, 1, 2, ... (one fma chain per output).  Accumulator v of lane
+// (i, g) holds tile row 4g+v for lane m0+16tm+i.  For k-blocked outputs the
+// weights' tile rows are stored permuted (row j holds feature dperm(j) of
+// its 16-row tile), so row 4g+v is feature 4v+g and lands at in-block
+// position 4g+v: each lane stores one float4.  Row-major outputs (the
+// logits) use unpermuted weights: row 4g+v is feature 4g+v.
+__device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4 acc, int n0, int m,
+                                             int g) {
+  if (m >= a.M || n0 >= a.N) return;
   int nf[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) nf[e] = a.row_major ? n0 + 4 * g + e : n0 + 4 * e + g;
@@ -114,7 +71,6 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
     }
     return;
   }
-  const bool full = n0 + 16 <= a.N;
   if (a.conv_di > 0 && n0 < a.conv_di) {
     float cv[4];
 #pragma unroll
@@ -137,7 +93,7 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
         *reinterpret_cast<const float4*>(a.res + ((size_t)(n0 >> 4) * a.ldr + m) * 16 + 4 * g);
     v[0] = v[0] + rv.x; v[1] = v[1] + rv.y; v[2] = v[2] + rv.z; v[3] = v[3] + rv.w;
   }
-  if (full) {
+  if (n0 + 16 <= a.N) {
     *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
   } else {
 #pragma unroll
@@ -146,201 +102,418 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
   }
 }
 
-hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
-  if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (a.ldw < (a.N + 15) / 16 * 16 || a.ldx < a.M || a.ldc < (a.row_major ? a.N : a.M) ||
-      (a.res && a.ldr < a.M) || (a.conv_di % 16))
-    return hipErrorInvalidValue;
-  const int tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16);
+// The K loop of one wave: loads run PD groups of UQ 16-k blocks ahead of the
+// MFMAs through a ring of PD + 1 register groups (fully unrolled, so every
+// ring index is a compile-time register).
+template <int KS, int TM, int TN, int UQ, int PD>
+__device__ __forceinline__ void dec_mainloop(const DecGemmArgs& a, int n0, int m0, int i, int g,
+                                             floatx4 (&acc)[TM][TN]) {
+  constexpr int QB = KS / 4;  // 16-k blocks in K
+  constexpr int G = QB / UQ;  // groups of UQ blocks
+  constexpr int R = (PD < G ? PD : G - 1) + 1;  // ring size
+  static_assert(QB % UQ == 0, "K must be a multiple of 16 UQ");
+  const float4* wp[TN];
+  const float4* xp[TM];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+    wp[t] = reinterpret_cast<const float4*>(a.W) + (size_t)min(n0 + 16 * t + i, a.ldw - 1) * 4 + g;
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+    xp[t] = reinterpret_cast<const float4*>(a.Xt) + (size_t)min(m0 + 16 * t + i, a.M - 1) * 4 + g;
+  const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // float4s per 16-k block
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float4 af[R][UQ][TN], bf[R][UQ][TM];
+#define BOA_DEC_LOAD(BUF, Q0)                                                     \
+  _Pragma("unroll") for (int q = 0; q < UQ; ++q) {                                \
+    _Pragma("unroll") for (int t = 0; t < TN; ++t) af[BUF][q][t] = wp[t][(size_t)((Q0) + q) * wq]; \
+    _Pragma("unroll") for (int t = 0; t < TM; ++t) bf[BUF][q][t] = xp[t][(size_t)((Q0) + q) * xq]; \
+  }                                                                               \
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < R - 1; ++p) { BOA_DEC_LOAD(p, p * UQ) }
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    if (gi + R - 1 < G) { BOA_DEC_LOAD((gi + R - 1) % R, (gi + R - 1) * UQ) }
+#pragma unroll
+    for (int q = 0; q < UQ; ++q) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int tn = 0; tn < TN; ++tn)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[gi % R][q][tn][e],
+                                                              bf[gi % R][q][tm][e], acc[tm][tn],
+                                                              0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#undef BOA_DEC_LOAD
+}
+
+template <int KS, int TM, int TN, int UQ, int PD>
+__global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15, g = lane >> 4;
+  const int n_tiles = (a.N + 16 * TN - 1) / (16 * TN);
+  const int m_tiles = (a.M + 16 * TM - 1) / (16 * TM);
+  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wid >= n_tiles * m_tiles) return;  // whole waves exit; no barriers below
+  const int n0 = (wid % n_tiles) * 16 * TN;
+  const int m0 = (wid / n_tiles) * 16 * TM;
+  floatx4 acc[TM][TN];
+  dec_mainloop<KS, TM, TN, UQ, PD>(a, n0, m0, i, g, acc);
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) dec_epilogue(a, acc[tm][tn], n0 + 16 * tn, m0 + 16 * tm + i, g);
+}
+
+namespace {
+template <int TM, int TN, int UQ, int PD>
+hipError_t dec_launch(const DecGemmArgs& a, hipStream_t s) {
+  const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {
-    case 64: hipLaunchKernelGGL((dec_gemm_kernel<16>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((dec_gemm_kernel<32>), grid, block, 0, s, a); break;
-    case 256: hipLaunchKernelGGL((dec_gemm_kernel<64>), grid, block, 0, s, a); break;
-    case 512: hipLaunchKernelGGL((dec_gemm_kernel<128>), grid, block, 0, s, a); break;
-    case 1024: hipLaunchKernelGGL((dec_gemm_kernel<256>), grid, block, 0, s, a); break;
-    case 2048: hipLaunchKernelGGL((dec_gemm_kernel<512>), grid, block, 0, s, a); break;
-    default: return hipErrorInvalidValue;  // decode needs d_model a power of two >= 16
+    case 64: hipLaunchKernelGGL((dec_gemm_kernel<16, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL((dec_gemm_kernel<32, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 256: hipLaunchKernelGGL((dec_gemm_kernel<64, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 512: hipLaunchKernelGGL((dec_gemm_kernel<128, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 1024: hipLaunchKernelGGL((dec_gemm_kernel<256, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 2048: hipLaunchKernelGGL((dec_gemm_kernel<512, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;  // decode needs d_model a power of two >= 64
   }
   return hipGetLastError();
 }
 
+hipError_t dec_check(const DecGemmArgs& a) {
+  if (a.ldw < (a.N + 15) / 16 * 16 || a.ldx < a.M || a.ldc < (a.row_major ? a.N : a.M) ||
+      (a.res && a.ldr < a.M) || (a.conv_di % 16))
+    return hipErrorInvalidValue;
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (hipError_t e = dec_check(a)) return e;
+  switch (cfg) {
+    case 0: return dec_launch<1, 1, 2, 2>(a, s);
+    case 1: return dec_launch<1, 1, 2, 4>(a, s);
+    case 2: return dec_launch<1, 1, 2, 6>(a, s);
+    case 3: return dec_launch<1, 1, 2, 8>(a, s);
+    case 4: return dec_launch<1, 1, 1, 8>(a, s);
+    case 5: return dec_launch<1, 1, 1, 16>(a, s);
+    case 6: return dec_launch<1, 1, 4, 4>(a, s);
+    case 7: return dec_launch<2, 1, 2, 4>(a, s);
+    case 8: return dec_launch<1, 2, 2, 4>(a, s);
+    case 9: return dec_launch<2, 2, 1, 6>(a, s);
+    case 10: return dec_launch<1, 1, 1, 2>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) { return dec_gemm_cfg(a, 0, s); }
+
 // Weight relayout for decode: W [K][ldw_in] row-major (the compress layout)
-// -> k-blocked [K/16][ldn][16]; with `permute`, tile row j of every 16-row
-// output tile holds feature (j & ~15) + dperm(j & 15) (dperm is its own
-// inverse).
-__global__ void dec_weight_blk_kernel(const float* __restrict__ w, int ldw_in, float* out, int K,
-                                      int ldn, int permute) {
+// -> k-blocked [K/16][ldn][16].  Logical output column j maps to source
+// column j (j < zs), to a zero column (zs <= j < ze) or to source column
+// j - (ze - zs) (j >= ze); with `permute`, tile row j of every 16-row
+// output tile holds logical column (j & ~15) + dperm(j & 15) (dperm is its
+// own inverse).
+__global__ void dec_weight_blk_kernel(const float* __restrict__ w, int ldw_in, int n_src,
+                                      float* out, int K, int ldn, int permute, int zs, int ze) {
   const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (size_t)K * ldn) return;
   const int k = (int)(idx / ldn), j = (int)(idx % ldn);
-  const int n = permute ? (j & ~15) + dperm(j & 15) : j;
-  out[dblk(k, j, ldn)] = w[(size_t)k * ldw_in + n];
+  const int jl = permute ? (j & ~15) + dperm(j & 15) : j;
+  const int n = jl < zs ? jl : (jl < ze ? -1 : jl - (ze - zs));
+  out[dblk(k, j, ldn)] = (n >= 0 && n < n_src) ? w[(size_t)k * ldw_in + n] : 0.0f;
 }
 
-hipError_t launch_dec_weight_blk(const float* w, int ldw_in, float* out, int K, int ldn,
-                                 int permute, hipStream_t s) {
-  if (K % 16 || ldn % 16 || ldn > ldw_in) return hipErrorInvalidValue;
+hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* out, int K, int ldn,
+                                 int permute, int zs, int ze, hipStream_t s) {
+  if (K % 16 || ldn % 16 || n_src > ldw_in || zs > ze) return hipErrorInvalidValue;
   const size_t n = (size_t)K * ldn;
   hipLaunchKernelGGL(dec_weight_blk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
-                     ldw_in, out, K, ldn, permute);
+                     ldw_in, n_src, out, K, ldn, permute, zs, ze);
+  return hipGetLastError();
+}
+
+// Per-channel scan parameters in the decode scan's quad layout: element
+// (c, j) of a [di][n] table at (((c/16) n/4 + j/4) 16 + c%16) 4 + j%4.
+// dt_proj weights come from [r][di] (zero padded to rb), -exp(A) from
+// [di][ds].
+__device__ __forceinline__ size_t quad_idx(int c, int j, int n) {
+  return ((size_t)((c >> 4) * (n >> 2) + (j >> 2)) * 16 + (c & 15)) * 4 + (j & 3);
+}
+
+__global__ void dec_scan_params_kernel(const float* __restrict__ w_dt, const float* __restrict__ na,
+                                       float* wdt_q, float* na_q, int r, int rb, int ds, int di) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < di * rb) {
+    const int c = idx / rb, j = idx % rb;
+    wdt_q[quad_idx(c, j, rb)] = j < r ? w_dt[(size_t)j * di + c] : 0.0f;
+  }
+  if (idx < di * ds) {
+    const int c = idx / ds, n = idx % ds;
+    na_q[quad_idx(c, n, ds)] = na[idx];
+  }
+}
+
+hipError_t launch_dec_scan_params(const float* w_dt, const float* na, float* wdt_q, float* na_q,
+                                  int r, int rb, int ds, int di, hipStream_t s) {
+  if (di % 16 || rb % 4 || ds % 4) return hipErrorInvalidValue;
+  const int n = di * (rb > ds ? rb : ds);
+  hipLaunchKernelGGL(dec_scan_params_kernel, dim3((n + 255) / 256), dim3(256), 0, s, w_dt, na, wdt_q,
+                     na_q, r, rb, ds, di);
   return hipGetLastError();
 }
 
 // -------------------------------------------------------------- LayerNorm
-// A 256-thread block normalises DEC_LN_MB lanes: the [d][MB] slab of the
-// features-major input is staged in LDS with coalesced row segments (row
-// stride MB+1), the statistics are computed in the reference's order, and
-// the normalised slab is written back coalesced.
-//   LN1 (mode 1): one 32-lane half-wave per lane; lane l sums elements l,
-//     l+32, ... in order, then the shuffle-down tree 16..1 (the
-//     reference's warp-per-row order, as in the compress LN1 kernel).
-//   LN2 (mode 2): one thread per lane sums all elements in order.
-// Layer 0's LN1 also gathers the embedding rows (and stores x^T).
-constexpr int DEC_LN_MB = 16;
-constexpr int DEC_LN_S = DEC_LN_MB + 1;
+// A 256-thread block normalises 16 lanes.  Thread t loads float4 t % 4 of
+// lane t / 4 % 16's feature block t / 64 + 4 it (a wavefront reads one
+// contiguous 1 KB per load), the slab is kept in LDS in natural feature
+// order, the statistics follow the reference's order, and each thread
+// normalises and stores the float4s it loaded.
+//   LN1 (MODE 1): 16 threads per lane; thread l sums features l, l+32, ...
+//     and l+16, l+48, ... (the partials of lanes l and l+16 of the
+//     reference's warp-per-row reduction), adds them (the shuffle step 16)
+//     and finishes the shuffle-down tree 8, 4, 2, 1 -- the order of the
+//     compress LN1 kernel.
+//   LN2 (MODE 2): one thread per lane sums all features in order.
+// Layer 0's LN1 reads the embedding rows instead (and stores them as x).
+constexpr int DEC_LN_LANES = 16;
 
-template <int MODE>
+template <int MODE, int NB, bool EMB>
 __global__ __launch_bounds__(256) void dec_ln_kernel(const float* __restrict__ emb,
                                                      const uint8_t* __restrict__ tok, float* xt,
                                                      const float* src, float* xnt,
                                                      const float* __restrict__ w,
-                                                     const float* __restrict__ b, int M, int d,
-                                                     int ld, int* t_counter) {
-  __shared__ float tile[512 * DEC_LN_S];
-  __shared__ float stats[2 * DEC_LN_MB];
+                                                     const float* __restrict__ b, int M, int ld,
+                                                     int* t_counter) {
+  constexpr int d = NB * 16;
+  constexpr int S = d + 4;                 // LDS row stride (floats)
+  constexpr int IT = (NB + 3) / 4;         // feature blocks per thread
+  __shared__ __align__(16) float tile[DEC_LN_LANES * S];
+  __shared__ float stats[2 * DEC_LN_LANES];
   if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
-  const int m0 = blockIdx.x * DEC_LN_MB;
-  const int nm = min(DEC_LN_MB, M - m0);
-  for (int q = threadIdx.x; q < d * DEC_LN_MB; q += blockDim.x) {
-    // q -> (feature block, lane, feature in block): contiguous in memory
-    const int i = (q / (16 * DEC_LN_MB)) * 16 + (q % 16), j = (q / 16) % DEC_LN_MB;
-    float v = 0.0f;
-    if (j < nm) {
-      const int m = m0 + j;
-      if (emb) {
-        v = emb[(size_t)tok[m] * d + i];
-        xt[dblk(i, m, ld)] = v;
-      } else {
-        v = src[dblk(i, m, ld)];
-      }
+  const int t = threadIdx.x;
+  const int j = (t >> 2) & 15, a4 = t & 3, kb0 = t >> 6;
+  const int m0 = blockIdx.x * DEC_LN_LANES;
+  const int m = min(m0 + j, M - 1);
+  const float* erow = EMB ? emb + (size_t)tok[m] * d : nullptr;
+  float4 v[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int kb = kb0 + 4 * it;
+    if (kb < NB) {
+      v[it] = EMB ? *reinterpret_cast<const float4*>(erow + 16 * kb + 4 * a4)
+                  : *reinterpret_cast<const float4*>(src + ((size_t)kb * ld + m) * 16 + 4 * a4);
     }
-    tile[i * DEC_LN_S + j] = v;
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int kb = kb0 + 4 * it;
+    if (kb < NB) {
+      float* row = tile + j * S + 16 * kb;
+      const float e4[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) row[EMB ? 4 * a4 + e : dperm(4 * a4 + e)] = e4[e];
+    }
   }
   __syncthreads();
   if (MODE == 1) {
-    const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
-    for (int j = half; j < DEC_LN_MB; j += 8) {
-      float sum = 0.0f, sq = 0.0f;
-      for (int idx = l; idx < d; idx += 32) {
-        const float v = tile[idx * DEC_LN_S + j];
-        sum = sum + v;
-        sq = sq + v * v;
-      }
-#pragma unroll
-      for (int off = 16; off > 0; off >>= 1) {
-        sum = sum + __shfl_down(sum, off, 32);
-        sq = sq + __shfl_down(sq, off, 32);
-      }
-      if (l == 0) {
-        const float mean = sum / (float)d;
-        const float var = sq / (float)d - mean * mean;
-        stats[2 * j] = mean;
-        stats[2 * j + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
-      }
+    const int lj = t >> 4, l = t & 15;
+    const float* row = tile + lj * S;
+    float s0 = 0.0f, q0 = 0.0f, s1 = 0.0f, q1 = 0.0f;
+#pragma unroll 4
+    for (int k = l; k < d; k += 32) {
+      const float x = row[k];
+      s0 = s0 + x;
+      q0 = q0 + x * x;
     }
-  } else if (threadIdx.x < DEC_LN_MB) {
-    const int j = threadIdx.x;
+#pragma unroll 4
+    for (int k = l + 16; k < d; k += 32) {
+      const float x = row[k];
+      s1 = s1 + x;
+      q1 = q1 + x * x;
+    }
+    float sum = s0 + s1, sq = q0 + q1;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+      sum = sum + __shfl_down(sum, off, 16);
+      sq = sq + __shfl_down(sq, off, 16);
+    }
+    if (l == 0) {
+      const float mean = sum / (float)d;
+      const float var = sq / (float)d - mean * mean;
+      stats[2 * lj] = mean;
+      stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    }
+  } else if (t < DEC_LN_LANES) {
+    const float4* row = reinterpret_cast<const float4*>(tile + t * S);
     float sum = 0.0f, sq = 0.0f;
-    for (int idx = 0; idx < d; ++idx) {
-      const float v = tile[idx * DEC_LN_S + j];
-      sum = sum + v;
-      sq = sq + v * v;
+#pragma unroll 8
+    for (int k4 = 0; k4 < d / 4; ++k4) {
+      const float4 x = row[k4];
+      sum = sum + x.x; sq = sq + x.x * x.x;
+      sum = sum + x.y; sq = sq + x.y * x.y;
+      sum = sum + x.z; sq = sq + x.z * x.z;
+      sum = sum + x.w; sq = sq + x.w * x.w;
     }
     const float mean = sum / (float)d;
     const float var = sq / (float)d - mean * mean;
-    stats[2 * j] = mean;
-    stats[2 * j + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    stats[2 * t] = mean;
+    stats[2 * t + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
   }
   __syncthreads();
-  for (int q = threadIdx.x; q < d * DEC_LN_MB; q += blockDim.x) {
-    const int i = (q / (16 * DEC_LN_MB)) * 16 + (q % 16), j = (q / 16) % DEC_LN_MB;
-    if (j < nm) {
-      const float v = tile[i * DEC_LN_S + j];
-      xnt[dblk(i, m0 + j, ld)] = ((v - stats[2 * j]) * stats[2 * j + 1]) * w[i] + b[i];
+  if (m0 + j >= M) return;
+  const float mean = stats[2 * j], rstd = stats[2 * j + 1];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int kb = kb0 + 4 * it;
+    if (kb < NB) {
+      const float* row = tile + j * S + 16 * kb;
+      float x[4], o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int f = dperm(4 * a4 + e);  // feature in block at position 4 a4 + e
+        x[e] = row[f];
+        o[e] = ((x[e] - mean) * rstd) * w[16 * kb + f] + b[16 * kb + f];
+      }
+      const size_t off = ((size_t)kb * ld + m0 + j) * 16 + 4 * a4;
+      if (EMB) *reinterpret_cast<float4*>(xt + off) = make_float4(x[0], x[1], x[2], x[3]);
+      *reinterpret_cast<float4*>(xnt + off) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }
 }
+
+namespace {
+template <int MODE>
+hipError_t dec_ln_launch(const float* emb, const uint8_t* tok, float* xt, const float* src,
+                         float* xnt, const float* w, const float* b, int M, int d, int ld,
+                         int* t_counter, hipStream_t s) {
+  const dim3 grid((M + DEC_LN_LANES - 1) / DEC_LN_LANES), block(256);
+#define BOA_DEC_LN(NBv)                                                                        \
+  if (emb)                                                                                     \
+    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, true>), grid, block, 0, s, emb, tok, xt, src, \
+                       xnt, w, b, M, ld, t_counter);                                           \
+  else                                                                                         \
+    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, false>), grid, block, 0, s, emb, tok, xt, src, \
+                       xnt, w, b, M, ld, t_counter);
+  switch (d) {
+    case 64: BOA_DEC_LN(4) break;
+    case 128: BOA_DEC_LN(8) break;
+    case 256: BOA_DEC_LN(16) break;
+    case 512: BOA_DEC_LN(32) break;
+    default: return hipErrorInvalidValue;  // decode needs d_model in {64, 128, 256, 512}
+  }
+#undef BOA_DEC_LN
+  return hipGetLastError();
+}
+}  // namespace
 
 hipError_t launch_dec_ln1(const float* emb, const uint8_t* tok, float* xt, float* xnt,
                           const float* w, const float* b, int M, int d, int ld, int* t_counter,
                           hipStream_t s) {
-  if (d > 512) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dec_ln_kernel<1>, dim3((M + DEC_LN_MB - 1) / DEC_LN_MB), dim3(256), 0, s, emb,
-                     tok, xt, xt, xnt, w, b, M, d, ld, t_counter);
-  return hipGetLastError();
+  return dec_ln_launch<1>(emb, tok, xt, xt, xnt, w, b, M, d, ld, t_counter, s);
 }
 
 hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const float* b, int M, int d,
                           int ld, hipStream_t s) {
-  if (d > 512) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dec_ln_kernel<2>, dim3((M + DEC_LN_MB - 1) / DEC_LN_MB), dim3(256), 0, s,
-                     nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, ld, nullptr);
-  return hipGetLastError();
+  return dec_ln_launch<2>(nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, ld, nullptr, s);
 }
 
 // ------------------------------------------------------------------- scan
-// Thread t of block (x, y): channel c = 16 y + t % 16, lane m = 16 x + t / 16
-// (16 lanes per block); the k-blocked state keeps h[c][n][m] at
-// ((c/16 * ds + n) * ld_state + m) * 16 + c % 16.
+__device__ __forceinline__ void dec_load16(const float* p, float* f) {
+  const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float4 t = q[a];
+    f[4 * a] = t.x; f[4 * a + 1] = t.y; f[4 * a + 2] = t.z; f[4 * a + 3] = t.w;
+  }
+}
+
+// Thread t of block (x, y): channel c = 16 y + t % 16, lane m = 16 x + t / 16.
+// The decode x_proj writes its row with dt_in at features [0, r), zeros up
+// to RB, B at [RB, RB + DS) and C at [RB + DS, RB + 2 DS), so the thread
+// loads whole 16-feature blocks (float4) and indexes them at compile time.
+// State, -exp(A) and dt_proj weights are stored in quads of four n (or j)
+// with the 16 channels of a channel block innermost, so that every float4
+// load of a wavefront reads one contiguous 1 KB (state) or 256 B span:
+//   h[c][n] of lane m at ((((c/16) DS/4 + n/4) ld_state + m) 16 + c%16) 4 + n%4
+//   na[c][n]          at (((c/16) DS/4 + n/4) 16 + c%16) 4 + n%4
+//   wdt[c][j]         at (((c/16) RB/4 + j/4) 16 + c%16) 4 + j%4
 template <int DS, int RB>
-__global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* __restrict__ zt,
+__global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* __restrict__ na_q,
+                                                       const float* __restrict__ wdt_q,
+                                                       const float* __restrict__ zt,
                                                        const float* __restrict__ cvt,
-                                                       const float* __restrict__ deltat,
+                                                       const float* __restrict__ rows,
                                                        float* ssm, float* yt, int M, int ld,
-                                                       int ld_state, int r, int di) {
+                                                       int ld_state, int r) {
+  constexpr int NB = (RB + 2 * DS + 15) / 16;
   const int cl = threadIdx.x & 15;
-  const int c = blockIdx.y * 16 + cl;
+  const int cb = blockIdx.y;
+  const int c = cb * 16 + cl;
   const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
   if (m >= M) return;
   ScanCtx<DS, RB> sc;
+  float4* h4 = reinterpret_cast<float4*>(ssm);
+  const float4* na4 = reinterpret_cast<const float4*>(na_q);
+  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
 #pragma unroll
-  for (int j = 0; j < RB; ++j) sc.wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
-  float* h = ssm + ((size_t)blockIdx.y * DS * ld_state + m) * 16 + cl;
+  for (int n4 = 0; n4 < DS / 4; ++n4) {
+    const float4 hv = h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl];
+    sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
+    const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
+    sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
+  }
 #pragma unroll
-  for (int n = 0; n < DS; ++n) {
-    sc.na[n] = Lw.neg_exp_a[(size_t)c * DS + n];
-    sc.h[n] = h[(size_t)n * ld_state * 16];
+  for (int j4 = 0; j4 < RB / 4; ++j4) {
+    const float4 wv = w4[(cb * (RB / 4) + j4) * 16 + cl];
+    sc.wdt[4 * j4] = wv.x; sc.wdt[4 * j4 + 1] = wv.y; sc.wdt[4 * j4 + 2] = wv.z; sc.wdt[4 * j4 + 3] = wv.w;
   }
   sc.bdt = Lw.b_dt[c];
   sc.dd = Lw.dd[c];
-  float drow[RB + 2 * DS];
+  float row[NB * 16];
 #pragma unroll
-  for (int j = 0; j < RB; ++j) drow[j] = j < r ? deltat[dblk(j, m, ld)] : 0.0f;
+  for (int kb = 0; kb < NB; ++kb) {
+    float f[16];
+    dec_load16(rows + ((size_t)kb * ld + m) * 16, f);
 #pragma unroll
-  for (int j = 0; j < 2 * DS; ++j) drow[RB + j] = deltat[dblk(r + j, m, ld)];
-  const float u = cvt[dblk(c, m, ld)];
-  const float z = zt[dblk(c, m, ld)];
-  yt[dblk(c, m, ld)] = scan_token<DS, RB>(sc, drow, drow + RB, r, u, z);
+    for (int j = 0; j < 16; ++j) row[16 * kb + j] = f[dperm(j)];
+  }
+  const size_t cm = dblk(c, m, ld);
+  const float u = cvt[cm];
+  const float z = zt[cm];
+  yt[cm] = scan_token<DS, RB>(sc, row, row + RB, r, u, z);
 #pragma unroll
-  for (int n = 0; n < DS; ++n) h[(size_t)n * ld_state * 16] = sc.h[n];
+  for (int n4 = 0; n4 < DS / 4; ++n4)
+    h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl] =
+        make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]);
 }
 
-hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* zt, const float* cvt,
-                           const float* deltat, float* ssm, float* yt, int M, int ld, int ld_state,
-                           hipStream_t s) {
-  if (D.di % 16) return hipErrorInvalidValue;
+hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
+                           const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
+                           int M, int ld, int ld_state, hipStream_t s) {
+  if (D.di % 16 || dec_rb(D.r) < D.r) return hipErrorInvalidValue;
   dim3 grid((M + 15) / 16, D.di / 16);
-#define BOA_DEC_SCAN(DSv, RBv)                                                                \
-  hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, zt, cvt, deltat, \
-                     ssm, yt, M, ld, ld_state, D.r, D.di)
+#define BOA_DEC_SCAN(DSv, RBv)                                                                   \
+  hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, zt, cvt, \
+                     rows, ssm, yt, M, ld, ld_state, D.r)
+  const int rb = dec_rb(D.r);
   if (D.ds == 16) {
-    if (D.r <= 8) BOA_DEC_SCAN(16, 8);
-    else if (D.r <= 16) BOA_DEC_SCAN(16, 16);
+    if (rb == 8) BOA_DEC_SCAN(16, 8);
+    else if (rb == 16) BOA_DEC_SCAN(16, 16);
     else BOA_DEC_SCAN(16, 32);
   } else if (D.ds == 32) {
-    if (D.r <= 8) BOA_DEC_SCAN(32, 8);
-    else if (D.r <= 16) BOA_DEC_SCAN(32, 16);
+    if (rb == 8) BOA_DEC_SCAN(32, 8);
+    else if (rb == 16) BOA_DEC_SCAN(32, 16);
     else BOA_DEC_SCAN(32, 32);
   } else {
     return hipErrorInvalidValue;
@@ -351,7 +524,7 @@ hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* zt, con
 
 // --------------------------------------------------- state layout changes
 // chunk layout: conv [lane][c][4], ssm [lane][c][n]
-// step layout:  conv [c][lane][4], ssm [c/16][n][lane][c%16] (lane stride ld_state)
+// step layout:  conv [c][lane][4], ssm [c/16][n/4][lane][c%16][n%4] (lane stride ld_state)
 __global__ void state_to_step_kernel(const float* conv_in, const float* ssm_in, float* conv_out,
                                      float* ssm_out, int lanes, int di, int ds, int ld_state) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -360,8 +533,8 @@ __global__ void state_to_step_kernel(const float* conv_in, const float* ssm_in, 
   reinterpret_cast<float4*>(conv_out)[(size_t)c * ld_state + b] =
       reinterpret_cast<const float4*>(conv_in)[idx];
   for (int n = 0; n < ds; ++n)
-    ssm_out[(((size_t)(c >> 4) * ds + n) * ld_state + b) * 16 + (c & 15)] =
-        ssm_in[(size_t)idx * ds + n];
+    ssm_out[((((size_t)(c >> 4) * (ds >> 2) + (n >> 2)) * ld_state + b) * 16 + (c & 15)) * 4 +
+            (n & 3)] = ssm_in[(size_t)idx * ds + n];
 }
 
 __global__ void state_to_chunk_kernel(const float* conv_in, const float* ssm_in, float* conv_out,
@@ -373,7 +546,8 @@ __global__ void state_to_chunk_kernel(const float* conv_in, const float* ssm_in,
       reinterpret_cast<const float4*>(conv_in)[(size_t)c * ld_state + b];
   for (int n = 0; n < ds; ++n)
     ssm_out[(size_t)idx * ds + n] =
-        ssm_in[(((size_t)(c >> 4) * ds + n) * ld_state + b) * 16 + (c & 15)];
+        ssm_in[((((size_t)(c >> 4) * (ds >> 2) + (n >> 2)) * ld_state + b) * 16 + (c & 15)) * 4 +
+               (n & 3)];
 }
 
 hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, float* conv_out,
