@@ -30,6 +30,34 @@ sys.path.insert(0, os.path.join(ROOT, "boa-constrictor_amd"))
 METRIC = ("compress & decompress input MB/s at d256×8L, 1000 chunks; "
           "compression ratio")
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E peak
+GEMM_KERNEL = "boa::gemm_f32_kernel<128, 256, 4, 4, 16>"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_c2_traffic.json")
+
+
+def gemm_traffic_bytes():
+    """HBM bytes per launch of the dominant GEMM from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs, scaled by the copy-kernel calibration."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return round((t["fetch_kib_per_dispatch"] * t["fetch_scale"] +
+                      t["write_kib_per_dispatch"] * t["write_scale"]) * 1024)
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_calibration(nbytes: int, reps: int) -> int:
+    """A plain device copy of `nbytes` (torch's copy kernel), for scaling the
+    FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": nbytes, "reps": reps}), flush=True)
+    return 0
 
 
 def uvarint_len(x: int) -> int:
@@ -78,7 +106,14 @@ def main() -> int:
     ap.add_argument("--cpu-sample-chunks", type=int, default=0)
     ap.add_argument("--cpu-sample-len", type=int, default=4096)
     ap.add_argument("--no-decompress", action="store_true")
+    ap.add_argument("--host-path", action="store_true",
+                    help="also time the host-buffer path (bytes in host memory -> BOA2 container "
+                         "in host memory, PCIe transfers included)")
+    ap.add_argument("--copy-calibrate", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
+    if args.copy_calibrate:
+        return copy_calibration(args.copy_calibrate, 5)
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -167,26 +202,55 @@ def main() -> int:
     dec_mb_s = n * K / t_d / 1e6 if not args.no_decompress else None
     ratio = n / container_bytes(lens, n_chunks)
 
+    # per-class kernel times come from HIP events recorded around every
+    # launch on the stream the kernels run on (boa_profile_*)
     g = prof["gemm"]
     gemm_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
     kernel_ms = {k: round(v["ms"], 3) for k, v in prof.items()}
     roofline = {
         "bound": "mfma",
-        "kernel": "boa::gemm_f32_kernel<128,128,2,2>",
+        "kernel": GEMM_KERNEL,
         "achieved": round(gemm_tflops, 2),
         "peak": PEAK_FP32_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(gemm_tflops / PEAK_FP32_TFLOPS, 4),
-        "traffic": None,
+        "traffic": gemm_traffic_bytes(),
         "launches": g["launches"],
         "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4),
         "flop_per_launch": round(g["work"] / max(g["launches"], 1)),
     }
+    sc = prof["scan"]
+    scan_gbs = sc["work"] / (sc["ms"] * 1e-3) / 1e9 if sc["ms"] > 0 else 0.0
+    roofline_scan = {
+        "bound": "hbm",
+        "kernel": "boa::scan_chunk_kernel<16, 16>",
+        "achieved": round(scan_gbs, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(scan_gbs / PEAK_HBM_GBS, 4),
+        "launches": sc["launches"],
+        "avg_launch_ms": round(sc["ms"] / max(sc["launches"], 1), 4),
+        "bytes_per_launch": round(sc["work"] / max(sc["launches"], 1)),
+    }
+
+    host = None
+    if args.host_path:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        blob = codec.compress(data, chunk_size=chunk)
+        t1 = time.perf_counter()
+        back = codec.decompress(blob) if not args.no_decompress else data
+        t2 = time.perf_counter()
+        host = {"compress_mb_s": round(n / (t1 - t0) / 1e6, 4),
+                "decompress_mb_s": round(n / (t2 - t1) / 1e6, 4) if not args.no_decompress else None,
+                "container_bytes": len(blob), "roundtrip_ok": back == data,
+                "container_matches_device_path": len(blob) == container_bytes(lens, n_chunks)}
+        ok_all = ok_all and host["roundtrip_ok"]
 
     cpu = None
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        sample_chunks = args.cpu_sample_chunks or 2 * threads
+        sample_chunks = args.cpu_sample_chunks or 4 * threads
         print(f"[bench] cpu baseline: {sample_chunks} chunks x {args.cpu_sample_len} B on {threads} threads",
               file=sys.stderr, flush=True)
         cb = cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, args.cpu_sample_len,
@@ -220,8 +284,11 @@ def main() -> int:
         "roundtrip_ok": ok_all,
         "compress_kernel_ms": kernel_ms,
         "roofline": roofline,
+        "roofline_scan": roofline_scan,
         "cpu_baseline": cpu,
     }
+    if host:
+        out["host_path"] = host
     if cpu:
         out["speedup_vs_cpu_compress"] = round(comp_mb_s / cpu["value"], 1)
     print(json.dumps(out), flush=True)

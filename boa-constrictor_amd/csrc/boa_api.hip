@@ -91,7 +91,11 @@ struct boa_ctx {
   uint64_t* offsets = nullptr;
   int32_t* lens = nullptr;
   uint8_t* tok = nullptr;
-  int* t_counter = nullptr;
+  int* t_counter = nullptr;     // decode step counter (device)
+
+  // decompress: every step is replayed from a HIP graph on dec_stream
+  hipStream_t dec_stream = nullptr;
+  hipEvent_t dec_fork = nullptr, dec_join = nullptr;
   int32_t* h_sizes = nullptr;  // pinned
 
   // profiling
@@ -238,53 +242,38 @@ hipError_t gemm(boa_ctx* c, const float* X, int ldx, const float* W, int ldw, fl
   return timed(c, cls, 2.0 * M * N * K, [&] { return gemm_f32(a, c->stream); });
 }
 
-// One mambav1 block on `rows` rows (boa_gpu.hpp:895-902 / :835-843):
+// One mambav1 block on `rows` = lanes x T rows (boa_gpu.hpp:895-902):
 // res = x; x = LN1(x); x = Mamba(x); x = LN2(x); x = FF(x) + res.
 // x keeps the residual, LN1 writes xn, out_proj writes xn.
-hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, bool step,
-                         const TokenSrc* tok0, int t0, const uint8_t* step_tok) {
+hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const TokenSrc& tok0,
+                         int t0) {
   const Dims& D = c->D;
   const LayerW W = layer_at(c, l);
   hipStream_t s = c->stream;
   hipError_t e;
   const double ln_bytes = 3.0 * 4 * rows * D.d;
-  if (l == 0 && step) {
-    e = timed(c, BOA_K_LN, ln_bytes, [&] {
-      return launch_ln1_step(c->emb, step_tok, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, s,
-                             c->t_counter);
-    });
-  } else if (l == 0) {
-    e = timed(c, BOA_K_LN, ln_bytes, [&] {
-      return launch_ln1(c->emb, *tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, s);
-    });
-  } else {
-    e = timed(c, BOA_K_LN, ln_bytes, [&] {
-      return launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b,
-                        rows, D.d, s);
-    });
-  }
+  e = timed(c, BOA_K_LN, ln_bytes, [&] {
+    return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, s)
+                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
+                               W.ln1_b, rows, D.d, s);
+  });
   if (e) return e;
   if ((e = gemm(c, c->xn, D.d, W.w_in, D.ld_in, c->xz, 2 * D.di, W.b_in, nullptr, 0, rows,
                 2 * D.di, D.d, ACT_NONE)))
     return e;
   const double conv_bytes = 4.0 * rows * D.di * 2;
   e = timed(c, BOA_K_CONV, conv_bytes, [&] {
-    return step ? launch_conv_step(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes,
-                                   D.di, s)
-                : launch_conv_chunk(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes,
-                                    T, D.di, s);
+    return launch_conv_chunk(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes, T,
+                             D.di, s);
   });
   if (e) return e;
   if ((e = gemm(c, c->cv, D.di, W.w_x, D.ld_x, c->delta, D.R, nullptr, nullptr, 0, rows, D.R, D.di,
                 ACT_NONE)))
     return e;
   // algorithmic bytes: u, z, y per element, the delta row per token
-  const double scan_bytes = 4.0 * rows * (3.0 * D.di + D.R) +
-                            (step ? 8.0 * lanes * D.di * D.ds : 0.0);
+  const double scan_bytes = 4.0 * rows * (3.0 * D.di + D.R);
   e = timed(c, BOA_K_SCAN, scan_bytes, [&] {
-    return step ? launch_scan_step(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes, s)
-                : launch_scan_chunk(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes,
-                                    T, s);
+    return launch_scan_chunk(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes, T, s);
   });
   if (e) return e;
   if ((e = gemm(c, c->y, D.di, W.w_out, D.ld_out, c->xn, D.d, W.b_out, nullptr, 0, rows, D.d, D.di,
@@ -316,7 +305,7 @@ hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t
   hipError_t es = ensure_state_layout(c, 0);
   if (es) return es;
   for (int l = 0; l < c->D.L; ++l) {
-    hipError_t e = block_forward(c, l, rows, lanes, T, false, &tok, t0, nullptr);
+    hipError_t e = block_forward(c, l, rows, lanes, T, tok, t0);
     if (e) return e;
   }
   return head_forward(c, rows, true, logits);
@@ -332,20 +321,11 @@ float* dec_ssm_of(boa_ctx* c, int l) {
 // W is a k-blocked decode weight with lane capacity round_up(N, 16).
 hipError_t dgemm(boa_ctx* c, const float* Xt, const float* W, float* C, int ldc,
                  const float* bias, const float* res, int M, int N, int K, int act,
-                 int row_major = 0, int conv_l = -1) {
+                 int row_major = 0) {
   DecGemmArgs a{};
   a.Xt = Xt; a.ldx = c->ld_dec; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ldc;
   a.bias = bias;
   a.res = res; a.ldr = c->ld_dec; a.M = M; a.N = N; a.K = K; a.act = act; a.row_major = row_major;
-  if (conv_l >= 0) {
-    const LayerW& L = c->layers[conv_l];
-    a.conv_di = c->D.di;
-    a.conv_state = dec_conv_of(c, conv_l);
-    a.ld_state = c->ld_dec;
-    a.conv_w = L.conv_w;
-    a.conv_b = L.conv_b;
-    a.conv_out = c->dcvt;
-  }
   return timed(c, BOA_K_GEMM_SMALL, 2.0 * M * N * K, [&] { return dec_gemm(a, c->stream); });
 }
 
@@ -370,51 +350,62 @@ hipError_t ensure_state_layout(boa_ctx* c, int want_step) {
   return hipSuccess;
 }
 
-// One decode step for `lanes` lanes on features-major buffers (the mambav1
-// block of boa_gpu.hpp:834-843 and the head of :1048-1052); the causal conv
-// step runs in in_proj's epilogue.  Logits are written row-major [lane][256].
-hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias, float* logits) {
+// One decode step for lanes [lane0, lane0 + lanes) on the k-blocked buffers
+// (the mambav1 block of boa_gpu.hpp:834-843 and the head of :1048-1052),
+// ordered on stream s; layer 0's LN1 advances *t_counter.  The causal conv
+// step runs in in_proj's epilogue.  Logits are written row-major [lane][256]
+// (logits points at lane 0 of the range).  The state must be in step layout.
+hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
+                      const uint8_t* tok, bool add_bias, float* logits) {
   const Dims& D = c->D;
   const int ld = c->ld_dec;
-  hipStream_t s = c->stream;
-  hipError_t e = ensure_state_layout(c, 1);
-  if (e) return e;
-  for (int l = 0; l < D.L; ++l) {
+  const size_t a0 = (size_t)lane0 * 16;  // k-blocked activations
+  float *xt = c->dxt + a0, *xnt = c->dxnt + a0, *ot = c->dot + a0, *zt = c->dzt + a0,
+        *cvt = c->dcvt + a0, *rows = c->ddeltat + a0, *yt = c->dyt + a0, *hidt = c->dhidt + a0;
+  hipStream_t saved = c->stream;
+  c->stream = s;  // dgemm and timed() launch on c->stream
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < D.L && !e; ++l) {
     const LayerW& W = c->layers[l];
     const boa_ctx::DecW& DW = c->dlayers[l];
+    float* conv = dec_conv_of(c, l) + (size_t)lane0 * 4;
+    float* ssm = dec_ssm_of(c, l) + (size_t)lane0 * 64;
     e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
-      return launch_dec_ln1(l == 0 ? c->emb : nullptr, tok, c->dxt, c->dxnt, W.ln1_w, W.ln1_b,
-                            lanes, D.d, ld, l == 0 ? c->t_counter : nullptr, s);
+      return launch_dec_ln1(l == 0 ? c->emb : nullptr, tok, xt, xnt, W.ln1_w, W.ln1_b, lanes, D.d,
+                            ld, l == 0 ? t_counter : nullptr, s);
     });
-    if (e) return e;
-    if ((e = dgemm(c, c->dxnt, DW.w_in, c->dzt, ld, W.b_in, nullptr, lanes, 2 * D.di, D.d,
-                   ACT_NONE, 0, l)))
-      return e;
-    if ((e = dgemm(c, c->dcvt, DW.w_x, c->ddeltat, ld, nullptr, nullptr, lanes, c->n_xdec, D.di,
-                   ACT_NONE)))
-      return e;
-    e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
-      return launch_dec_scan(D, W, DW.na, DW.w_dt, c->dzt, c->dcvt, c->ddeltat, dec_ssm_of(c, l),
-                             c->dyt, lanes, ld, ld, s);
-    });
-    if (e) return e;
-    if ((e = dgemm(c, c->dyt, DW.w_out, c->dot, ld, W.b_out, nullptr, lanes, D.d, D.di,
-                   ACT_NONE)))
-      return e;
-    e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d,
-              [&] { return launch_dec_ln2(c->dot, c->dxnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
-    if (e) return e;
-    if ((e = dgemm(c, c->dxnt, DW.w1, c->dhidt, ld, W.b1, nullptr, lanes, 4 * D.d, D.d,
-                   ACT_GELU)))
-      return e;
-    if ((e = dgemm(c, c->dhidt, DW.w2, c->dxt, ld, W.b2, c->dxt, lanes, D.d, 4 * D.d,
-                   ACT_NONE)))
-      return e;
+    if (!e) {
+      DecGemmArgs a{};
+      a.Xt = xnt; a.ldx = ld; a.W = DW.w_in; a.ldw = 2 * D.di; a.C = zt; a.ldc = ld;
+      a.bias = W.b_in; a.M = lanes; a.N = 2 * D.di; a.K = D.d; a.act = ACT_NONE;
+      a.conv_di = D.di; a.conv_state = conv; a.ld_state = ld; a.conv_w = W.conv_w;
+      a.conv_b = W.conv_b; a.conv_out = cvt;
+      e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
+    }
+    if (!e) e = dgemm(c, cvt, DW.w_x, rows, ld, nullptr, nullptr, lanes, c->n_xdec, D.di, ACT_NONE);
+    if (!e)
+      e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
+        return launch_dec_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, s);
+      });
+    if (!e) e = dgemm(c, yt, DW.w_out, ot, ld, W.b_out, nullptr, lanes, D.d, D.di, ACT_NONE);
+    if (!e)
+      e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d,
+                [&] { return launch_dec_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
+    if (!e) e = dgemm(c, xnt, DW.w1, hidt, ld, W.b1, nullptr, lanes, 4 * D.d, D.d, ACT_GELU);
+    if (!e) e = dgemm(c, hidt, DW.w2, xt, ld, W.b2, xt, lanes, D.d, 4 * D.d, ACT_NONE);
   }
-  if ((e = dgemm(c, c->dxt, c->dhw1, c->dot, ld, c->hb1, nullptr, lanes, D.d, D.d, ACT_RELU)))
-    return e;
-  return dgemm(c, c->dot, c->dhw2, logits, VOCAB, add_bias ? c->hb2 : nullptr, nullptr,
-               lanes, VOCAB, D.d, ACT_NONE, 1);
+  if (!e) e = dgemm(c, xt, c->dhw1, ot, ld, c->hb1, nullptr, lanes, D.d, D.d, ACT_RELU);
+  if (!e)
+    e = dgemm(c, ot, c->dhw2, logits, VOCAB, add_bias ? c->hb2 : nullptr, nullptr, lanes, VOCAB,
+              D.d, ACT_NONE, 1);
+  c->stream = saved;
+  return e;
+}
+
+hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias, float* logits) {
+  hipError_t e = ensure_state_layout(c, 1);
+  if (e) return e;
+  return step_range(c, 0, lanes, c->stream, c->t_counter, tok, add_bias, logits);
 }
 
 int check_ready(boa_ctx* c) {
@@ -479,6 +470,66 @@ struct HostReader {
 
 }  // namespace
 
+namespace {
+
+// Steps 1 .. maxlen-1 of a batch.  Every step is the same launch sequence
+// (the step counter lives on the device), so it is captured once into a HIP
+// graph on the decode stream and replayed; the decode stream is ordered
+// after, and the context stream after it, by events.  With profiling on, the
+// steps are launched directly on the context stream.
+hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t chunk,
+                        const uint32_t* d_payload) {
+  hipStream_t s = c->stream;
+  auto one_step = [&](hipStream_t gs) -> hipError_t {
+    hipError_t e = step_range(c, 0, lanes, gs, c->t_counter, c->tok, false, c->dlogits);
+    if (e) return e;
+    hipStream_t saved = c->stream;
+    c->stream = gs;
+    e = timed(c, BOA_K_DECODE, 1024.0 * lanes, [&] {
+      return launch_decode_step(c->dlogits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter, out,
+                                chunk, c->dec, d_payload, c->offsets, c->sizes, lanes, gs);
+    });
+    c->stream = saved;
+    return e;
+  };
+  if (c->prof_on || maxlen <= 2) {
+    for (int t = 1; t < maxlen; ++t) {
+      hipError_t e = one_step(s);
+      if (e) return e;
+    }
+    return hipSuccess;
+  }
+  hipError_t e = hipSuccess;
+  if (!c->dec_stream) e = hipStreamCreateWithFlags(&c->dec_stream, hipStreamNonBlocking);
+  if (!e && !c->dec_fork) e = hipEventCreateWithFlags(&c->dec_fork, hipEventDisableTiming);
+  if (!e && !c->dec_join) e = hipEventCreateWithFlags(&c->dec_join, hipEventDisableTiming);
+  if (!e) e = hipEventRecord(c->dec_fork, s);
+  if (!e) e = hipStreamWaitEvent(c->dec_stream, c->dec_fork, 0);
+  if (e) return e;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  e = hipStreamBeginCapture(c->dec_stream, hipStreamCaptureModeThreadLocal);
+  if (!e) {
+    hipError_t le = one_step(c->dec_stream);
+    e = hipStreamEndCapture(c->dec_stream, &graph);
+    if (!e) e = le;
+  }
+  if (!e) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (graph) (void)hipGraphDestroy(graph);
+  for (int t = 1; t < maxlen && !e; ++t) e = hipGraphLaunch(exec, c->dec_stream);
+  hipError_t e2 = hipEventRecord(c->dec_join, c->dec_stream);
+  if (!e2) e2 = hipStreamWaitEvent(s, c->dec_join, 0);
+  // the executable graph is released only after its last replay finished
+  if (exec) {
+    hipError_t e3 = hipStreamSynchronize(c->dec_stream);
+    if (!e2) e2 = e3;
+    (void)hipGraphExecDestroy(exec);
+  }
+  return e ? e : e2;
+}
+
+}  // namespace
+
 // ================================================================ C ABI
 extern "C" {
 
@@ -494,7 +545,8 @@ int64_t boa_weight_file_bytes(int32_t d, int32_t L, int32_t ds, int32_t fp16) {
 int boa_create(const boa_config* cfg, boa_ctx** out) {
   if (!cfg || !out) return BOA_E_ARG;
   *out = nullptr;
-  if (cfg->d_model < 16 || cfg->d_model % 16 || cfg->d_model > 512 || cfg->n_layers < 1 ||
+  const int d = cfg->d_model;
+  if ((d != 64 && d != 128 && d != 256 && d != 512) || cfg->n_layers < 1 ||
       (cfg->d_state != 16 && cfg->d_state != 32) || cfg->max_lanes < 1 || cfg->max_lanes > 65535 ||
       cfg->precision != 0 || cfg->tile < 0)
     return BOA_E_ARG;
@@ -545,6 +597,9 @@ void boa_destroy(boa_ctx* c) {
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
   dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
   if (c->h_sizes) (void)hipHostFree(c->h_sizes);
+  if (c->dec_stream) (void)hipStreamDestroy(c->dec_stream);
+  if (c->dec_fork) (void)hipEventDestroy(c->dec_fork);
+  if (c->dec_join) (void)hipEventDestroy(c->dec_join);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -939,19 +994,10 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
                        c->lens, c->tok, out, chunk, lanes, c->t_counter);
     e = hipGetLastError();
     if (!e) e = launch_rc_dec_init(c->dec, d_payload, c->offsets, c->sizes, lanes, s);
+    if (!e) e = ensure_state_layout(c, 1);
     if (e) { dfree(d_first); return hip_fail(c, e, "decode init"); }
-    // The step kernel of layer 0 advances the device-side t counter, the
-    // decode kernel reads it: the sequence of launches is identical for
-    // every step (graph-capturable).
-    for (int32_t t = 1; t < maxlen; ++t) {
-      e = step_forward(c, c->tok, lanes, false, c->dlogits);
-      if (!e)
-        e = timed(c, BOA_K_DECODE, 1024.0 * lanes, [&] {
-          return launch_decode_step(c->dlogits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter,
-                                    out, chunk, c->dec, d_payload, c->offsets, c->sizes, lanes, s);
-        });
-      if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }
-    }
+    e = decode_steps(c, lanes, maxlen, out, chunk, d_payload);
+    if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }
     e = hipStreamSynchronize(s);
     if (e) { dfree(d_first); return hip_fail(c, e, "decode sync"); }
   }

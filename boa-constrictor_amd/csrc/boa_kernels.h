@@ -63,21 +63,14 @@ struct Dims {
 // written), which fuses the embedding lookup into layer 0's LN1.
 hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, float* xn,
                       const float* w, const float* b, int rows, int d, hipStream_t s);
-// Decode-step variant: token per lane from a device byte array.
-hipError_t launch_ln1_step(const float* emb, const uint8_t* tok, float* x, float* xn, const float* w,
-                           const float* b, int rows, int d, hipStream_t s, int* t_counter);
 // LayerNorm with sequential per-row sums (LN2 order), in place allowed.
 hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b, int rows, int d,
                       hipStream_t s);
 hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w, const float* cb,
                              float* out, int lanes, int T, int di, hipStream_t s);
-hipError_t launch_conv_step(const float* xz, float* conv_state, const float* w, const float* cb,
-                            float* out, int lanes, int di, hipStream_t s);
 hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
                              const float* delta, float* ssm_state, float* y, int lanes, int T,
                              hipStream_t s);
-hipError_t launch_scan_step(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
-                            const float* delta, float* ssm_state, float* y, int lanes, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
 // ---- decode step, features-major activations X^T[feature][lane] ----------

@@ -78,34 +78,12 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
   ln_halfwave_row(src, xc, xn + (size_t)row * d, w, b, d, l);
 }
 
-__global__ __launch_bounds__(256) void ln1_step_kernel(const float* __restrict__ emb,
-                                                       const uint8_t* tok, float* x, float* xn,
-                                                       const float* __restrict__ w,
-                                                       const float* __restrict__ b, int rows,
-                                                       int d, int* t_counter) {
-  if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
-  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
-  const int l = threadIdx.x & 31;
-  if (row >= rows) return;
-  const float* src = emb + (size_t)tok[row] * d;
-  ln_halfwave_row(src, x + (size_t)row * d, xn + (size_t)row * d, w, b, d, l);
-}
-
 hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, float* xn,
                       const float* w, const float* b, int rows, int d, hipStream_t s) {
   if (d > 32 * LN_MAXE) return hipErrorInvalidValue;
   int blocks = (rows + 7) / 8;
   hipLaunchKernelGGL(ln1_kernel, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T, t0, x, xn,
                      w, b, rows, d);
-  return hipGetLastError();
-}
-
-hipError_t launch_ln1_step(const float* emb, const uint8_t* tok, float* x, float* xn, const float* w,
-                           const float* b, int rows, int d, hipStream_t s, int* t_counter) {
-  if (d > 32 * LN_MAXE) return hipErrorInvalidValue;
-  int blocks = (rows + 7) / 8;
-  hipLaunchKernelGGL(ln1_step_kernel, dim3(blocks), dim3(256), 0, s, emb, tok, x, xn, w, b, rows, d,
-                     t_counter);
   return hipGetLastError();
 }
 
@@ -195,35 +173,11 @@ __global__ __launch_bounds__(256) void conv_chunk_kernel(const float* __restrict
   *st = make_float4(xm4, xm3, xm2, xm1);
 }
 
-__global__ __launch_bounds__(256) void conv_step_kernel(const float* __restrict__ xz,
-                                                        float* conv_state,
-                                                        const float* __restrict__ w,
-                                                        const float* __restrict__ cb, float* out,
-                                                        int lanes, int di) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= lanes * di) return;
-  const int c = idx % di, b = idx / di;
-  float4* st = reinterpret_cast<float4*>(conv_state) + idx;
-  float4 s0 = *st;
-  const float x0 = xz[(size_t)b * 2 * di + c];
-  const float4 wv = reinterpret_cast<const float4*>(w)[c];
-  out[idx] = conv_value(cb[c], s0.y, s0.z, s0.w, x0, wv);
-  *st = make_float4(s0.y, s0.z, s0.w, x0);
-}
-
 hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w, const float* cb,
                              float* out, int lanes, int T, int di, hipStream_t s) {
   int n = lanes * di;
   hipLaunchKernelGGL(conv_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xz, conv_state, w,
                      cb, out, lanes, T, di);
-  return hipGetLastError();
-}
-
-hipError_t launch_conv_step(const float* xz, float* conv_state, const float* w, const float* cb,
-                            float* out, int lanes, int di, hipStream_t s) {
-  int n = lanes * di;
-  hipLaunchKernelGGL(conv_step_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xz, conv_state, w,
-                     cb, out, lanes, di);
   return hipGetLastError();
 }
 
@@ -261,25 +215,6 @@ __global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
   scan_store<DS, RB>(sc, ssm);
 }
 
-template <int DS, int RB>
-__global__ __launch_bounds__(256) void scan_step_kernel(Dims D, LayerW Lw,
-                                                        const float* __restrict__ xz,
-                                                        const float* __restrict__ conv,
-                                                        const float* __restrict__ delta,
-                                                        float* ssm_state, float* y, int lanes) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  const int di = D.di;
-  if (idx >= lanes * di) return;
-  const int c = idx % di, b = idx / di;
-  float* ssm = ssm_state + (size_t)idx * DS;
-  ScanCtx<DS, RB> sc;
-  scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
-  const float* drow = delta + (size_t)b * D.R;
-  y[idx] = scan_token<DS, RB>(sc, drow, drow + D.r, D.r, conv[idx],
-                              xz[(size_t)b * 2 * di + di + c]);
-  scan_store<DS, RB>(sc, ssm);
-}
-
 static int block_for(int di) {
   for (int bs = 256; bs >= 32; bs >>= 1)
     if (di % bs == 0) return bs;
@@ -293,15 +228,6 @@ static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const float* xz
   const size_t lds = sizeof(float) * SCAN_TB * D.R;
   hipLaunchKernelGGL((scan_chunk_kernel<DS, RB>), dim3((lanes * D.di) / bs), dim3(bs), lds, s, D,
                      Lw, xz, conv, delta, ssm_state, y, lanes, T);
-  return hipGetLastError();
-}
-
-template <int DS, int RB>
-static hipError_t scan_step_go(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
-                               const float* delta, float* ssm_state, float* y, int lanes, int bs,
-                               hipStream_t s) {
-  hipLaunchKernelGGL((scan_step_kernel<DS, RB>), dim3((lanes * D.di) / bs), dim3(bs), 0, s, D, Lw,
-                     xz, conv, delta, ssm_state, y, lanes);
   return hipGetLastError();
 }
 
@@ -324,14 +250,6 @@ hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, c
   const int bs = block_for(D.di);
   if (!bs || D.r > RMAX || (D.ds != 16 && D.ds != 32)) return hipErrorInvalidValue;
   BOA_SCAN_DISPATCH(scan_chunk_go, D, Lw, xz, conv, delta, ssm_state, y, lanes, T, bs, s);
-}
-
-hipError_t launch_scan_step(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
-                            const float* delta, float* ssm_state, float* y, int lanes,
-                            hipStream_t s) {
-  const int bs = block_for(D.di);
-  if (!bs || D.r > RMAX || (D.ds != 16 && D.ds != 32)) return hipErrorInvalidValue;
-  BOA_SCAN_DISPATCH(scan_step_go, D, Lw, xz, conv, delta, ssm_state, y, lanes, bs, s);
 }
 
 // ------------------------------------------------------------------ misc

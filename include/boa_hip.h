@@ -42,7 +42,7 @@ typedef struct boa_ctx boa_ctx;
  * --temperature CLI state of boa.cpp:838-897.  d_conv = 4 and expand = 2 are
  * fixed as in the reference; dt_rank = ceil(d_model / 16). */
 typedef struct {
-    int32_t d_model;     /* multiple of 16, <= 512 */
+    int32_t d_model;     /* 64, 128, 256 or 512 */
     int32_t n_layers;
     int32_t d_state;     /* 16 or 32 (the reference supports 16 only) */
     int32_t max_lanes;   /* chunks processed in parallel (--gpu-batch) */
@@ -149,7 +149,7 @@ void boa_free(void* p);
 uint32_t boa_crc32(const uint8_t* data, int64_t n);
 
 /* ---- profiling: HIP events on the context stream ------------------------ */
-#define BOA_K_GEMM 0       /* GEMMs on the 128x128 tile (compress bulk) */
+#define BOA_K_GEMM 0       /* GEMMs on the 128x256 tile (compress bulk) */
 #define BOA_K_SCAN 1
 #define BOA_K_CONV 2
 #define BOA_K_LN 3

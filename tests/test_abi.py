@@ -28,6 +28,7 @@ def test_host_only_entry_points():
 def test_create_rejects_bad_configs():
     h = ctypes.c_void_p()
     for bad in [boa_hip.Config(250, 8, 16, 10, 0, 0, 1.0),   # d_model % 16
+                boa_hip.Config(80, 8, 16, 10, 0, 0, 1.0),    # d_model not a power of two
                 boa_hip.Config(256, 8, 24, 10, 0, 0, 1.0),   # d_state
                 boa_hip.Config(256, 8, 16, 0, 0, 0, 1.0),    # lanes
                 boa_hip.Config(256, 8, 16, 10, 0, 1, 1.0)]:  # precision
