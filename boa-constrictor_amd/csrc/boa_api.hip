@@ -1060,6 +1060,12 @@ int boa_decompress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, uint8_t** 
   if (!boa2_parse(h_in, (size_t)n, P, why)) return fail(c, BOA_E_FORMAT, why);
   if (P.hdr.flags & 1u) return fail(c, BOA_E_FORMAT, "warm-start containers are not supported");
   const size_t nc = P.hdr.n_chunks;
+  if (nc == 0) {  // empty input
+    *h_out = (uint8_t*)malloc(1);
+    if (!*h_out) return fail(c, BOA_E_NOMEM, "host allocation failed");
+    *out_len = 0;
+    return BOA_OK;
+  }
   // streams re-packed on 32-bit word boundaries
   std::vector<uint64_t> offs(std::max<size_t>(nc, 1)), lens(std::max<size_t>(nc, 1));
   uint64_t words = 0;

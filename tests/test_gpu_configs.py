@@ -1,0 +1,129 @@
+"""GPU parity across model shapes, weight formats, options and edge cases.
+
+Each case runs the HIP library through the C ABI and the CPU oracle on the
+same seeded inputs, and requires identical logit bits, identical BOA2 bytes
+and byte-identical round trips.  Shapes cover the BASELINE configs' models
+at reduced depth (C2 d256, C5 d512 with d_state 32) so the oracle finishes
+in seconds.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    return torch
+
+
+def _codec(d, L, ds=16, lanes=64, tile=0, w=None, temperature=1.0):
+    import boa_hip
+    import torch
+    c = boa_hip.Codec(d, L, ds, lanes, tile, temperature)
+    c.set_stream(torch.cuda.current_stream().cuda_stream)
+    if w is not None:
+        c.load_weights(w)
+    return c
+
+
+@pytest.mark.parametrize("d,L,ds", [(128, 1, 16), (256, 2, 16), (512, 1, 32)])
+def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
+    """Chunk-mode logits equal the oracle's; step-mode logits equal chunk mode."""
+    torch = torch_dev
+    w = make_weights(d, L, ds)
+    lanes, T = 5, 24
+    rng = np.random.default_rng(d + L + ds)
+    tok = rng.integers(0, 256, size=(lanes, T), dtype=np.uint8)
+    want = oracle.Model(w, d, L, ds).new_state(lanes).forward_chunk(tok)
+    c = _codec(d, L, ds, lanes=lanes, w=w)
+    c.reset_state(lanes)
+    d_log = torch.zeros(lanes * T * 256, dtype=torch.float32, device="cuda")
+    c.forward_chunk(torch.from_numpy(tok).cuda(), lanes, T, d_log)
+    torch.cuda.synchronize()
+    got = d_log.cpu().numpy().reshape(lanes, T, 256)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+        f"d={d} L={L} ds={ds}: max |diff| {np.abs(got - want).max()}"
+    c.reset_state(lanes)
+    d_s = torch.zeros(lanes * 256, dtype=torch.float32, device="cuda")
+    for t in range(T):
+        c.step_batch(torch.from_numpy(np.ascontiguousarray(tok[:, t])).cuda(), lanes, d_s, True)
+        st = d_s.cpu().numpy().reshape(lanes, 256)
+        assert np.array_equal(st.view(np.uint32), want[:, t].view(np.uint32)), f"step {t}"
+
+
+def _same_container(oracle, w, d, L, ds, data, chunk, lanes, tile=0, temperature=1.0,
+                    max_chunks=0):
+    m = oracle.Model(w, d, L, ds)
+    want = m.compress(data, chunk_size=chunk, tile=tile, max_chunks=max_chunks,
+                      temperature=temperature)
+    c = _codec(d, L, ds, lanes=lanes, tile=tile, w=w, temperature=temperature)
+    got = c.compress(data, chunk_size=chunk, max_chunks=max_chunks)
+    assert got == want, f"container differs ({len(got)} vs {len(want)} bytes)"
+    n = len(data) if max_chunks <= 0 else min(len(data), max_chunks * chunk)
+    assert c.decompress(got) == data[:n]
+    assert m.decompress(got, temperature=temperature) == data[:n]
+    return got
+
+
+def test_container_c2_shape(torch_dev, oracle, make_weights):
+    data = synth.gen_c2(4096)[:9 * 700 + 3]
+    _same_container(oracle, make_weights(256, 2), 256, 2, 16, data, 700, lanes=4)
+
+
+def test_container_c5_shape_d_state_32(torch_dev, oracle, make_weights):
+    data = synth.gen_c5(2048)[:5 * 512 + 77]
+    _same_container(oracle, make_weights(512, 1, 32), 512, 1, 32, data, 512, lanes=6)
+
+
+def test_container_markov_source(torch_dev, oracle, w_c1):
+    data = synth.gen_c4(8 * 1500)
+    _same_container(oracle, w_c1, 64, 2, 16, data, 1500, lanes=8)
+
+
+def test_container_fp16_weights(torch_dev, oracle, make_weights):
+    w16 = make_weights(64, 2, 16, seed=3, fp16=True)
+    data = synth.gen_c1()[:6 * 900]
+    _same_container(oracle, w16, 64, 2, 16, data, 900, lanes=6)
+
+
+def test_container_temperature(torch_dev, oracle, w_c1):
+    data = synth.gen_c1()[:5 * 800 + 5]
+    blob = _same_container(oracle, w_c1, 64, 2, 16, data, 800, lanes=8, temperature=0.7)
+    assert blob != oracle.Model(w_c1, 64, 2).compress(data, chunk_size=800)
+
+
+@pytest.mark.parametrize("n,chunk,lanes,max_chunks", [
+    (0, 512, 4, 0),          # empty input: header, empty index
+    (1, 512, 4, 0),          # one byte: one chunk, no coded symbols
+    (513, 512, 4, 0),        # last chunk of one byte
+    (7 * 300, 300, 3, 0),    # three batches of lanes
+    (10 * 256, 256, 4, 4),   # --max-chunks truncation
+])
+def test_container_edges(torch_dev, oracle, w_c1, n, chunk, lanes, max_chunks):
+    data = synth.gen_c1()[:n]
+    _same_container(oracle, w_c1, 64, 2, 16, data, chunk, lanes=lanes, max_chunks=max_chunks)
+
+
+def test_cli_round_trip_matches_oracle(torch_dev, oracle, w_c1, tmp_path):
+    """The C++ CLI (boa.cpp's command line) writes the oracle's container."""
+    exe = os.path.join(os.path.dirname(__file__), "..", "boa-constrictor_amd", "boa")
+    data = synth.gen_c1()[:12 * 1000 + 17]
+    src = tmp_path / "in.bin"
+    src.write_bytes(data)
+    boa_f = tmp_path / "out.boa"
+    back = tmp_path / "back.bin"
+    subprocess.run([exe, "compress", str(w_c1), str(src), str(boa_f), "64", "2",
+                    "--gpu-batch", "5", "--chunk-size", "1000"], check=True, timeout=120)
+    want = oracle.Model(w_c1, 64, 2).compress(data, chunk_size=1000)
+    assert boa_f.read_bytes() == want
+    subprocess.run([exe, "decompress", str(w_c1), str(boa_f), str(back), "64", "2",
+                    "--gpu-batch", "5"], check=True, timeout=120)
+    assert back.read_bytes() == data
