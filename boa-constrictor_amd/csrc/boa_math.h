@@ -26,14 +26,21 @@ namespace boa {
 BOA_DEV float u2f(uint32_t u) { return __uint_as_float(u); }
 BOA_DEV uint32_t f2u(float f) { return __float_as_uint(f); }
 
-BOA_DEV float expf_(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __builtin_huge_valf();
-  if (x < -87.0f) return 0.0f;
+// e^x and log(y) in two forms with identical results for every input:
+// expf_ / logf_ are branch-free (the arithmetic runs on a clamped or rescaled
+// argument and selects give the special values, so a wavefront never
+// diverges), expf_br / logf_br return early on special values.  2^k is
+// applied with ldexp, which is exact here as the product with 2^k is (for
+// k = 128 either form overflows alike).  Long per-element chains (the chunk
+// scan) run faster branch-free; latency-bound kernels (the decode step) run
+// faster with the early returns.
+
+// e^x for finite x in [-87, 88.7228...]
+BOA_DEV float exp_core(float x) {
   const float LOG2E = 1.44269504088896340736f;
   const float LN2_HI = 0.693147182464599609375f;
   const float LN2_LO = -1.904654323148236e-09f;
-  float kf = __builtin_rintf(x * LOG2E);
+  const float kf = __builtin_rintf(x * LOG2E);
   float r = __builtin_fmaf(-kf, LN2_HI, x);
   r = __builtin_fmaf(-kf, LN2_LO, r);
   float p = 1.98412698412698412698e-4f;
@@ -44,24 +51,32 @@ BOA_DEV float expf_(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int k = (int)kf;
-  if (k > 127) return (p * u2f((uint32_t)(127 + 127) << 23)) * 2.0f;
-  return p * u2f((uint32_t)(k + 127) << 23);
+  return __builtin_ldexpf(p, (int)kf);
 }
 
-BOA_DEV float logf_(float y) {
-  if (y != y) return y;
-  if (y == __builtin_huge_valf()) return y;
-  if (y <= 0.0f) return (y == 0.0f) ? -__builtin_huge_valf() : __builtin_nanf("");
-  uint32_t u = f2u(y);
-  int e = (int)(u >> 23) - 127;
-  if ((u >> 23) == 0) {
-    y = y * 8388608.0f;
-    u = f2u(y);
-    e = (int)(u >> 23) - 127 - 23;
-  }
+BOA_DEV float expf_(float x) {
+  float res = exp_core(__builtin_fminf(__builtin_fmaxf(x, -87.0f), 88.72283935546875f));
+  res = x < -87.0f ? 0.0f : res;
+  res = x > 88.72283935546875f ? __builtin_huge_valf() : res;
+  return x != x ? x : res;
+}
+
+BOA_DEV float expf_br(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return __builtin_huge_valf();
+  if (x < -87.0f) return 0.0f;
+  return exp_core(x);
+}
+
+// log(y) for y > 0 finite (subnormals rescaled)
+BOA_DEV float log_core(float y) {
+  const bool sub = (f2u(y) >> 23) == 0;
+  const uint32_t u = f2u(sub ? y * 8388608.0f : y);
+  int e = (int)(u >> 23) - 127 - (sub ? 23 : 0);
   float m = u2f((u & 0x007FFFFFu) | 0x3F800000u);
-  if (m > 1.41421353816986083984375f) { m = m * 0.5f; e += 1; }
+  const bool hi = m > 1.41421353816986083984375f;
+  m = hi ? m * 0.5f : m;
+  e = hi ? e + 1 : e;
   float s = (m - 1.0f) / (m + 1.0f);
   float s2 = s * s;
   float p = 0.0909090909090909090909f;
@@ -77,10 +92,28 @@ BOA_DEV float logf_(float y) {
   return __builtin_fmaf(ef, LN2_HI, __builtin_fmaf(ef, LN2_LO, lm));
 }
 
-// activations.hpp:33-84 (device branch)
-BOA_DEV float repro_exp(float x) {
-  if (x <= -88.0f) return 0.0f;
-  if (x >= 88.0f) x = 88.0f;
+BOA_DEV float logf_(float y) {
+  float res = log_core(y);
+  res = y == 0.0f ? -__builtin_huge_valf() : res;
+  res = y < 0.0f ? __builtin_nanf("") : res;
+  res = y == __builtin_huge_valf() ? y : res;
+  return y != y ? y : res;
+}
+
+BOA_DEV float logf_br(float y) {
+  if (y != y) return y;
+  if (y == __builtin_huge_valf()) return y;
+  if (y <= 0.0f) return (y == 0.0f) ? -__builtin_huge_valf() : __builtin_nanf("");
+  return log_core(y);
+}
+
+template <bool BR>
+BOA_DEV float exp_sel(float x) { return BR ? expf_br(x) : expf_(x); }
+template <bool BR>
+BOA_DEV float log_sel(float x) { return BR ? logf_br(x) : logf_(x); }
+
+// activations.hpp:33-84 (device branch); core for x in [-88, 88]
+BOA_DEV float repro_exp_core(float x) {
   float kf = __builtin_floorf(x * 1.44269504088896340736f + 0.5f);
   int k = (int)kf;
   float r = x + (-(kf * 0.69314718055994530942f));
@@ -93,29 +126,44 @@ BOA_DEV float repro_exp(float x) {
   return t * u2f((uint32_t)((k + 127) << 23));
 }
 
+template <bool BR>
+BOA_DEV float repro_exp(float x) {
+  if (BR) {
+    if (x <= -88.0f) return 0.0f;
+    return repro_exp_core(x >= 88.0f ? 88.0f : x);
+  }
+  const float res = repro_exp_core(__builtin_fminf(__builtin_fmaxf(x, -88.0f), 88.0f));
+  return x <= -88.0f ? 0.0f : (x != x ? x : res);
+}
+
 // activations.hpp:87-98
+template <bool BR>
 BOA_DEV float repro_tanh(float x) {
-  float ax = x < 0.0f ? -x : x;
-  if (ax > 10.0f) return (x > 0.0f) ? 1.0f : -1.0f;
-  float e2x = repro_exp(2.0f * x);
-  return (e2x + -1.0f) / (e2x + 1.0f);
+  const float ax = x < 0.0f ? -x : x;
+  if (BR && ax > 10.0f) return (x > 0.0f) ? 1.0f : -1.0f;
+  const float e2x = repro_exp<BR>(2.0f * x);
+  const float th = (e2x + -1.0f) / (e2x + 1.0f);
+  return ax > 10.0f ? ((x > 0.0f) ? 1.0f : -1.0f) : th;
 }
 
 // activations.hpp:105-117 (tanh GELU used by the FF epilogue)
+template <bool BR = false>
 BOA_DEV float gelu(float x) {
   float cube = (x * x) * x;
   float inner = 0.79788456080286535588f * (x + 0.044715f * cube);
-  float th = repro_tanh(inner);
+  float th = repro_tanh<BR>(inner);
   return 0.5f * (x * (1.0f + th));
 }
 
 // SiLU in the form v * (1 / (1 + exp(-v))) (mamba_kernels.cu:188-189)
+template <bool BR = false>
 BOA_DEV float silu(float x) {
-  float sg = 1.0f / (1.0f + expf_(-x));
+  float sg = 1.0f / (1.0f + exp_sel<BR>(-x));
   return x * sg;
 }
 
 // unthresholded softplus log(1 + exp(x)) (inference_kernels.cu:376-382)
-BOA_DEV float softplus(float x) { return logf_(1.0f + expf_(x)); }
+template <bool BR = false>
+BOA_DEV float softplus(float x) { return log_sel<BR>(1.0f + exp_sel<BR>(x)); }
 
 }  // namespace boa
