@@ -109,8 +109,10 @@ def _ptr(x):
 class Codec:
     """One context: weights, recurrent state and work buffers on one GPU."""
 
-    def __init__(self, d_model, n_layers, d_state=16, max_lanes=64, tile=0, temperature=1.0):
-        self.cfg = Config(d_model, n_layers, d_state, max_lanes, tile, 0, temperature)
+    def __init__(self, d_model, n_layers, d_state=16, max_lanes=64, tile=0, temperature=1.0,
+                 precision="fp32"):
+        prec = {"fp32": 0, "bf16": 1}[precision]
+        self.cfg = Config(d_model, n_layers, d_state, max_lanes, tile, prec, temperature)
         h = C.c_void_p()
         rc = lib().boa_create(C.byref(self.cfg), C.byref(h))
         if rc != BOA_OK:

@@ -26,6 +26,20 @@ __device__ __forceinline__ float conv_step_value(float bias, float4 s, float x0,
   return conv_value<BR>(bias, s.y, s.z, s.w, x0, w);
 }
 
+// Decode-step activation layouts, lane capacity ld:
+//   fp32 "k-blocked": feature k of lane m at ((k/16) ld + m) 16 + dperm(k%16),
+//     dperm(j) = 4 (j%4) + j/4 (a 4x4 transpose, its own inverse), so that the
+//     four k-steps of a 16x16x4 MFMA operand are one float4 of the lane;
+//   bf16 "32-blocked": feature k of lane m at ((k/32) ld + m) 32 + k%32, so
+//     that the 8 k of a 16x16x32 bf16 MFMA operand slot group are 16 bytes.
+__device__ __forceinline__ int dperm(int j) { return ((j & 3) << 2) | ((j >> 2) & 3); }
+__device__ __forceinline__ size_t dblk(int k, int m, int ld) {
+  return ((size_t)(k >> 4) * ld + m) * 16 + dperm(k & 15);
+}
+__device__ __forceinline__ size_t dblk32(int k, int m, int ld) {
+  return ((size_t)(k >> 5) * ld + m) * 32 + (k & 31);
+}
+
 constexpr int RMAX = 32;  // dt_rank <= 32 (d_model <= 512)
 constexpr int SCAN_TB = 32;  // timesteps of delta rows staged in LDS per pass
 

@@ -48,6 +48,7 @@ struct boa_ctx {
   float inv_temp = 1.0f;
 
   // weights (one device allocation)
+  bool bf16 = false;  // precision 1: bf16 weights and activations
   float* wbuf = nullptr;
   const float* emb = nullptr;
   const float *hw1 = nullptr, *hb1 = nullptr, *hw2 = nullptr, *hb2 = nullptr;
@@ -68,6 +69,14 @@ struct boa_ctx {
   int n_xdec = 0;  // decode x_proj width: dec_rb(r) + 2 ds
   float* dwbuf = nullptr;
   std::vector<DecW> dlayers;
+  // bf16 precision: Linear weights in bf16 for the compress GEMM ([N_pad][K])
+  // and the decode GEMM (32-blocked), one allocation
+  struct B16W {
+    const uint16_t *w_in, *w_x, *w_out, *w1, *w2;
+  };
+  uint16_t* b16buf = nullptr;
+  std::vector<B16W> b16c, b16d;
+  const uint16_t *b16c_h1 = nullptr, *b16c_h2 = nullptr, *b16d_h1 = nullptr, *b16d_h2 = nullptr;
   const float *dhw1 = nullptr, *dhw2 = nullptr;
   int ld_dec = 0;
   float* dec_conv = nullptr;
@@ -242,6 +251,58 @@ hipError_t gemm(boa_ctx* c, const float* X, int ldx, const float* W, int ldw, fl
   return timed(c, cls, 2.0 * M * N * K, [&] { return gemm_f32(a, c->stream); });
 }
 
+// bf16 GEMM of the compress pass: X bf16 [M][K], W bf16 [N_pad][K].
+hipError_t gemmb(boa_ctx* c, const void* X, const uint16_t* W, void* C, int ldc, bool c_bf16,
+                 uint16_t* C2, const float* bias, const float* res, int ldr, int M, int N, int K,
+                 int act) {
+  GemmB16Args a{(const uint16_t*)X, K, W, K, C, ldc, c_bf16 ? 1 : 0, C2, bias, res, ldr, M, N, K,
+                act};
+  const int cls = N >= 256 ? BOA_K_GEMM : BOA_K_GEMM_SMALL;
+  return timed(c, cls, 2.0 * M * N * K, [&] { return gemm_bf16(a, c->stream); });
+}
+
+// bf16 block (precision 1): the fp32 block's sequence with bf16 activations
+// (xn, xz, conv, delta, y, out_proj output, hid) and fp32 x; the last layer's
+// FF2 also stores a bf16 copy of x (into y's buffer) for head1.
+hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, const TokenSrc& tok0,
+                             int t0) {
+  const Dims& D = c->D;
+  const LayerW W = layer_at(c, l);
+  const boa_ctx::B16W& B = c->b16c[l];
+  hipStream_t s = c->stream;
+  const double ln_bytes = 3.0 * 4 * rows * D.d;
+  hipError_t e = timed(c, BOA_K_LN, ln_bytes, [&] {
+    return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, true, s)
+                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
+                               W.ln1_b, rows, D.d, true, s);
+  });
+  if (!e) e = gemmb(c, c->xn, B.w_in, c->xz, 2 * D.di, true, nullptr, W.b_in, nullptr, 0, rows,
+                    2 * D.di, D.d, ACT_NONE);
+  if (!e)
+    e = timed(c, BOA_K_CONV, 2.0 * rows * D.di * 2, [&] {
+      return launch_conv_chunk(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes, T,
+                               D.di, true, s);
+    });
+  if (!e) e = gemmb(c, c->cv, B.w_x, c->delta, D.R, true, nullptr, nullptr, nullptr, 0, rows, D.R,
+                    D.di, ACT_NONE);
+  if (!e)
+    e = timed(c, BOA_K_SCAN, 2.0 * rows * (3.0 * D.di + D.R), [&] {
+      return launch_scan_chunk(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes, T,
+                               true, s);
+    });
+  if (!e) e = gemmb(c, c->y, B.w_out, c->xn, D.d, true, nullptr, W.b_out, nullptr, 0, rows, D.d,
+                    D.di, ACT_NONE);
+  if (!e)
+    e = timed(c, BOA_K_LN, 2.0 * 2 * rows * D.d,
+              [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, true, s); });
+  if (!e) e = gemmb(c, c->xn, B.w1, c->hid, 4 * D.d, true, nullptr, W.b1, nullptr, 0, rows, 4 * D.d,
+                    D.d, ACT_GELU);
+  if (!e)
+    e = gemmb(c, c->hid, B.w2, c->x, D.d, false, l == D.L - 1 ? (uint16_t*)c->y : nullptr, W.b2,
+              c->x, D.d, rows, D.d, 4 * D.d, ACT_NONE);
+  return e;
+}
+
 // One mambav1 block on `rows` = lanes x T rows (boa_gpu.hpp:895-902):
 // res = x; x = LN1(x); x = Mamba(x); x = LN2(x); x = FF(x) + res.
 // x keeps the residual, LN1 writes xn, out_proj writes xn.
@@ -253,9 +314,10 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
   hipError_t e;
   const double ln_bytes = 3.0 * 4 * rows * D.d;
   e = timed(c, BOA_K_LN, ln_bytes, [&] {
-    return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, s)
+    return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
+                               false, s)
                   : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
-                               W.ln1_b, rows, D.d, s);
+                               W.ln1_b, rows, D.d, false, s);
   });
   if (e) return e;
   if ((e = gemm(c, c->xn, D.d, W.w_in, D.ld_in, c->xz, 2 * D.di, W.b_in, nullptr, 0, rows,
@@ -264,7 +326,7 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
   const double conv_bytes = 4.0 * rows * D.di * 2;
   e = timed(c, BOA_K_CONV, conv_bytes, [&] {
     return launch_conv_chunk(c->xz, conv_state_of(c, l), W.conv_w, W.conv_b, c->cv, lanes, T,
-                             D.di, s);
+                             D.di, false, s);
   });
   if (e) return e;
   if ((e = gemm(c, c->cv, D.di, W.w_x, D.ld_x, c->delta, D.R, nullptr, nullptr, 0, rows, D.R, D.di,
@@ -273,14 +335,15 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
   // algorithmic bytes: u, z, y per element, the delta row per token
   const double scan_bytes = 4.0 * rows * (3.0 * D.di + D.R);
   e = timed(c, BOA_K_SCAN, scan_bytes, [&] {
-    return launch_scan_chunk(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes, T, s);
+    return launch_scan_chunk(D, W, c->xz, c->cv, c->delta, ssm_state_of(c, l), c->y, lanes, T,
+                             false, s);
   });
   if (e) return e;
   if ((e = gemm(c, c->y, D.di, W.w_out, D.ld_out, c->xn, D.d, W.b_out, nullptr, 0, rows, D.d, D.di,
                 ACT_NONE)))
     return e;
   e = timed(c, BOA_K_LN, ln_bytes,
-            [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, s); });
+            [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, false, s); });
   if (e) return e;
   if ((e = gemm(c, c->xn, D.d, W.w1, D.ld_1, c->hid, 4 * D.d, W.b1, nullptr, 0, rows, 4 * D.d, D.d,
                 ACT_GELU)))
@@ -291,6 +354,13 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
 
 hipError_t head_forward(boa_ctx* c, int rows, bool add_bias, float* logits) {
   const Dims& D = c->D;
+  if (c->bf16) {  // head1 reads the bf16 copy of x stored in y's buffer
+    hipError_t e = gemmb(c, c->y, c->b16c_h1, c->xn, D.d, true, nullptr, c->hb1, nullptr, 0, rows,
+                         D.d, D.d, ACT_RELU);
+    if (e) return e;
+    return gemmb(c, c->xn, c->b16c_h2, logits, VOCAB, false, nullptr, add_bias ? c->hb2 : nullptr,
+                 nullptr, 0, rows, VOCAB, D.d, ACT_NONE);
+  }
   hipError_t e = gemm(c, c->x, D.d, c->hw1, D.ld_h1, c->xn, D.d, c->hb1, nullptr, 0, rows, D.d, D.d,
                       ACT_RELU);
   if (e) return e;
@@ -305,7 +375,8 @@ hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t
   hipError_t es = ensure_state_layout(c, 0);
   if (es) return es;
   for (int l = 0; l < c->D.L; ++l) {
-    hipError_t e = block_forward(c, l, rows, lanes, T, tok, t0);
+    hipError_t e = c->bf16 ? block_forward_b16(c, l, rows, lanes, T, tok, t0)
+                           : block_forward(c, l, rows, lanes, T, tok, t0);
     if (e) return e;
   }
   return head_forward(c, rows, true, logits);
@@ -355,8 +426,12 @@ hipError_t ensure_state_layout(boa_ctx* c, int want_step) {
 // ordered on stream s; layer 0's LN1 advances *t_counter.  The causal conv
 // step runs in in_proj's epilogue.  Logits are written row-major [lane][256]
 // (logits points at lane 0 of the range).  The state must be in step layout.
+hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
+                          const uint8_t* tok, bool add_bias, float* logits);
+
 hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
                       const uint8_t* tok, bool add_bias, float* logits) {
+  if (c->bf16) return step_range_b16(c, lane0, lanes, s, t_counter, tok, add_bias, logits);
   const Dims& D = c->D;
   const int ld = c->ld_dec;
   const size_t a0 = (size_t)lane0 * 16;  // k-blocked activations
@@ -399,6 +474,72 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     e = dgemm(c, ot, c->dhw2, logits, VOCAB, add_bias ? c->hb2 : nullptr, nullptr, lanes, VOCAB,
               D.d, ACT_NONE, 1);
   c->stream = saved;
+  return e;
+}
+
+// bf16 decode step: bf16 32-blocked activations, fp32 k-blocked x; the
+// last layer's FF2 also writes x in bf16 (into y's buffer) for head1.
+hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
+                          const uint8_t* tok, bool add_bias, float* logits) {
+  const Dims& D = c->D;
+  const int ld = c->ld_dec;
+  const size_t a0 = (size_t)lane0 * 32;  // bf16 32-blocked activations
+  float* xt = c->dxt + (size_t)lane0 * 16;
+  uint16_t *xnt = (uint16_t*)c->dxnt + a0, *ot = (uint16_t*)c->dot + a0,
+           *zt = (uint16_t*)c->dzt + a0, *cvt = (uint16_t*)c->dcvt + a0,
+           *rows = (uint16_t*)c->ddeltat + a0, *yt = (uint16_t*)c->dyt + a0,
+           *hidt = (uint16_t*)c->dhidt + a0;
+  auto g = [&](const uint16_t* X, const uint16_t* W, int N, int K, void* C, int mode,
+               const float* bias, int act) {
+    DecB16Args a{};
+    a.X = X; a.ldx = ld; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ld;
+    a.out_mode = mode; a.bias = bias; a.M = lanes; a.N = N; a.K = K; a.act = act;
+    return a;
+  };
+  auto run = [&](const DecB16Args& a) {
+    return timed(c, BOA_K_GEMM_SMALL, 2.0 * a.M * a.N * a.K, [&] { return dec_b16_gemm(a, s); });
+  };
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < D.L && !e; ++l) {
+    const LayerW& W = c->layers[l];
+    const boa_ctx::DecW& DW = c->dlayers[l];
+    const boa_ctx::B16W& B = c->b16d[l];
+    float* conv = dec_conv_of(c, l) + (size_t)lane0 * 4;
+    float* ssm = dec_ssm_of(c, l) + (size_t)lane0 * 64;
+    e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
+      return launch_dec_b16_ln1(l == 0 ? c->emb : nullptr, tok, xt, xnt, W.ln1_w, W.ln1_b, lanes,
+                                D.d, ld, l == 0 ? t_counter : nullptr, s);
+    });
+    if (!e) {
+      DecB16Args a = g(xnt, B.w_in, 2 * D.di, D.d, zt, DEC_OUT_B16, W.b_in, ACT_NONE);
+      a.conv_di = D.di; a.conv_state = conv; a.ld_state = ld; a.conv_w = W.conv_w;
+      a.conv_b = W.conv_b; a.conv_out = cvt;
+      e = run(a);
+    }
+    if (!e) e = run(g(cvt, B.w_x, c->n_xdec, D.di, rows, DEC_OUT_B16, nullptr, ACT_NONE));
+    if (!e)
+      e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 2.0 * lanes * (3.0 * D.di + D.R), [&] {
+        return launch_dec_b16_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, s);
+      });
+    if (!e) e = run(g(yt, B.w_out, D.d, D.di, ot, DEC_OUT_B16, W.b_out, ACT_NONE));
+    if (!e)
+      e = timed(c, BOA_K_LN, 2.0 * 2 * lanes * D.d,
+                [&] { return launch_dec_b16_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
+    if (!e) e = run(g(xnt, B.w1, 4 * D.d, D.d, hidt, DEC_OUT_B16, W.b1, ACT_GELU));
+    if (!e) {
+      DecB16Args a = g(hidt, B.w2, D.d, 4 * D.d, xt, DEC_OUT_F32, W.b2, ACT_NONE);
+      a.res = xt; a.ldr = ld;
+      if (l == D.L - 1) a.C2 = yt;
+      e = run(a);
+    }
+  }
+  if (!e) e = run(g(yt, c->b16d_h1, D.d, D.d, ot, DEC_OUT_B16, c->hb1, ACT_RELU));
+  if (!e) {
+    DecB16Args a = g(ot, c->b16d_h2, VOCAB, D.d, logits, DEC_OUT_ROWMAJOR,
+                     add_bias ? c->hb2 : nullptr, ACT_NONE);
+    a.ldc = VOCAB;
+    e = run(a);
+  }
   return e;
 }
 
@@ -548,7 +689,7 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
   const int d = cfg->d_model;
   if ((d != 64 && d != 128 && d != 256 && d != 512) || cfg->n_layers < 1 ||
       (cfg->d_state != 16 && cfg->d_state != 32) || cfg->max_lanes < 1 || cfg->max_lanes > 65535 ||
-      cfg->precision != 0 || cfg->tile < 0)
+      (cfg->precision != 0 && cfg->precision != 1) || cfg->tile < 0)
     return BOA_E_ARG;
   boa_ctx* c = new boa_ctx();
   c->cfg = *cfg;
@@ -560,6 +701,7 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
   c->stream = c->own_stream;
   const Dims& D = c->D;
   const size_t L = D.L, B = cfg->max_lanes;
+  c->bf16 = cfg->precision == 1;
   c->ld_dec = (int)round_up(cfg->max_lanes, 64);
   c->n_xdec = dec_rb(D.r) + 2 * D.ds;
   const size_t ldd = c->ld_dec;
@@ -587,7 +729,7 @@ void boa_destroy(boa_ctx* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   prof_flush(c);
   for (hipEvent_t e : c->ev_pool) (void)hipEventDestroy(e);
-  dfree(c->wbuf); dfree(c->dwbuf);
+  dfree(c->wbuf); dfree(c->dwbuf); dfree(c->b16buf);
   dfree(c->conv_state); dfree(c->ssm_state);
   dfree(c->dec_conv); dfree(c->dec_ssm);
   dfree(c->dxt); dfree(c->dxnt); dfree(c->dot); dfree(c->dzt); dfree(c->dcvt); dfree(c->ddeltat);
@@ -781,6 +923,54 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
                                       D.ds, D.di, c->stream));
     c->dlayers[l].w_dt = wq;
     c->dlayers[l].na = nq;
+  }
+  if (c->bf16) {  // bf16 copies of the Linear weights: compress [N_pad][K], decode 32-blocked
+    struct B16Part {
+      const float* src;
+      int ldw_in, n_src, K, N, zs, ze;
+      const uint16_t** cdst;
+      const uint16_t** ddst;
+    };
+    std::vector<B16Part> bp;
+    c->b16c.assign(D.L, boa_ctx::B16W{});
+    c->b16d.assign(D.L, boa_ctx::B16W{});
+    for (int l = 0; l < D.L; ++l) {
+      const LayerW& L = c->layers[l];
+      boa_ctx::B16W &C_ = c->b16c[l], &D_ = c->b16d[l];
+      bp.push_back({L.w_in, D.ld_in, 2 * D.di, D.d, 2 * D.di, 0, 0, &C_.w_in, &D_.w_in});
+      bp.push_back({L.w_x, D.ld_x, D.R, D.di, D.R, 0, 0, &C_.w_x, nullptr});
+      bp.push_back({L.w_x, D.ld_x, D.R, D.di, c->n_xdec, D.r, rb, nullptr, &D_.w_x});
+      bp.push_back({L.w_out, D.ld_out, D.d, D.di, D.d, 0, 0, &C_.w_out, &D_.w_out});
+      bp.push_back({L.w1, D.ld_1, 4 * D.d, D.d, 4 * D.d, 0, 0, &C_.w1, &D_.w1});
+      bp.push_back({L.w2, D.ld_2, D.d, 4 * D.d, D.d, 0, 0, &C_.w2, &D_.w2});
+    }
+    bp.push_back({c->hw1, D.ld_h1, D.d, D.d, D.d, 0, 0, &c->b16c_h1, &c->b16d_h1});
+    bp.push_back({c->hw2, D.ld_h2, VOCAB, D.d, VOCAB, 0, 0, &c->b16c_h2, &c->b16d_h2});
+    size_t btotal = 0;
+    std::vector<size_t> coff(bp.size()), doff2(bp.size());
+    for (size_t i = 0; i < bp.size(); ++i) {
+      const B16Part& q = bp[i];
+      coff[i] = btotal;
+      if (q.cdst) btotal += (size_t)round_up(q.N, 256) * q.K;
+      doff2[i] = btotal;
+      if (q.ddst) btotal += (size_t)q.K * round_up(q.N, 16);
+    }
+    dfree(c->b16buf);
+    c->b16buf = nullptr;
+    if (dalloc(&c->b16buf, btotal)) return fail(c, BOA_E_NOMEM, "device allocation of weights failed");
+    for (size_t i = 0; i < bp.size(); ++i) {
+      const B16Part& q = bp[i];
+      if (q.cdst) {
+        HIP_TRY(c, launch_b16_weight_nk(q.src, q.ldw_in, q.n_src, q.K, (int)round_up(q.N, 256),
+                                        c->b16buf + coff[i], c->stream));
+        *q.cdst = c->b16buf + coff[i];
+      }
+      if (q.ddst) {
+        HIP_TRY(c, launch_dec_b16_weight(q.src, q.ldw_in, q.n_src, c->b16buf + doff2[i], q.K,
+                                         (int)round_up(q.N, 16), q.zs, q.ze, c->stream));
+        *q.ddst = c->b16buf + doff2[i];
+      }
+    }
   }
   HIP_TRY(c, hipStreamSynchronize(c->stream));
   c->loaded = true;

@@ -5,7 +5,7 @@
 //   boa <compress|decompress> <model.bin> <input> <output> [d_model=256]
 //       [n_layers=1] [--gpu-batch B] [--max-chunks C] [--chunk-size S]
 //       [--tile T] [--temperature T] [--backbone mamba] [--show-timings]
-//       [--no-graph] [--d-state N] [--precision fp32]
+//       [--no-graph] [--d-state N] [--precision fp32|bf16]
 // --gpu-batch 0 (default) sizes the batch from free device memory like
 // auto_size_params (boa.cpp:109-156).  --warm-start is rejected (see the
 // design notes); --measure-energy is not provided.
@@ -24,7 +24,7 @@ static int usage() {
   fprintf(stderr,
           "Usage: boa <compress|decompress> <model> <input> <output> [d_model] [n_layers] "
           "[--gpu-batch B] [--max-chunks C] [--chunk-size S] [--tile T] [--temperature T] "
-          "[--d-state N] [--precision fp32] [--show-timings]\n");
+          "[--d-state N] [--precision fp32|bf16] [--show-timings]\n");
   return 1;
 }
 
@@ -56,7 +56,7 @@ static int auto_batch(boa_config cfg, int64_t chunk, bool compress) {
 int main(int argc, char** argv) {
   if (argc < 5) return usage();
   std::vector<std::string> args;
-  int gpu_batch = 0, max_chunks = -1, tile = 0, d_state = 16;
+  int gpu_batch = 0, max_chunks = -1, tile = 0, d_state = 16, precision = 0;
   long long chunk = 4096;
   float temperature = 1.0f;
   bool show_timings = false;
@@ -74,7 +74,9 @@ int main(int argc, char** argv) {
     else if (s == "--d-state") d_state = atoi(next("--d-state"));
     else if (s == "--precision") {
       std::string p = next("--precision");
-      if (p != "fp32") { fprintf(stderr, "precision %s is not supported\n", p.c_str()); return 1; }
+      if (p == "fp32") precision = 0;
+      else if (p == "bf16") precision = 1;
+      else { fprintf(stderr, "precision %s is not supported\n", p.c_str()); return 1; }
     } else if (s == "--backbone") {
       std::string b = next("--backbone");
       if (b != "mamba" && b != "mambav1") {
@@ -96,7 +98,7 @@ int main(int argc, char** argv) {
   cfg.n_layers = args.size() > 5 ? atoi(args[5].c_str()) : 1;
   cfg.d_state = d_state;
   cfg.tile = tile;
-  cfg.precision = 0;
+  cfg.precision = precision;
   cfg.temperature = temperature;
   if (chunk <= 0) chunk = 4096;
   const bool compress = mode == "compress";

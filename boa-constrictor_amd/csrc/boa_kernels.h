@@ -61,16 +61,35 @@ struct Dims {
 // LayerNorm of rows with the reference's 32-lane tree reduction order; when
 // `tok` is set, row b*T+t is first filled from the embedding table (and x is
 // written), which fuses the embedding lookup into layer 0's LN1.
-hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, float* xn,
-                      const float* w, const float* b, int rows, int d, hipStream_t s);
+// bf16 GEMM (precision 1): X bf16 [M][ldx], W bf16 [N_pad][ldw] (k contiguous,
+// N_pad = round_up(N, 256), zero rows), fp32 accumulation and epilogue; C is
+// fp32 or bf16 (c_bf16), C2 an optional bf16 copy of C, res an fp32 residual.
+struct GemmB16Args {
+  const uint16_t* X; int ldx;
+  const uint16_t* W; int ldw;
+  void* C; int ldc; int c_bf16;
+  uint16_t* C2;
+  const float* bias;
+  const float* res; int ldr;
+  int M, N, K, act;
+};
+hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s);
+hipError_t gemm_bf16_sweep(int cfg, const GemmB16Args& a, hipStream_t s);
+hipError_t launch_b16_weight_nk(const float* w, int ldw_in, int N, int K, int n_pad, uint16_t* out,
+                                hipStream_t s);
+
+// Activations other than the residual stream x are fp32, or bf16 (uint16_t)
+// when `bf16` is set; x and the recurrent state are always fp32.
+hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, void* xn,
+                      const float* w, const float* b, int rows, int d, bool bf16, hipStream_t s);
 // LayerNorm with sequential per-row sums (LN2 order), in place allowed.
-hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b, int rows, int d,
-                      hipStream_t s);
-hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w, const float* cb,
-                             float* out, int lanes, int T, int di, hipStream_t s);
-hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
-                             const float* delta, float* ssm_state, float* y, int lanes, int T,
-                             hipStream_t s);
+hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, int rows, int d,
+                      bool bf16, hipStream_t s);
+hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, const float* cb,
+                             void* out, int lanes, int T, int di, bool bf16, hipStream_t s);
+hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const void* xz, const void* conv,
+                             const void* delta, float* ssm_state, void* y, int lanes, int T,
+                             bool bf16, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 
 // ---- decode step, features-major activations X^T[feature][lane] ----------
@@ -107,6 +126,35 @@ hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const flo
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
                            const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
                            int M, int ld, int ld_state, hipStream_t s);
+// ---- decode step, bf16 precision (decode_bf16.hip) ----------------------
+// Activations bf16 in the 32-blocked layout (feature k of lane m at
+// ((k/32) ld + m) 32 + k%32), the residual stream fp32 k-blocked.
+enum { DEC_OUT_B16 = 0, DEC_OUT_F32 = 1, DEC_OUT_ROWMAJOR = 2 };
+struct DecB16Args {
+  const uint16_t* X; int ldx;   // bf16 32-blocked activations
+  const uint16_t* W; int ldw;   // bf16 32-blocked weights, ldw >= round_up(N, 16)
+  void* C; int ldc; int out_mode;
+  uint16_t* C2;                 // DEC_OUT_F32: optional bf16 32-blocked copy of C
+  const float* bias;
+  const float* res; int ldr;    // DEC_OUT_F32: fp32 k-blocked residual
+  int M, N, K, act;
+  int conv_di;                  // DEC_OUT_B16 in_proj: the conv step on features < conv_di
+  float* conv_state; int ld_state;
+  const float* conv_w; const float* conv_b; uint16_t* conv_out;
+};
+hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s);
+hipError_t launch_dec_b16_weight(const float* w, int ldw_in, int n_src, uint16_t* out, int K,
+                                 int ldn, int zs, int ze, hipStream_t s);
+hipError_t launch_dec_b16_ln1(const float* emb, const uint8_t* tok, float* xt, uint16_t* xnt,
+                              const float* w, const float* b, int M, int d, int ld, int* t_counter,
+                              hipStream_t s);
+hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w, const float* b,
+                              int M, int d, int ld, hipStream_t s);
+hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
+                               const float* wdt_q, const uint16_t* zt, const uint16_t* cvt,
+                               const uint16_t* rows, float* ssm, uint16_t* yt, int M, int ld,
+                               int ld_state, hipStream_t s);
+
 // chunk layout: conv [lane][c][4], ssm [lane][c][n]; step layout: conv
 // [c][lane][4], ssm [c/16][n/4][lane][c%16][n%4] with lane stride ld_state.
 hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, float* conv_out,

@@ -26,6 +26,22 @@ namespace boa {
 BOA_DEV float u2f(uint32_t u) { return __uint_as_float(u); }
 BOA_DEV uint32_t f2u(float f) { return __float_as_uint(f); }
 
+// bfloat16 storage (uint16_t): the upper half of a float32, rounded to
+// nearest even; a NaN stays a quiet NaN.
+BOA_DEV uint16_t f32_to_bf16(float x) {
+  const uint32_t u = f2u(x);
+  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)(((u & 0x7FFFFFFFu) > 0x7F800000u) ? ((u >> 16) | 0x40u) : r);
+}
+BOA_DEV float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+BOA_DEV float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// activation storage: fp32 or bf16
+BOA_DEV float ldv(const float* p) { return *p; }
+BOA_DEV float ldv(const uint16_t* p) { return bf16_to_f32(*p); }
+BOA_DEV void stv(float* p, float v) { *p = v; }
+BOA_DEV void stv(uint16_t* p, float v) { *p = f32_to_bf16(v); }
+
 // e^x and log(y) in two forms with identical results for every input:
 // expf_ / logf_ are branch-free (the arithmetic runs on a clamped or rescaled
 // argument and selects give the special values, so a wavefront never

@@ -26,13 +26,6 @@ namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// In-block position of feature k % 16 (a 4x4 transpose, its own inverse).
-__device__ __forceinline__ int dperm(int j) { return ((j & 3) << 2) | ((j >> 2) & 3); }
-
-// k-blocked index of (feature k, lane m), lane capacity ld.
-__device__ __forceinline__ size_t dblk(int k, int m, int ld) {
-  return ((size_t)(k >> 4) * ld + m) * 16 + dperm(k & 15);
-}
 
 // ------------------------------------------------------------------- GEMM
 // A wave computes TN x TM MFMA tiles of 16 output features x 16 lanes.  Lane

@@ -1,0 +1,399 @@
+// Decode-step kernels of the bf16 precision (one token per lane).
+//
+// Activations are bf16 in the 32-blocked layout (feature k of lane m at
+// ((k/32) ld + m) 32 + k%32, 64 contiguous bytes per lane and block) except
+// the residual stream x, which stays fp32 in the k-blocked layout of the
+// fp32 step.  Weights are bf16 in the same 32-blocked layout over their
+// output rows.  A v_mfma_f32_16x16x32_bf16 operand slot group (8 k) is then
+// one 16-byte load, and each load instruction of a wavefront reads 1 KB.
+// The GEMM chain, the epilogue and the per-element sequences are those of
+// the bf16 compress kernels, so decode logits equal compress logits.
+#include "block_device.h"
+#include "boa_kernels.h"
+
+namespace boa {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// ------------------------------------------------------------------- GEMM
+// Wave tile 16 features x 16 lanes; lane (i, g) loads, per k-step s of 32,
+// W[s][n0+i][8g..8g+7] and X[s][m0+i][8g..8g+7]; accumulator v holds feature
+// n0 + 4g + v of lane m0 + i.
+__device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floatx4 acc, int n0,
+                                                 int m, int g) {
+  if (m >= a.M || n0 >= a.N) return;
+  const int nb = n0 + 4 * g;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float r = acc[e] + (a.bias ? a.bias[min(nb + e, a.N - 1)] : 0.0f);
+    if (a.act == ACT_GELU) r = gelu<true>(r);
+    else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
+    v[e] = r;
+  }
+  if (a.out_mode == DEC_OUT_ROWMAJOR) {  // logits [M][ldc] fp32
+    float* C = reinterpret_cast<float*>(a.C) + (size_t)m * a.ldc + nb;
+    if (nb + 4 <= a.N) {
+      *reinterpret_cast<float4*>(C) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nb + e < a.N) C[e] = v[e];
+    }
+    return;
+  }
+  if (a.out_mode == DEC_OUT_F32) {  // residual stream: fp32 k-blocked, + res
+    float* C = reinterpret_cast<float*>(a.C);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int n = nb + e;
+      if (n >= a.N) break;
+      float r = v[e];
+      if (a.res) r = r + a.res[dblk(n, m, a.ldr)];
+      v[e] = r;
+      C[dblk(n, m, a.ldc)] = r;
+    }
+    if (a.C2 && nb + 4 <= a.N)
+      *reinterpret_cast<ushort4*>(a.C2 + dblk32(nb, m, a.ldc)) =
+          make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+    return;
+  }
+  // bf16 32-blocked output; in_proj runs the conv step on its x half
+  uint16_t o[4];
+  if (a.conv_di > 0 && nb < a.conv_di) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int n = nb + e;
+      const float x0 = bf16r(v[e]);  // the compress pass reads xz in bf16
+      float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
+      const float4 s0 = *st;
+      const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
+      o[e] = f32_to_bf16(conv_step_value<true>(a.conv_b[n], s0, x0, wv));
+      *st = make_float4(s0.y, s0.z, s0.w, x0);
+    }
+    *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) = make_ushort4(o[0], o[1], o[2], o[3]);
+    return;
+  }
+  const int row = a.conv_di > 0 ? nb - a.conv_di : nb;
+  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+  if (nb + 4 <= a.N) {
+    *reinterpret_cast<ushort4*>(C + dblk32(row, m, a.ldc)) =
+        make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (nb + e < a.N) C[dblk32(row + e, m, a.ldc)] = f32_to_bf16(v[e]);
+  }
+}
+
+template <int KS, int PD>
+__global__ __launch_bounds__(256) void dec_b16_gemm_kernel(DecB16Args a) {
+  constexpr int UQ = 2;                        // k-steps per prefetch group
+  constexpr int G = KS / UQ;                   // groups
+  constexpr int R = (PD < G ? PD : G - 1) + 1;  // ring size
+  static_assert(KS % UQ == 0, "K must be a multiple of 64");
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15, g = lane >> 4;
+  const int n_tiles = (a.N + 15) / 16;
+  const int m_tiles = (a.M + 15) / 16;
+  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wid >= n_tiles * m_tiles) return;  // whole waves exit; no barriers below
+  const int n0 = (wid % n_tiles) * 16;
+  const int m0 = (wid / n_tiles) * 16;
+  const u32x4* wp =
+      reinterpret_cast<const u32x4*>(a.W) + (size_t)min(n0 + i, a.ldw - 1) * 4 + g;
+  const u32x4* xp = reinterpret_cast<const u32x4*>(a.X) + (size_t)min(m0 + i, a.M - 1) * 4 + g;
+  const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // 16-byte units per k-step
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  u32x4 af[R][UQ], bf[R][UQ];
+#define BOA_B16_DLOAD(BUF, S0)                            \
+  _Pragma("unroll") for (int q = 0; q < UQ; ++q) {        \
+    af[BUF][q] = wp[(size_t)((S0) + q) * wq];             \
+    bf[BUF][q] = xp[(size_t)((S0) + q) * xq];             \
+  }                                                       \
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < R - 1; ++p) { BOA_B16_DLOAD(p, p * UQ) }
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    if (gi + R - 1 < G) { BOA_B16_DLOAD((gi + R - 1) % R, (gi + R - 1) * UQ) }
+#pragma unroll
+    for (int q = 0; q < UQ; ++q)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[gi % R][q]),
+                                                    __builtin_bit_cast(bf16x8, bf[gi % R][q]), acc,
+                                                    0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#undef BOA_B16_DLOAD
+  dec_b16_epilogue(a, acc, n0, m0 + i, g);
+}
+
+hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.ldw < (a.N + 15) / 16 * 16 || a.ldx < a.M || (a.conv_di % 16) ||
+      (a.out_mode != DEC_OUT_ROWMAJOR && a.ldc < a.M) || (a.res && a.ldr < a.M))
+    return hipErrorInvalidValue;
+  const int tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16);
+  const dim3 grid((tiles + 3) / 4), block(256);
+  switch (a.K) {
+    case 64: hipLaunchKernelGGL((dec_b16_gemm_kernel<2, 2>), grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL((dec_b16_gemm_kernel<4, 2>), grid, block, 0, s, a); break;
+    case 256: hipLaunchKernelGGL((dec_b16_gemm_kernel<8, 2>), grid, block, 0, s, a); break;
+    case 512: hipLaunchKernelGGL((dec_b16_gemm_kernel<16, 2>), grid, block, 0, s, a); break;
+    case 1024: hipLaunchKernelGGL((dec_b16_gemm_kernel<32, 2>), grid, block, 0, s, a); break;
+    case 2048: hipLaunchKernelGGL((dec_b16_gemm_kernel<64, 2>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Weight relayout: W [K][ldw_in] fp32 (the fp32 compress layout) -> bf16
+// 32-blocked over its output columns [K/32][ldn][32]; logical column j maps
+// to source column j (j < zs), a zero column (zs <= j < ze) or source column
+// j - (ze - zs) (j >= ze).
+__global__ void dec_b16_weight_kernel(const float* __restrict__ w, int ldw_in, int n_src,
+                                      uint16_t* out, int K, int ldn, int zs, int ze) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)K * ldn) return;
+  const int k = (int)(idx / ldn), j = (int)(idx % ldn);
+  const int n = j < zs ? j : (j < ze ? -1 : j - (ze - zs));
+  out[dblk32(k, j, ldn)] = (n >= 0 && n < n_src) ? f32_to_bf16(w[(size_t)k * ldw_in + n]) : 0;
+}
+
+hipError_t launch_dec_b16_weight(const float* w, int ldw_in, int n_src, uint16_t* out, int K,
+                                 int ldn, int zs, int ze, hipStream_t s) {
+  if (K % 32 || ldn % 16 || n_src > ldw_in || zs > ze) return hipErrorInvalidValue;
+  const size_t n = (size_t)K * ldn;
+  hipLaunchKernelGGL(dec_b16_weight_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
+                     ldw_in, n_src, out, K, ldn, zs, ze);
+  return hipGetLastError();
+}
+
+// -------------------------------------------------------------- LayerNorm
+// As the fp32 step LayerNorm (16 lanes per 256-thread block, reference
+// reduction orders), reading fp32 k-blocked x (LN1), the embedding (layer
+// 0, which also stores x) or bf16 32-blocked activations (LN2), and writing
+// bf16 32-blocked output.
+enum { LN_IN_F32 = 0, LN_IN_EMB = 1, LN_IN_B16 = 2 };
+
+template <int MODE, int NB, int IN>
+__global__ __launch_bounds__(256) void dec_b16_ln_kernel(const float* __restrict__ emb,
+                                                         const uint8_t* __restrict__ tok, float* xt,
+                                                         const void* src, uint16_t* xnt,
+                                                         const float* __restrict__ w,
+                                                         const float* __restrict__ b, int M,
+                                                         int ld, int* t_counter) {
+  constexpr int d = NB * 16;
+  constexpr int S = d + 4;
+  __shared__ __align__(16) float tile[16 * S];
+  __shared__ float stats[32];
+  if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
+  const int t = threadIdx.x;
+  const int m0 = blockIdx.x * 16;
+  {  // stage the 16 rows in natural feature order
+    const int j = (t >> 2) & 15, a4 = t & 3;
+    const int m = min(m0 + j, M - 1);
+    if (IN == LN_IN_B16) {
+      // thread: 8 features (16 bytes) of a 32-feature block
+      const uint16_t* s16 = reinterpret_cast<const uint16_t*>(src);
+      for (int kb = t >> 6; kb < d / 32; kb += 4) {
+        const u32x4 r = *reinterpret_cast<const u32x4*>(s16 + dblk32(32 * kb + 8 * a4, m, ld));
+        float* row = tile + j * S + 32 * kb + 8 * a4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          row[2 * e] = u2f(r[e] << 16);
+          row[2 * e + 1] = u2f(r[e] & 0xFFFF0000u);
+        }
+      }
+    } else {
+      const float* erow = IN == LN_IN_EMB ? emb + (size_t)tok[m] * d : nullptr;
+      const float* s32 = reinterpret_cast<const float*>(src);
+      for (int kb = t >> 6; kb < NB; kb += 4) {
+        float* row = tile + j * S + 16 * kb;
+        if (IN == LN_IN_EMB) {
+          const float4 v = *reinterpret_cast<const float4*>(erow + 16 * kb + 4 * a4);
+          row[4 * a4] = v.x; row[4 * a4 + 1] = v.y; row[4 * a4 + 2] = v.z; row[4 * a4 + 3] = v.w;
+        } else {
+          const float4 v = *reinterpret_cast<const float4*>(s32 + ((size_t)kb * ld + m) * 16 + 4 * a4);
+          row[dperm(4 * a4)] = v.x; row[dperm(4 * a4 + 1)] = v.y;
+          row[dperm(4 * a4 + 2)] = v.z; row[dperm(4 * a4 + 3)] = v.w;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (MODE == 1) {
+    const int lj = t >> 4, l = t & 15;
+    const float* row = tile + lj * S;
+    float s0 = 0.0f, q0 = 0.0f, s1 = 0.0f, q1 = 0.0f;
+    for (int k = l; k < d; k += 32) { const float x = row[k]; s0 = s0 + x; q0 = q0 + x * x; }
+    for (int k = l + 16; k < d; k += 32) { const float x = row[k]; s1 = s1 + x; q1 = q1 + x * x; }
+    float sum = s0 + s1, sq = q0 + q1;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+      sum = sum + __shfl_down(sum, off, 16);
+      sq = sq + __shfl_down(sq, off, 16);
+    }
+    if (l == 0) {
+      const float mean = sum / (float)d;
+      const float var = sq / (float)d - mean * mean;
+      stats[2 * lj] = mean;
+      stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    }
+  } else if (t < 16) {
+    const float4* row = reinterpret_cast<const float4*>(tile + t * S);
+    float sum = 0.0f, sq = 0.0f;
+    for (int k4 = 0; k4 < d / 4; ++k4) {
+      const float4 x = row[k4];
+      sum = sum + x.x; sq = sq + x.x * x.x;
+      sum = sum + x.y; sq = sq + x.y * x.y;
+      sum = sum + x.z; sq = sq + x.z * x.z;
+      sum = sum + x.w; sq = sq + x.w * x.w;
+    }
+    const float mean = sum / (float)d;
+    const float var = sq / (float)d - mean * mean;
+    stats[2 * t] = mean;
+    stats[2 * t + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+  }
+  __syncthreads();
+  const int j = (t >> 2) & 15, a4 = t & 3;
+  if (m0 + j >= M) return;
+  const float mean = stats[2 * j], rstd = stats[2 * j + 1];
+  const float* row = tile + j * S;
+  for (int kb = t >> 6; kb < d / 32; kb += 4) {  // 8 features per thread and block
+    const int k0 = 32 * kb + 8 * a4;
+    uint32_t r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = k0 + 2 * e;
+      const float o0 = ((row[k] - mean) * rstd) * w[k] + b[k];
+      const float o1 = ((row[k + 1] - mean) * rstd) * w[k + 1] + b[k + 1];
+      r[e] = (uint32_t)f32_to_bf16(o0) | ((uint32_t)f32_to_bf16(o1) << 16);
+    }
+    *reinterpret_cast<u32x4*>(xnt + dblk32(k0, m0 + j, ld)) = u32x4{r[0], r[1], r[2], r[3]};
+  }
+  if (IN == LN_IN_EMB) {  // x = the embedding row, fp32 k-blocked
+    for (int kb = t >> 6; kb < NB; kb += 4) {
+      const float* rr = row + 16 * kb;
+      *reinterpret_cast<float4*>(xt + ((size_t)kb * ld + m0 + j) * 16 + 4 * a4) =
+          make_float4(rr[dperm(4 * a4)], rr[dperm(4 * a4 + 1)], rr[dperm(4 * a4 + 2)],
+                      rr[dperm(4 * a4 + 3)]);
+    }
+  }
+}
+
+template <int MODE, int IN>
+static hipError_t dec_b16_ln_go(const float* emb, const uint8_t* tok, float* xt, const void* src,
+                                uint16_t* xnt, const float* w, const float* b, int M, int d, int ld,
+                                int* t_counter, hipStream_t s) {
+  const dim3 grid((M + 15) / 16), block(256);
+  switch (d) {
+    case 64: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 4, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 128: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 8, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 256: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 16, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 512: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 32, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// LN1: from the embedding (emb != null; also stores x) or from fp32 x.
+hipError_t launch_dec_b16_ln1(const float* emb, const uint8_t* tok, float* xt, uint16_t* xnt,
+                              const float* w, const float* b, int M, int d, int ld, int* t_counter,
+                              hipStream_t s) {
+  return emb ? dec_b16_ln_go<1, LN_IN_EMB>(emb, tok, xt, nullptr, xnt, w, b, M, d, ld, t_counter, s)
+             : dec_b16_ln_go<1, LN_IN_F32>(nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, ld,
+                                           t_counter, s);
+}
+
+hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w, const float* b,
+                              int M, int d, int ld, hipStream_t s) {
+  return dec_b16_ln_go<2, LN_IN_B16>(nullptr, nullptr, nullptr, src, xnt, w, b, M, d, ld, nullptr,
+                                     s);
+}
+
+// ------------------------------------------------------------------- scan
+// As the fp32 step scan (16 channels x 16 lanes per block, quad-layout state
+// and parameters), with bf16 32-blocked u, z, rows and y.
+template <int DS, int RB>
+__global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const float* __restrict__ na_q,
+                                                           const float* __restrict__ wdt_q,
+                                                           const uint16_t* __restrict__ zt,
+                                                           const uint16_t* __restrict__ cvt,
+                                                           const uint16_t* __restrict__ rows,
+                                                           float* ssm, uint16_t* yt, int M, int ld,
+                                                           int ld_state, int r) {
+  constexpr int NB = (RB + 2 * DS + 31) / 32;
+  const int cl = threadIdx.x & 15;
+  const int cb = blockIdx.y;
+  const int c = cb * 16 + cl;
+  const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (m >= M) return;
+  ScanCtx<DS, RB> sc;
+  float4* h4 = reinterpret_cast<float4*>(ssm);
+  const float4* na4 = reinterpret_cast<const float4*>(na_q);
+  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
+#pragma unroll
+  for (int n4 = 0; n4 < DS / 4; ++n4) {
+    const float4 hv = h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl];
+    sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
+    const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
+    sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
+  }
+#pragma unroll
+  for (int j4 = 0; j4 < RB / 4; ++j4) {
+    const float4 wv = w4[(cb * (RB / 4) + j4) * 16 + cl];
+    sc.wdt[4 * j4] = wv.x; sc.wdt[4 * j4 + 1] = wv.y; sc.wdt[4 * j4 + 2] = wv.z; sc.wdt[4 * j4 + 3] = wv.w;
+  }
+  sc.bdt = Lw.b_dt[c];
+  sc.dd = Lw.dd[c];
+  float row[NB * 32];
+#pragma unroll
+  for (int kb = 0; kb < NB; ++kb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(rows + dblk32(32 * kb + 8 * q, m, ld));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        row[32 * kb + 8 * q + 2 * e] = u2f(v[e] << 16);
+        row[32 * kb + 8 * q + 2 * e + 1] = u2f(v[e] & 0xFFFF0000u);
+      }
+    }
+  const size_t cm = dblk32(c, m, ld);
+  const float u = bf16_to_f32(cvt[cm]);
+  const float z = bf16_to_f32(zt[cm]);
+  yt[cm] = f32_to_bf16(scan_token<DS, RB, true>(sc, row, row + RB, r, u, z));
+#pragma unroll
+  for (int n4 = 0; n4 < DS / 4; ++n4)
+    h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl] =
+        make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]);
+}
+
+hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
+                               const float* wdt_q, const uint16_t* zt, const uint16_t* cvt,
+                               const uint16_t* rows, float* ssm, uint16_t* yt, int M, int ld,
+                               int ld_state, hipStream_t s) {
+  if (D.di % 16 || dec_rb(D.r) < D.r) return hipErrorInvalidValue;
+  dim3 grid((M + 15) / 16, D.di / 16);
+#define BOA_B16_SCAN(DSv, RBv)                                                                  \
+  hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, zt, \
+                     cvt, rows, ssm, yt, M, ld, ld_state, D.r)
+  const int rb = dec_rb(D.r);
+  if (D.ds == 16) {
+    if (rb == 8) BOA_B16_SCAN(16, 8);
+    else if (rb == 16) BOA_B16_SCAN(16, 16);
+    else BOA_B16_SCAN(16, 32);
+  } else if (D.ds == 32) {
+    if (rb == 8) BOA_B16_SCAN(32, 8);
+    else if (rb == 16) BOA_B16_SCAN(32, 16);
+    else BOA_B16_SCAN(32, 32);
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef BOA_B16_SCAN
+  return hipGetLastError();
+}
+
+}  // namespace boa

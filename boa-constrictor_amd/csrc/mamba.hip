@@ -20,11 +20,29 @@ namespace boa {
 
 constexpr int LN_MAXE = 16;  // d_model <= 512
 
+// four consecutive activations (fp32 or bf16 storage)
+__device__ __forceinline__ void ld4(const float* p, float* v) {
+  const float4 t = *reinterpret_cast<const float4*>(p);
+  v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+}
+__device__ __forceinline__ void ld4(const uint16_t* p, float* v) {
+  const ushort4 t = *reinterpret_cast<const ushort4*>(p);
+  v[0] = bf16_to_f32(t.x); v[1] = bf16_to_f32(t.y); v[2] = bf16_to_f32(t.z); v[3] = bf16_to_f32(t.w);
+}
+__device__ __forceinline__ void st4(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st4(uint16_t* p, const float* v) {
+  *reinterpret_cast<ushort4*>(p) =
+      make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+}
+
 // -------------------------------------------------------------- LayerNorm
 // One 32-lane half-wave per row: lane l accumulates elements l, l+32, ...
 // in order, then lanes combine by the shuffle-down tree 16, 8, 4, 2, 1 and
 // lane 0's totals are broadcast (the reference's warp-per-row order).
-__device__ __forceinline__ void ln_halfwave_row(const float* src, float* x_copy, float* dst,
+template <typename TO>
+__device__ __forceinline__ void ln_halfwave_row(const float* src, float* x_copy, TO* dst,
                                                 const float* __restrict__ w,
                                                 const float* __restrict__ b, int d, int l) {
   float v[LN_MAXE];
@@ -53,12 +71,13 @@ __device__ __forceinline__ void ln_halfwave_row(const float* src, float* x_copy,
 #pragma unroll
   for (int e = 0; e < LN_MAXE; ++e) {
     int idx = l + 32 * e;
-    if (idx < d) dst[idx] = ((v[e] - mean) * inv_std) * w[idx] + b[idx];
+    if (idx < d) stv(dst + idx, ((v[e] - mean) * inv_std) * w[idx] + b[idx]);
   }
 }
 
+template <typename TO>
 __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb, TokenSrc tok,
-                                                  int use_tok, int T, int t0, float* x, float* xn,
+                                                  int use_tok, int T, int t0, float* x, TO* xn,
                                                   const float* __restrict__ w,
                                                   const float* __restrict__ b, int rows, int d) {
   const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
@@ -78,12 +97,16 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
   ln_halfwave_row(src, xc, xn + (size_t)row * d, w, b, d, l);
 }
 
-hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, float* xn,
-                      const float* w, const float* b, int rows, int d, hipStream_t s) {
+hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, void* xn,
+                      const float* w, const float* b, int rows, int d, bool bf16, hipStream_t s) {
   if (d > 32 * LN_MAXE) return hipErrorInvalidValue;
   int blocks = (rows + 7) / 8;
-  hipLaunchKernelGGL(ln1_kernel, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T, t0, x, xn,
-                     w, b, rows, d);
+  if (bf16)
+    hipLaunchKernelGGL(ln1_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T,
+                       t0, x, (uint16_t*)xn, w, b, rows, d);
+  else
+    hipLaunchKernelGGL(ln1_kernel<float>, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T,
+                       t0, x, (float*)xn, w, b, rows, d);
   return hipGetLastError();
 }
 
@@ -92,7 +115,8 @@ hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, f
 // loads (row stride d+1 keeps the per-row sequential reads conflict-free),
 // one thread per row runs the sequential sums, then all threads normalise
 // and store coalesced.  In place is allowed.
-__global__ __launch_bounds__(256) void ln2_kernel(const float* x, float* out,
+template <typename T>
+__global__ __launch_bounds__(256) void ln2_kernel(const T* x, T* out,
                                                   const float* __restrict__ w,
                                                   const float* __restrict__ b, int rows, int d,
                                                   int rows_per_block) {
@@ -104,9 +128,10 @@ __global__ __launch_bounds__(256) void ln2_kernel(const float* x, float* out,
   const int dq = d / 4, S = d + 1;
   for (int q = threadIdx.x; q < nr * dq; q += blockDim.x) {
     const int r = q / dq, c4 = q % dq;
-    const float4 v = *reinterpret_cast<const float4*>(x + (size_t)(r0 + r) * d + 4 * c4);
+    float v[4];
+    ld4(x + (size_t)(r0 + r) * d + 4 * c4, v);
     float* dst = tile + r * S + 4 * c4;
-    dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
+    dst[0] = v[0]; dst[1] = v[1]; dst[2] = v[2]; dst[3] = v[3];
   }
   __syncthreads();
   if (threadIdx.x < nr) {
@@ -129,31 +154,36 @@ __global__ __launch_bounds__(256) void ln2_kernel(const float* x, float* out,
     const float* src = tile + r * S + 4 * c4;
     const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c4);
     const float4 bv = *reinterpret_cast<const float4*>(b + 4 * c4);
-    float4 o;
-    o.x = ((src[0] - mean) * inv_std) * wv.x + bv.x;
-    o.y = ((src[1] - mean) * inv_std) * wv.y + bv.y;
-    o.z = ((src[2] - mean) * inv_std) * wv.z + bv.z;
-    o.w = ((src[3] - mean) * inv_std) * wv.w + bv.w;
-    *reinterpret_cast<float4*>(out + (size_t)(r0 + r) * d + 4 * c4) = o;
+    float o[4];
+    o[0] = ((src[0] - mean) * inv_std) * wv.x + bv.x;
+    o[1] = ((src[1] - mean) * inv_std) * wv.y + bv.y;
+    o[2] = ((src[2] - mean) * inv_std) * wv.z + bv.z;
+    o[3] = ((src[3] - mean) * inv_std) * wv.w + bv.w;
+    st4(out + (size_t)(r0 + r) * d + 4 * c4, o);
   }
 }
 
-hipError_t launch_ln2(const float* x, float* out, const float* w, const float* b, int rows, int d,
-                      hipStream_t s) {
+hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, int rows, int d,
+                      bool bf16, hipStream_t s) {
   if (d % 4 || d > 512) return hipErrorInvalidValue;
   // at most ~48 KB of LDS per block
   const int rpb = std::min(64, (48 * 1024) / (4 * (d + 1)));
   const size_t lds = sizeof(float) * ((size_t)rpb * (d + 1) + 2 * rpb);
-  hipLaunchKernelGGL(ln2_kernel, dim3((rows + rpb - 1) / rpb), dim3(256), lds, s, x, out, w, b,
-                     rows, d, rpb);
+  if (bf16)
+    hipLaunchKernelGGL(ln2_kernel<uint16_t>, dim3((rows + rpb - 1) / rpb), dim3(256), lds, s,
+                       (const uint16_t*)x, (uint16_t*)out, w, b, rows, d, rpb);
+  else
+    hipLaunchKernelGGL(ln2_kernel<float>, dim3((rows + rpb - 1) / rpb), dim3(256), lds, s,
+                       (const float*)x, (float*)out, w, b, rows, d, rpb);
   return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ conv1d
-__global__ __launch_bounds__(256) void conv_chunk_kernel(const float* __restrict__ xz,
+template <typename TA>
+__global__ __launch_bounds__(256) void conv_chunk_kernel(const TA* __restrict__ xz,
                                                          float* conv_state,
                                                          const float* __restrict__ w,
-                                                         const float* __restrict__ cb, float* out,
+                                                         const float* __restrict__ cb, TA* out,
                                                          int lanes, int T, int di) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= lanes * di) return;
@@ -163,21 +193,25 @@ __global__ __launch_bounds__(256) void conv_chunk_kernel(const float* __restrict
   const float4 wv = reinterpret_cast<const float4*>(w)[c];
   const float bias = cb[c];
   float xm4 = s0.x, xm3 = s0.y, xm2 = s0.z, xm1 = s0.w;
-  const float* xp = xz + (size_t)b * T * (2 * di) + c;
-  float* op = out + (size_t)b * T * di + c;
+  const TA* xp = xz + (size_t)b * T * (2 * di) + c;
+  TA* op = out + (size_t)b * T * di + c;
   for (int t = 0; t < T; ++t) {
-    float x0 = xp[(size_t)t * 2 * di];
-    op[(size_t)t * di] = conv_value(bias, xm3, xm2, xm1, x0, wv);
+    float x0 = ldv(xp + (size_t)t * 2 * di);
+    stv(op + (size_t)t * di, conv_value(bias, xm3, xm2, xm1, x0, wv));
     xm4 = xm3; xm3 = xm2; xm2 = xm1; xm1 = x0;
   }
   *st = make_float4(xm4, xm3, xm2, xm1);
 }
 
-hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w, const float* cb,
-                             float* out, int lanes, int T, int di, hipStream_t s) {
+hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, const float* cb,
+                             void* out, int lanes, int T, int di, bool bf16, hipStream_t s) {
   int n = lanes * di;
-  hipLaunchKernelGGL(conv_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, xz, conv_state, w,
-                     cb, out, lanes, T, di);
+  if (bf16)
+    hipLaunchKernelGGL(conv_chunk_kernel<uint16_t>, dim3((n + 255) / 256), dim3(256), 0, s,
+                       (const uint16_t*)xz, conv_state, w, cb, (uint16_t*)out, lanes, T, di);
+  else
+    hipLaunchKernelGGL(conv_chunk_kernel<float>, dim3((n + 255) / 256), dim3(256), 0, s,
+                       (const float*)xz, conv_state, w, cb, (float*)out, lanes, T, di);
   return hipGetLastError();
 }
 
@@ -185,12 +219,12 @@ hipError_t launch_conv_chunk(const float* xz, float* conv_state, const float* w,
 // Thread per (lane, channel); a block never straddles two lanes, so the
 // delta rows (dt_in | B | C of one token) are shared by the whole block: they
 // are staged in LDS SCAN_TB timesteps at a time and read as broadcasts.
-template <int DS, int RB>
+template <int DS, int RB, typename TA>
 __global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
-                                                         const float* __restrict__ xz,
-                                                         const float* __restrict__ conv,
-                                                         const float* __restrict__ delta,
-                                                         float* ssm_state, float* y, int lanes,
+                                                         const TA* __restrict__ xz,
+                                                         const TA* __restrict__ conv,
+                                                         const TA* __restrict__ delta,
+                                                         float* ssm_state, TA* y, int lanes,
                                                          int T) {
   extern __shared__ float s_delta[];  // [SCAN_TB][R]
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -199,17 +233,17 @@ __global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
   float* ssm = ssm_state + (size_t)idx * DS;
   ScanCtx<DS, RB> sc;
   scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
-  const float* drows = delta + (size_t)b * T * R;
+  const TA* drows = delta + (size_t)b * T * R;
   for (int t0 = 0; t0 < T; t0 += SCAN_TB) {
     const int nt = min(SCAN_TB, T - t0);
     __syncthreads();
-    for (int q = threadIdx.x; q < nt * R; q += blockDim.x) s_delta[q] = drows[(size_t)t0 * R + q];
+    for (int q = threadIdx.x; q < nt * R; q += blockDim.x) s_delta[q] = ldv(drows + (size_t)t0 * R + q);
     __syncthreads();
     for (int tt = 0; tt < nt; ++tt) {
       const size_t row = (size_t)b * T + t0 + tt;
-      const float u = conv[row * di + c];
-      const float z = xz[row * 2 * di + di + c];
-      y[row * di + c] = scan_token<DS, RB>(sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z);
+      const float u = ldv(conv + row * di + c);
+      const float z = ldv(xz + row * 2 * di + di + c);
+      stv(y + row * di + c, scan_token<DS, RB>(sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z));
     }
   }
   scan_store<DS, RB>(sc, ssm);
@@ -222,12 +256,18 @@ static int block_for(int di) {
 }
 
 template <int DS, int RB>
-static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
-                                const float* delta, float* ssm_state, float* y, int lanes, int T,
-                                int bs, hipStream_t s) {
+static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const void* xz, const void* conv,
+                                const void* delta, float* ssm_state, void* y, int lanes, int T,
+                                int bs, bool bf16, hipStream_t s) {
   const size_t lds = sizeof(float) * SCAN_TB * D.R;
-  hipLaunchKernelGGL((scan_chunk_kernel<DS, RB>), dim3((lanes * D.di) / bs), dim3(bs), lds, s, D,
-                     Lw, xz, conv, delta, ssm_state, y, lanes, T);
+  if (bf16)
+    hipLaunchKernelGGL((scan_chunk_kernel<DS, RB, uint16_t>), dim3((lanes * D.di) / bs), dim3(bs),
+                       lds, s, D, Lw, (const uint16_t*)xz, (const uint16_t*)conv,
+                       (const uint16_t*)delta, ssm_state, (uint16_t*)y, lanes, T);
+  else
+    hipLaunchKernelGGL((scan_chunk_kernel<DS, RB, float>), dim3((lanes * D.di) / bs), dim3(bs), lds,
+                       s, D, Lw, (const float*)xz, (const float*)conv, (const float*)delta,
+                       ssm_state, (float*)y, lanes, T);
   return hipGetLastError();
 }
 
@@ -244,12 +284,12 @@ static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const float* xz
     return GO<32, 32>(__VA_ARGS__);                                       \
   } while (0)
 
-hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const float* xz, const float* conv,
-                             const float* delta, float* ssm_state, float* y, int lanes, int T,
-                             hipStream_t s) {
+hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const void* xz, const void* conv,
+                             const void* delta, float* ssm_state, void* y, int lanes, int T,
+                             bool bf16, hipStream_t s) {
   const int bs = block_for(D.di);
   if (!bs || D.r > RMAX || (D.ds != 16 && D.ds != 32)) return hipErrorInvalidValue;
-  BOA_SCAN_DISPATCH(scan_chunk_go, D, Lw, xz, conv, delta, ssm_state, y, lanes, T, bs, s);
+  BOA_SCAN_DISPATCH(scan_chunk_go, D, Lw, xz, conv, delta, ssm_state, y, lanes, T, bs, bf16, s);
 }
 
 // ------------------------------------------------------------------ misc

@@ -47,7 +47,8 @@ typedef struct {
     int32_t d_state;     /* 16 or 32 (the reference supports 16 only) */
     int32_t max_lanes;   /* chunks processed in parallel (--gpu-batch) */
     int32_t tile;        /* compress forward tile in tokens (--tile); 0 = auto */
-    int32_t precision;   /* 0 = fp32 (only value supported) */
+    int32_t precision;   /* 0 = fp32; 1 = bf16 weights and activations (fp32
+                            accumulation, residual stream, scan state, logits) */
     float temperature;   /* softmax temperature (--temperature), 1.0 default */
 } boa_config;
 

@@ -22,6 +22,19 @@
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 
+/* bfloat16: the upper half of a float32, rounded to nearest even; NaN stays
+ * a quiet NaN. */
+uint16_t ref_f32_to_bf16(float x) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+float ref_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+static inline float bf16r(float x) { return ref_bf16_to_f32(ref_f32_to_bf16(x)); }
+static void bf16_round(float* p, size_t n) {
+    for (size_t i = 0; i < n; ++i) p[i] = bf16r(p[i]);
+}
+
 /* =====================================================================
  * Math.  ref_expf/ref_logf are this project's own functions (the GPU
  * kernels evaluate the same operation sequence, so results agree bit for
@@ -434,6 +447,7 @@ typedef struct {
 
 struct ref_model {
     int d, L, di, r, ds, dc, R;
+    int bf16;                /* 1: bf16 weights and activations (ref_model_set_bf16) */
     float* emb;              /* [256][d] */
     ref_layer* layers;
     float *hw1, *hb1;        /* [d][d], [d] */
@@ -570,6 +584,23 @@ void ref_model_free(ref_model* m) {
     free(m->layers);
     free(m->emb); free(m->hw1); free(m->hb1); free(m->hw2); free(m->hb2);
     free(m);
+}
+
+int32_t ref_model_set_bf16(ref_model* m) {
+    if (!m || m->bf16) return m ? 0 : -1;
+    int d = m->d, di = m->di, R = m->R;
+    for (int l = 0; l < m->L; ++l) {
+        ref_layer* y = &m->layers[l];
+        bf16_round(y->w_in, (size_t)d * 2 * di);
+        bf16_round(y->w_x, (size_t)di * R);
+        bf16_round(y->w_out, (size_t)di * d);
+        bf16_round(y->w1, (size_t)d * 4 * d);
+        bf16_round(y->w2, (size_t)4 * d * d);
+    }
+    bf16_round(m->hw1, (size_t)d * d);
+    bf16_round(m->hw2, (size_t)d * 256);
+    m->bf16 = 1;
+    return 0;
 }
 
 ref_state* ref_state_new(const ref_model* m, int32_t lanes) {
@@ -716,9 +747,12 @@ static void block_rows(const ref_model* m, const ref_state* st, int l, scratch_t
                        int chunk_mode, int lane0) {
     const ref_layer* Ly = &m->layers[l];
     int d = m->d, di = m->di, R = m->R, ds = m->ds;
+    const int bf = m->bf16;  /* bf16 mode: round every stored activation but x */
     for (int i = 0; i < rows; ++i)
         layernorm_warp_row(sc->x + (size_t)i * d, Ly->ln1_w, Ly->ln1_b, sc->xn + (size_t)i * d, d);
+    if (bf) bf16_round(sc->xn, (size_t)rows * d);
     gemm_rows(sc->xn, d, Ly->w_in, d, 2 * di, Ly->b_in, ACT_NONE, NULL, 0, sc->xz, 2 * di, rows);
+    if (bf) bf16_round(sc->xz, (size_t)rows * 2 * di);
     /* causal depthwise conv1d + SiLU */
     if (chunk_mode) {
         float* cs_all = conv_state(st, l, lane0);
@@ -755,7 +789,9 @@ static void block_rows(const ref_model* m, const ref_state* st, int l, scratch_t
             }
         }
     }
+    if (bf) bf16_round(sc->cv, (size_t)rows * di);
     gemm_rows(sc->cv, di, Ly->w_x, di, R, NULL, ACT_NONE, NULL, 0, sc->delta, R, rows);
+    if (bf) bf16_round(sc->delta, (size_t)rows * R);
     if (chunk_mode) {
         float* hs = ssm_state(st, l, lane0);
         for (int c = 0; c < di; ++c) {
@@ -776,16 +812,27 @@ static void block_rows(const ref_model* m, const ref_state* st, int l, scratch_t
         }
     }
     /* out_proj, LN2, FF1+GELU, FF2+bias+residual(saved pre-LN1 x) */
+    if (bf) bf16_round(sc->y, (size_t)rows * di);
     gemm_rows(sc->y, di, Ly->w_out, di, d, Ly->b_out, ACT_NONE, NULL, 0, sc->xn, d, rows);
+    if (bf) bf16_round(sc->xn, (size_t)rows * d);
     for (int i = 0; i < rows; ++i)
         layernorm_seq_row(sc->xn + (size_t)i * d, Ly->ln2_w, Ly->ln2_b, sc->xn + (size_t)i * d, d);
+    if (bf) bf16_round(sc->xn, (size_t)rows * d);
     gemm_rows(sc->xn, d, Ly->w1, d, 4 * d, Ly->b1, ACT_GELU, NULL, 0, sc->hid, 4 * d, rows);
+    if (bf) bf16_round(sc->hid, (size_t)rows * 4 * d);
     gemm_rows(sc->hid, 4 * d, Ly->w2, 4 * d, d, Ly->b2, ACT_NONE, sc->x, d, sc->x, d, rows);
 }
 
 static void head_rows(const ref_model* m, scratch_t* sc, int rows, int add_bias, float* logits) {
     int d = m->d;
-    gemm_rows(sc->x, d, m->hw1, d, d, m->hb1, ACT_RELU, NULL, 0, sc->hh, d, rows);
+    const float* xin = sc->x;
+    if (m->bf16) {  /* the residual stream stays fp32; head1 reads its bf16 copy */
+        memcpy(sc->xn, sc->x, sizeof(float) * (size_t)rows * d);
+        bf16_round(sc->xn, (size_t)rows * d);
+        xin = sc->xn;
+    }
+    gemm_rows(xin, d, m->hw1, d, d, m->hb1, ACT_RELU, NULL, 0, sc->hh, d, rows);
+    if (m->bf16) bf16_round(sc->hh, (size_t)rows * d);
     gemm_rows(sc->hh, d, m->hw2, d, 256, add_bias ? m->hb2 : NULL, ACT_NONE, NULL, 0, logits, 256, rows);
 }
 

@@ -113,6 +113,15 @@ typedef struct ref_state ref_state;
  * fp32).  Returns NULL and fills err on failure (size mismatch included). */
 ref_model* ref_model_load(const char* path, int32_t d_model, int32_t n_layers,
                           int32_t d_state, char* err, int32_t err_len);
+/* bf16 mode (BASELINE configs 3 and 5; beyond the reference, whose path is
+ * fp32): the Linear weights are rounded to bf16 once, and every activation
+ * is rounded to bf16 where the GPU path stores it in bf16 -- after LN1,
+ * in_proj, conv, x_proj, the scan, out_proj, LN2, FF1 and head1, and the
+ * copy of x that head1 reads.  The residual stream x, the recurrent state
+ * and the logits stay fp32; GEMMs accumulate in fp32. */
+int32_t ref_model_set_bf16(ref_model* m);
+uint16_t ref_f32_to_bf16(float x);
+float ref_bf16_to_f32(uint16_t h);
 void ref_model_free(ref_model* m);
 int64_t ref_model_expected_bytes(int32_t d_model, int32_t n_layers, int32_t d_state,
                                  int32_t fp16);

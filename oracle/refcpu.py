@@ -81,6 +81,9 @@ def lib():
             "ref_cdf_quantize": (None, [f64p, u32p]),
             "ref_cdf_search": (C.c_int32, [f64p, C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
             "ref_model_load": (P, [C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.c_char_p, C.c_int32]),
+            "ref_model_set_bf16": (C.c_int32, [P]),
+            "ref_f32_to_bf16": (C.c_uint16, [C.c_float]),
+            "ref_bf16_to_f32": (C.c_float, [C.c_uint16]),
             "ref_model_free": (None, [P]),
             "ref_model_expected_bytes": (C.c_int64, [C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
             "ref_state_new": (P, [P, C.c_int32]),
@@ -146,13 +149,15 @@ def decode_cdf_stream(cdf, n_sym, words):
 
 
 class Model:
-    def __init__(self, path, d_model, n_layers, d_state=16):
+    def __init__(self, path, d_model, n_layers, d_state=16, bf16=False):
         err = C.create_string_buffer(512)
         h = lib().ref_model_load(str(path).encode(), d_model, n_layers, d_state, err, 512)
         if not h:
             raise ValueError(err.value.decode())
         self.h = h
         self.d_model, self.n_layers, self.d_state = d_model, n_layers, d_state
+        if bf16:
+            lib().ref_model_set_bf16(h)
 
     def close(self):
         if self.h:

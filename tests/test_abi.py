@@ -31,5 +31,5 @@ def test_create_rejects_bad_configs():
                 boa_hip.Config(80, 8, 16, 10, 0, 0, 1.0),    # d_model not a power of two
                 boa_hip.Config(256, 8, 24, 10, 0, 0, 1.0),   # d_state
                 boa_hip.Config(256, 8, 16, 0, 0, 0, 1.0),    # lanes
-                boa_hip.Config(256, 8, 16, 10, 0, 1, 1.0)]:  # precision
+                boa_hip.Config(256, 8, 16, 10, 0, 2, 1.0)]:  # precision
         assert boa_hip.lib().boa_create(ctypes.byref(bad), ctypes.byref(h)) == -1

@@ -229,3 +229,33 @@ def test_real_checkpoint_round_trip(oracle, weights_dir):
     zblob = m.compress(zeros, chunk_size=4096)
     assert m.decompress(zblob) == zeros
     assert len(zblob) * 1.3 < len(zeros)
+
+
+def test_bf16_rounding_kats(oracle):
+    to = oracle.lib().ref_f32_to_bf16
+    f = lambda u: np.array([u], np.uint32).view(np.float32)[0]
+    assert to(1.0) == 0x3F80
+    assert to(f(0x3F808000)) == 0x3F80          # tie -> even
+    assert to(f(0x3F818000)) == 0x3F82          # tie -> even (odd below)
+    assert to(f(0x3F808001)) == 0x3F81          # above the tie
+    assert to(f(0x7F7FFFFF)) == 0x7F80          # rounds up to +inf
+    assert to(f(0x7FC00001)) & 0x7FC0 == 0x7FC0  # NaN stays NaN
+    v = np.random.default_rng(3).standard_normal(10000).astype(np.float32)
+    bits = np.array([to(float(x)) for x in v], np.uint32) << 16
+    back = bits.view(np.float32)
+    assert np.all(np.abs(back - v) <= np.abs(v) * 2.0 ** -8)
+
+
+def test_bf16_model_close_to_fp32_and_chunk_equals_step(oracle, w_c1):
+    tok = np.random.default_rng(9).integers(0, 256, size=(3, 50), dtype=np.uint8)
+    a = oracle.Model(w_c1, 64, 2).new_state(3).forward_chunk(tok)
+    m16 = oracle.Model(w_c1, 64, 2, bf16=True)
+    b = m16.new_state(3).forward_chunk(tok)
+    assert not np.array_equal(a, b)
+    assert np.abs(a - b).max() <= 2e-2 * np.abs(a).max()
+    st = m16.new_state(3)
+    step = np.stack([st.step(tok[:, t]) for t in range(50)], 1)
+    assert np.array_equal(b.view(np.uint32), step.view(np.uint32))
+    data = synth.gen_c1()[:3000]
+    blob = m16.compress(data, chunk_size=700)
+    assert m16.decompress(blob) == data
