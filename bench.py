@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X codec path on BASELINE config 2.
+"""Benchmark of the MI355X codec path on BASELINE config 2 (other configs with --config).
 
 Workload: Mamba d_model=256, 8 layers, d_state=16,
 fp32, random-init weights (seed 0); 64 MiB of interleaved float32 records
@@ -29,9 +29,10 @@ sys.path.insert(0, os.path.join(ROOT, "boa-constrictor_amd"))
 
 METRIC = ("compress & decompress input MB/s at d256×8L, 1000 chunks; "
           "compression ratio")
-PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+PEAK_TFLOPS = {"fp32": 157.3, "bf16": 2500.0}  # MI355X dense matrix peaks
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E peak
-GEMM_KERNEL = "boa::gemm_f32_kernel<128, 256, 4, 4, 16>"
+GEMM_KERNEL = {"fp32": "boa::gemm_f32_kernel<128, 256, 4, 4, 16>",
+               "bf16": "boa::gemm_bf16_kernel<256, 256, 4, 4, 64>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_c2_traffic.json")
 
 
@@ -73,12 +74,13 @@ def container_bytes(stream_bytes, n_chunks) -> int:
     return 33 + int(sum(stream_bytes)) + 4 + n_chunks + sum(uvarint_len(int(x)) for x in stream_bytes) + 4
 
 
-def cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, sample_len, threads, d, L, ds):
+def cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, sample_len, threads, d, L, ds,
+                 bf16=False):
     """Time the CPU oracle on the first `sample_chunks` chunks x `sample_len` bytes."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import refcpu
     sample = b"".join(data[c * chunk: c * chunk + sample_len] for c in range(min(sample_chunks, n_chunks)))
-    m = refcpu.Model(weights, d, L, ds)
+    m = refcpu.Model(weights, d, L, ds, bf16=bf16)
     t0 = time.perf_counter()
     blob = m.compress(sample, chunk_size=sample_len, n_threads=threads)
     t1 = time.perf_counter()
@@ -97,7 +99,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1)
     ap.add_argument("--warmup", type=int, default=0)
-    ap.add_argument("--chunks", type=int, default=1000)
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c5"],
+                    help="BASELINE config (c2 is the metric's config)")
+    ap.add_argument("--chunks", type=int, default=0)
     ap.add_argument("--chunk-len", type=int, default=0,
                     help="probe only: shorten every chunk to this many bytes (not the metric config)")
     ap.add_argument("--tile", type=int, default=0)
@@ -126,24 +130,26 @@ def main() -> int:
     import synth
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
-    d, L, ds = 256, 8, 16
+    cfg = synth.CONFIGS[args.config]
+    d, L, ds, prec = cfg["d_model"], cfg["n_layers"], cfg["d_state"], cfg["precision"]
     tmp = tempfile.mkdtemp(prefix="boa_bench_")
-    weights = os.path.join(tmp, "c2_d256_L8_seed0.bin")
+    weights = os.path.join(tmp, f"{args.config}_d{d}_L{L}_seed0.bin")
     synth.write_random_weights(weights, d, L, ds, seed=0)
-    data = synth.gen_c2()
-    n_chunks = args.chunks
+    data = cfg["gen"]()
+    n_chunks = args.chunks or cfg["chunks"]
     chunk = synth.chunk_size_for(len(data), n_chunks)
-    workload = "c2"
+    workload = args.config
     if args.chunk_len:
+        full = chunk
         chunk = args.chunk_len
-        data = b"".join(data[c * synth.chunk_size_for(len(data), n_chunks):][:chunk] for c in range(n_chunks))
-        workload = f"c2-probe-{chunk}B-chunks"
+        data = b"".join(data[c * full: c * full + chunk] for c in range(n_chunks))
+        workload = f"{args.config}-probe-{chunk}B-chunks"
     n = len(data)
     n_chunks = math.ceil(n / chunk)
     print(f"[bench] {workload}: {n} bytes, {n_chunks} chunks of {chunk} B", file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream()
-    codec = boa_hip.Codec(d, L, ds, max_lanes=n_chunks, tile=args.tile)
+    codec = boa_hip.Codec(d, L, ds, max_lanes=n_chunks, tile=args.tile, precision=prec)
     codec.set_stream(stream.cuda_stream)
     codec.load_weights(weights)
     d_data = torch.frombuffer(bytearray(data), dtype=torch.uint8).cuda()
@@ -209,12 +215,12 @@ def main() -> int:
     kernel_ms = {k: round(v["ms"], 3) for k, v in prof.items()}
     roofline = {
         "bound": "mfma",
-        "kernel": GEMM_KERNEL,
+        "kernel": GEMM_KERNEL[prec],
         "achieved": round(gemm_tflops, 2),
-        "peak": PEAK_FP32_TFLOPS,
+        "peak": PEAK_TFLOPS[prec],
         "unit": "TFLOP/s",
-        "frac": round(gemm_tflops / PEAK_FP32_TFLOPS, 4),
-        "traffic": gemm_traffic_bytes(),
+        "frac": round(gemm_tflops / PEAK_TFLOPS[prec], 4),
+        "traffic": gemm_traffic_bytes() if workload == "c2" else None,
         "launches": g["launches"],
         "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4),
         "flop_per_launch": round(g["work"] / max(g["launches"], 1)),
@@ -223,7 +229,7 @@ def main() -> int:
     scan_gbs = sc["work"] / (sc["ms"] * 1e-3) / 1e9 if sc["ms"] > 0 else 0.0
     roofline_scan = {
         "bound": "hbm",
-        "kernel": "boa::scan_chunk_kernel<16, 16>",
+        "kernel": f"boa::scan_chunk_kernel<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>",
         "achieved": round(scan_gbs, 1),
         "peak": PEAK_HBM_GBS,
         "unit": "GB/s",
@@ -254,7 +260,7 @@ def main() -> int:
         print(f"[bench] cpu baseline: {sample_chunks} chunks x {args.cpu_sample_len} B on {threads} threads",
               file=sys.stderr, flush=True)
         cb = cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, args.cpu_sample_len,
-                          threads, d, L, ds)
+                          threads, d, L, ds, bf16=prec == "bf16")
         cpu = {"value": round(cb["compress_mb_s"], 5), "unit": "MB/s", "cores": threads,
                "kind": "port",
                "sample": f"first {args.cpu_sample_len} B of each of the first {sample_chunks} chunks "
@@ -273,11 +279,12 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if prec == "fp32" else "bf16",
         "data": "synthetic",
         "config": {"workload": workload, "d_model": d, "n_layers": L, "d_state": ds,
                    "chunks": n_chunks, "chunk_len": chunk, "input_bytes": n,
-                   "weights": "random-init seed 0", "input": "synth.gen_c2 (seed 2)"},
+                   "precision": prec, "weights": "random-init seed 0",
+                   "input": f"synth.gen_{args.config}"},
         "compress_mb_s": round(comp_mb_s, 4),
         "decompress_mb_s": round(dec_mb_s, 4) if dec_mb_s else None,
         "compression_ratio": round(ratio, 5),

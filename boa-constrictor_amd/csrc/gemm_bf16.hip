@@ -169,9 +169,12 @@ static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 
 }
 
 // W must hold round_up(N, 256) rows (zero padded) for every configuration.
+// Chosen from a sweep on MI355X at compress shapes (M ~ 10^6): 256x256 with
+// 16 waves of 64x64 (the LDS traffic per MFMA halves against 32x64 waves) for
+// N >= 256, 128x64 with 8 waves for the narrow x_proj.
 hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
-  if (a.N >= 256) return launch_b16<128, 256, 4, 4, 64>(a, s);
+  if (a.N >= 256) return launch_b16<256, 256, 4, 4, 64>(a, s);
   return launch_b16<128, 64, 4, 2, 64>(a, s);
 }
 

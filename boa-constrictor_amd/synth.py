@@ -198,9 +198,13 @@ def gen_c5(n: int = 268_435_456) -> bytes:
     return x.astype("<f4").tobytes()
 
 
+# model shape, precision, chunk count, input generator
 CONFIGS = {
-    "c1": dict(d_model=64, n_layers=2, d_state=16, chunks=64, gen=gen_c1),
-    "c2": dict(d_model=256, n_layers=8, d_state=16, chunks=1000, gen=gen_c2),
+    "c1": dict(d_model=64, n_layers=2, d_state=16, precision="fp32", chunks=64, gen=gen_c1),
+    "c2": dict(d_model=256, n_layers=8, d_state=16, precision="fp32", chunks=1000, gen=gen_c2),
+    "c3": dict(d_model=256, n_layers=8, d_state=16, precision="bf16", chunks=8192, gen=gen_c3),
+    "c4": dict(d_model=256, n_layers=8, d_state=16, precision="fp32", chunks=4096, gen=gen_c4),
+    "c5": dict(d_model=512, n_layers=12, d_state=32, precision="bf16", chunks=16384, gen=gen_c5),
 }
 
 
