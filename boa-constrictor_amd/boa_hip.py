@@ -65,6 +65,7 @@ def lib():
             "boa_set_stream": (C.c_int, [P, P]),
             "boa_use_own_stream": (C.c_int, [P]),
             "boa_set_temperature": (C.c_int, [P, f32]),
+            "boa_set_warm_start": (C.c_int, [P, i32]),
             "boa_load_weights": (C.c_int, [P, C.c_char_p]),
             "boa_load_weights_mem": (C.c_int, [P, P, C.c_size_t]),
             "boa_weight_file_bytes": (i64, [i32, i32, i32, i32]),
@@ -187,6 +188,10 @@ class Codec:
                                                 lens.ctypes.data, fb.ctypes.data, len(fb),
                                                 chunk_len, last_len, _ptr(d_out)),
                     "decompress_device")
+
+    def set_warm_start(self, interleave_batch):
+        """--warm-start (boa.cpp:310-319): 0 turns it off."""
+        self._check(lib().boa_set_warm_start(self.h, int(interleave_batch)), "set_warm_start")
 
     def compress(self, data: bytes, chunk_size=4096, max_chunks=0) -> bytes:
         import numpy as np

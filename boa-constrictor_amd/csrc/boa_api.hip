@@ -46,6 +46,7 @@ struct boa_ctx {
   std::string err;
   bool loaded = false;
   float inv_temp = 1.0f;
+  int32_t warm_batch = 0;  // warm-start interleave batch; 0 = every chunk starts cold
 
   // weights (one device allocation)
   bool bf16 = false;  // precision 1: bf16 weights and activations
@@ -273,7 +274,7 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
   const double ln_bytes = 3.0 * 4 * rows * D.d;
   hipError_t e = timed(c, BOA_K_LN, ln_bytes, [&] {
     return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, true, s)
-                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
+                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
                                W.ln1_b, rows, D.d, true, s);
   });
   if (!e) e = gemmb(c, c->xn, B.w_in, c->xz, 2 * D.di, true, nullptr, W.b_in, nullptr, 0, rows,
@@ -316,7 +317,7 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
   e = timed(c, BOA_K_LN, ln_bytes, [&] {
     return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
                                false, s)
-                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
+                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
                                W.ln1_b, rows, D.d, false, s);
   });
   if (e) return e;
@@ -767,6 +768,12 @@ int boa_set_temperature(boa_ctx* c, float t) {
   return BOA_OK;
 }
 
+int boa_set_warm_start(boa_ctx* c, int32_t interleave_batch) {
+  if (!c || interleave_batch < 0) return BOA_E_ARG;
+  c->warm_batch = interleave_batch;
+  return BOA_OK;
+}
+
 int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
   if (!c || !data) return BOA_E_ARG;
   const Dims& D = c->D;
@@ -1024,7 +1031,7 @@ int boa_forward_chunk(boa_ctx* c, const uint8_t* d_tokens, int32_t lanes, int32_
   if (!d_tokens || !d_logits || lanes < 1 || lanes > c->cfg.max_lanes || T < 1)
     return fail(c, BOA_E_ARG, "boa_forward_chunk: bad arguments");
   if ((rc = ensure_rows(c, (int64_t)lanes * T))) return rc;
-  TokenSrc tok{d_tokens, T, (int64_t)lanes * T};
+  TokenSrc tok{d_tokens, T, (int64_t)lanes * T, T};
   HIP_TRY(c, forward_tile(c, tok, lanes, T, 0, d_logits));
   return BOA_OK;
 }
@@ -1076,6 +1083,15 @@ int64_t boa_payload_bound_words(int64_t n, int64_t chunk, int32_t max_chunks) {
   return nc * pitch_words_for(chunk);
 }
 
+// Lanes of one batch iteration.  Cold: chunks u0 .. u0+G-1.  Warm-start
+// (boa.cpp:395-401, 414): unit u runs chunk u*S + i at iteration i, and the
+// units whose chunk exists lead the group.
+static int iter_lanes(bool warm, int64_t nc, int64_t S, int64_t u0, int G, int64_t i) {
+  if (!warm) return G;
+  const int64_t live = (nc - i + S - 1) / S - u0;  // units u with u*S + i < nc, minus u0
+  return (int)std::max<int64_t>(0, std::min<int64_t>(G, live));
+}
+
 int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t chunk,
                         int32_t max_chunks, uint32_t* d_payload, int64_t payload_cap_words,
                         uint64_t* h_stream_bytes, uint8_t* h_first, int64_t* h_payload_words) {
@@ -1085,61 +1101,111 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
       chunk > (1 << 30))
     return fail(c, BOA_E_ARG, "boa_compress_device: bad arguments");
   const int64_t nc = boa_num_chunks(n, chunk, max_chunks);
+  if (nc > INT32_MAX) return fail(c, BOA_E_ARG, "boa_compress_device: too many chunks");
+  if (h_payload_words) *h_payload_words = 0;
+  if (nc == 0) return BOA_OK;
   const int B = c->cfg.max_lanes;
   const int64_t pitch = pitch_words_for(chunk);
-  const int64_t T = auto_tile(c, chunk, (int)std::min<int64_t>(B, std::max<int64_t>(nc, 1)));
+  // warm-start: W lanes of S consecutive chunks each (boa.cpp:310-319)
+  const bool warm = c->warm_batch > 0;
+  const int64_t W = warm ? std::min<int64_t>(c->warm_batch, nc) : 0;
+  const int64_t S = warm ? (nc + W - 1) / W : 1;
+  const int64_t units = warm ? W : nc;
+  const int64_t T = auto_tile(c, chunk, (int)std::min<int64_t>(B, units));
   if ((rc = ensure_rows(c, (int64_t)B * T))) return rc;
   if ((rc = ensure_words(c, pitch))) return rc;
-  uint8_t* d_first = nullptr;
-  if (dalloc(&d_first, (size_t)B)) return fail(c, BOA_E_NOMEM, "allocation failed");
-  int64_t out_words = 0;
   hipStream_t s = c->stream;
-  for (int64_t c0 = 0; c0 < nc; c0 += B) {
-    const int lanes = (int)std::min<int64_t>(B, nc - c0);
-    const TokenSrc tok{d_data + c0 * chunk, chunk, n - c0 * chunk};
-    if ((rc = boa_reset_state(c, lanes))) { dfree(d_first); return rc; }
-    hipError_t e = launch_rc_enc_init(c->enc, lanes, s);
-    if (e) { dfree(d_first); return hip_fail(c, e, "rc init"); }
-    for (int64_t t0 = 0; t0 < chunk; t0 += T) {
-      const int Tt = (int)std::min<int64_t>(T, chunk - t0);
-      e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
-      if (!e)
-        e = timed(c, BOA_K_CDF, 1024.0 * lanes * Tt, [&] {
-          return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
-                                           c->lowprob, s);
-        });
-      if (!e)
-        e = timed(c, BOA_K_CODER, 8.0 * lanes * Tt, [&] {
-          return launch_rc_encode_tile(c->lowprob, tok, Tt, (int)t0, lanes, c->enc, c->words,
-                                       pitch, s);
-        });
-      if (e) { dfree(d_first); return hip_fail(c, e, "compress tile"); }
-    }
-    e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
-    if (!e) e = hipMemcpyAsync(c->h_sizes, c->sizes, sizeof(int32_t) * lanes, hipMemcpyDeviceToHost, s);
-    if (!e) e = hipStreamSynchronize(s);
-    if (e) { dfree(d_first); return hip_fail(c, e, "finish"); }
-    int64_t batch_words = 0;
-    for (int b = 0; b < lanes; ++b) batch_words += c->h_sizes[b];
-    if (out_words + batch_words > payload_cap_words) {
-      dfree(d_first);
-      return fail(c, BOA_E_ARG, "payload buffer too small");
-    }
-    e = timed(c, BOA_K_CODER, 8.0 * batch_words, [&] {
-      return launch_compact(c->words, pitch, c->sizes, lanes, c->offsets, d_payload + out_words, s);
-    });
-    if (!e) {
-      hipLaunchKernelGGL(gather_first_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, tok.base,
-                         tok.stride, tok.total, lanes, d_first);
-      e = hipGetLastError();
-    }
-    if (!e) e = hipMemcpyAsync(h_first + c0, d_first, lanes, hipMemcpyDeviceToHost, s);
-    if (!e) e = hipStreamSynchronize(s);
-    if (e) { dfree(d_first); return hip_fail(c, e, "compaction"); }
-    for (int b = 0; b < lanes; ++b) h_stream_bytes[c0 + b] = 4ull * (uint64_t)c->h_sizes[b];
-    out_words += batch_words;
-  }
+  uint8_t* d_first = nullptr;
+  if (dalloc(&d_first, (size_t)nc)) return fail(c, BOA_E_NOMEM, "allocation failed");
+  hipLaunchKernelGGL(gather_first_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s,
+                     d_data, chunk, n, (int)nc, d_first);
+  hipError_t e = hipGetLastError();
+  if (!e) e = hipMemcpyAsync(h_first, d_first, (size_t)nc, hipMemcpyDeviceToHost, s);
+  if (!e) e = hipStreamSynchronize(s);
   dfree(d_first);
+  if (e) return hip_fail(c, e, "first bytes");
+  // warm-start: where each chunk's stream landed in the iteration-ordered payload
+  std::vector<uint64_t> stage_off(warm ? (size_t)nc : 0);
+  int64_t out_words = 0;
+  for (int64_t u0 = 0; u0 < units; u0 += B) {
+    const int G = (int)std::min<int64_t>(B, units - u0);
+    for (int64_t i = 0; i < S; ++i) {
+      const int lanes = iter_lanes(warm, nc, S, u0, G, i);
+      if (lanes == 0) break;
+      const int64_t c0 = warm ? u0 * S + i : u0;  // chunk of lane 0
+      const TokenSrc tok{d_data + c0 * chunk, warm ? S * chunk : chunk, n - c0 * chunk, chunk};
+      // warm-start keeps the state across a unit's chunks (boa.cpp:432-435)
+      if (i == 0 && (rc = boa_reset_state(c, G))) return rc;
+      e = launch_rc_enc_init(c->enc, lanes, s);
+      if (e) return hip_fail(c, e, "rc init");
+      for (int64_t t0 = 0; t0 < chunk; t0 += T) {
+        const int Tt = (int)std::min<int64_t>(T, chunk - t0);
+        e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
+        if (!e)
+          e = timed(c, BOA_K_CDF, 1024.0 * lanes * Tt, [&] {
+            return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
+                                             c->lowprob, s);
+          });
+        if (!e)
+          e = timed(c, BOA_K_CODER, 8.0 * lanes * Tt, [&] {
+            return launch_rc_encode_tile(c->lowprob, tok, Tt, (int)t0, lanes, c->enc, c->words,
+                                         pitch, s);
+          });
+        if (e) return hip_fail(c, e, "compress tile");
+      }
+      e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
+      if (!e) e = hipMemcpyAsync(c->h_sizes, c->sizes, sizeof(int32_t) * lanes, hipMemcpyDeviceToHost, s);
+      if (!e) e = hipStreamSynchronize(s);
+      if (e) return hip_fail(c, e, "finish");
+      int64_t batch_words = 0;
+      for (int b = 0; b < lanes; ++b) batch_words += c->h_sizes[b];
+      if (out_words + batch_words > payload_cap_words)
+        return fail(c, BOA_E_ARG, "payload buffer too small");
+      e = timed(c, BOA_K_CODER, 8.0 * batch_words, [&] {
+        return launch_compact(c->words, pitch, c->sizes, lanes, c->offsets, d_payload + out_words, s);
+      });
+      if (!e) e = hipStreamSynchronize(s);
+      if (e) return hip_fail(c, e, "compaction");
+      int64_t at = out_words;
+      for (int b = 0; b < lanes; ++b) {
+        const int64_t ci = warm ? (u0 + b) * S + i : u0 + b;
+        h_stream_bytes[ci] = 4ull * (uint64_t)c->h_sizes[b];
+        if (warm) stage_off[(size_t)ci] = (uint64_t)at;
+        at += c->h_sizes[b];
+      }
+      out_words += batch_words;
+    }
+  }
+  if (warm && S > 1 && out_words > 0) {
+    // the container stores streams in chunk order (boa.cpp:560-565)
+    std::vector<uint64_t> dst_off((size_t)nc);
+    std::vector<int32_t> sizes((size_t)nc);
+    uint64_t at = 0;
+    for (int64_t ci = 0; ci < nc; ++ci) {
+      dst_off[(size_t)ci] = at;
+      sizes[(size_t)ci] = (int32_t)(h_stream_bytes[ci] / 4);
+      at += sizes[(size_t)ci];
+    }
+    uint32_t* tmp = nullptr;
+    uint64_t* d_off = nullptr;
+    int32_t* d_sz = nullptr;
+    if (dalloc(&tmp, (size_t)out_words) || dalloc(&d_off, 2 * (size_t)nc) ||
+        dalloc(&d_sz, (size_t)nc)) {
+      dfree(tmp); dfree(d_off);
+      return fail(c, BOA_E_NOMEM, "allocation failed");
+    }
+    e = hipMemcpyAsync(d_off, stage_off.data(), 8 * (size_t)nc, hipMemcpyHostToDevice, s);
+    if (!e) e = hipMemcpyAsync(d_off + nc, dst_off.data(), 8 * (size_t)nc, hipMemcpyHostToDevice, s);
+    if (!e) e = hipMemcpyAsync(d_sz, sizes.data(), 4 * (size_t)nc, hipMemcpyHostToDevice, s);
+    if (!e)
+      e = timed(c, BOA_K_CODER, 8.0 * out_words, [&] {
+        return launch_gather_streams(d_payload, d_off, d_off + nc, d_sz, nc, tmp, s);
+      });
+    if (!e) e = hipMemcpyAsync(d_payload, tmp, 4 * (size_t)out_words, hipMemcpyDeviceToDevice, s);
+    if (!e) e = hipStreamSynchronize(s);
+    dfree(tmp); dfree(d_off); dfree(d_sz);
+    if (e) return hip_fail(c, e, "warm-start reorder");
+  }
   if (h_payload_words) *h_payload_words = out_words;
   return BOA_OK;
 }
@@ -1152,44 +1218,65 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
   if (!d_payload || !h_offsets_words || !h_stream_bytes || !h_first || !d_out || nc < 0 ||
       chunk < 1 || last_len < 0 || last_len > chunk)
     return fail(c, BOA_E_ARG, "boa_decompress_device: bad arguments");
+  if (nc == 0) return BOA_OK;
   const int B = c->cfg.max_lanes;
+  const bool warm = c->warm_batch > 0;
+  const int64_t W = warm ? std::min<int64_t>(c->warm_batch, nc) : 0;
+  const int64_t S = warm ? (nc + W - 1) / W : 1;
+  const int64_t units = warm ? W : nc;
   hipStream_t s = c->stream;
   std::vector<uint64_t> offs(B);
   std::vector<int32_t> nw(B), lens(B);
+  std::vector<uint8_t> first(B);
   uint8_t* d_first = nullptr;
   if (dalloc(&d_first, (size_t)B)) return fail(c, BOA_E_NOMEM, "allocation failed");
   const int64_t pitch_bytes = pitch_words_for(chunk) * 4;
-  for (int64_t c0 = 0; c0 < nc; c0 += B) {
-    const int lanes = (int)std::min<int64_t>(B, nc - c0);
-    int32_t maxlen = 0;
-    for (int b = 0; b < lanes; ++b) {
-      const int64_t ci = c0 + b;
-      if ((int64_t)h_stream_bytes[ci] > pitch_bytes) {
-        dfree(d_first);
-        return fail(c, BOA_E_FORMAT, "stream too large for the chunk length");
+  for (int64_t u0 = 0; u0 < units; u0 += B) {
+    const int G = (int)std::min<int64_t>(B, units - u0);
+    for (int64_t i = 0; i < S; ++i) {
+      const int lanes = iter_lanes(warm, nc, S, u0, G, i);
+      if (lanes == 0) break;
+      int32_t maxlen = 0;
+      for (int b = 0; b < lanes; ++b) {
+        const int64_t ci = warm ? (u0 + b) * S + i : u0 + b;
+        if ((int64_t)h_stream_bytes[ci] > pitch_bytes) {
+          dfree(d_first);
+          return fail(c, BOA_E_FORMAT, "stream too large for the chunk length");
+        }
+        offs[b] = h_offsets_words[ci];
+        nw[b] = (int32_t)(h_stream_bytes[ci] / 4);
+        lens[b] = (int32_t)(ci == nc - 1 ? last_len : chunk);
+        first[b] = h_first[ci];
+        maxlen = std::max(maxlen, lens[b]);
       }
-      offs[b] = h_offsets_words[ci];
-      nw[b] = (int32_t)(h_stream_bytes[ci] / 4);
-      lens[b] = (int32_t)(ci == nc - 1 ? last_len : chunk);
-      maxlen = std::max(maxlen, lens[b]);
+      hipError_t e = hipMemcpyAsync(c->offsets, offs.data(), 8 * lanes, hipMemcpyHostToDevice, s);
+      if (!e) e = hipMemcpyAsync(c->sizes, nw.data(), 4 * lanes, hipMemcpyHostToDevice, s);
+      if (!e) e = hipMemcpyAsync(c->lens, lens.data(), 4 * lanes, hipMemcpyHostToDevice, s);
+      if (!e) e = hipMemcpyAsync(d_first, first.data(), lanes, hipMemcpyHostToDevice, s);
+      if (e) { dfree(d_first); return hip_fail(c, e, "decode upload"); }
+      // warm-start resets the state only before a unit's first chunk (boa.cpp:690-693)
+      if (i == 0 && (rc = boa_reset_state(c, G))) { dfree(d_first); return rc; }
+      const int64_t c0 = warm ? u0 * S + i : u0;
+      const int64_t stride = warm ? S * chunk : chunk;
+      uint8_t* out = d_out + c0 * chunk;
+      hipLaunchKernelGGL(decode_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, d_first,
+                         c->lens, c->tok, out, stride, lanes, c->t_counter);
+      e = hipGetLastError();
+      if (!e) e = launch_rc_dec_init(c->dec, d_payload, c->offsets, c->sizes, lanes, s);
+      if (!e) e = ensure_state_layout(c, 1);
+      if (e) { dfree(d_first); return hip_fail(c, e, "decode init"); }
+      e = decode_steps(c, lanes, maxlen, out, stride, d_payload);
+      if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }
+      // The compressor's state consumed every byte of the chunk; the units
+      // that go on feed the last decoded byte before their next chunk.
+      const int next = warm && i + 1 < S ? iter_lanes(warm, nc, S, u0, G, i + 1) : 0;
+      if (next > 0) {
+        e = step_forward(c, c->tok, next, false, c->dlogits);
+        if (e) { dfree(d_first); return hip_fail(c, e, "warm-start carry step"); }
+      }
+      e = hipStreamSynchronize(s);
+      if (e) { dfree(d_first); return hip_fail(c, e, "decode sync"); }
     }
-    hipError_t e = hipMemcpyAsync(c->offsets, offs.data(), 8 * lanes, hipMemcpyHostToDevice, s);
-    if (!e) e = hipMemcpyAsync(c->sizes, nw.data(), 4 * lanes, hipMemcpyHostToDevice, s);
-    if (!e) e = hipMemcpyAsync(c->lens, lens.data(), 4 * lanes, hipMemcpyHostToDevice, s);
-    if (!e) e = hipMemcpyAsync(d_first, h_first + c0, lanes, hipMemcpyHostToDevice, s);
-    if (e) { dfree(d_first); return hip_fail(c, e, "decode upload"); }
-    if ((rc = boa_reset_state(c, lanes))) { dfree(d_first); return rc; }
-    uint8_t* out = d_out + c0 * chunk;
-    hipLaunchKernelGGL(decode_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, d_first,
-                       c->lens, c->tok, out, chunk, lanes, c->t_counter);
-    e = hipGetLastError();
-    if (!e) e = launch_rc_dec_init(c->dec, d_payload, c->offsets, c->sizes, lanes, s);
-    if (!e) e = ensure_state_layout(c, 1);
-    if (e) { dfree(d_first); return hip_fail(c, e, "decode init"); }
-    e = decode_steps(c, lanes, maxlen, out, chunk, d_payload);
-    if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }
-    e = hipStreamSynchronize(s);
-    if (e) { dfree(d_first); return hip_fail(c, e, "decode sync"); }
   }
   dfree(d_first);
   return BOA_OK;
@@ -1230,6 +1317,12 @@ int boa_compress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, int64_t chun
   h.chunk_len = (uint32_t)chunk;
   h.n_chunks = (uint32_t)nc;
   h.last_chunk_len = (uint32_t)(nc > 1 ? processed - (nc - 1) * chunk : processed);
+  if (c->warm_batch > 0) {  // flags bit 0 + u32 interleave batch (boa.cpp:542-559)
+    const uint32_t W = (uint32_t)std::min<int64_t>(c->warm_batch, nc);
+    h.flags = 1u;
+    h.fp.resize(4);
+    memcpy(h.fp.data(), &W, 4);
+  }
   std::vector<uint8_t> blob;
   boa2_write(h, payload, first.data(), lens.data(), (size_t)nc, blob);
   uint8_t* o = (uint8_t*)malloc(blob.size() ? blob.size() : 1);
@@ -1248,8 +1341,11 @@ int boa_decompress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, uint8_t** 
   Boa2Parsed P;
   std::string why;
   if (!boa2_parse(h_in, (size_t)n, P, why)) return fail(c, BOA_E_FORMAT, why);
-  if (P.hdr.flags & 1u) return fail(c, BOA_E_FORMAT, "warm-start containers are not supported");
   const size_t nc = P.hdr.n_chunks;
+  // warm-start: the interleave batch comes from the header (boa.cpp:603-610)
+  const bool warm = (P.hdr.flags & 1u) != 0;
+  if (warm && nc > 0 && P.interleave_batch == 0)
+    return fail(c, BOA_E_FORMAT, "warm-start container without a valid interleave batch");
   if (nc == 0) {  // empty input
     *h_out = (uint8_t*)malloc(1);
     if (!*h_out) return fail(c, BOA_E_NOMEM, "host allocation failed");
@@ -1277,8 +1373,11 @@ int boa_decompress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, uint8_t** 
   }
   hipError_t e = hipMemcpy(d_pay, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
   if (e) { dfree(d_pay); dfree(d_out); return hip_fail(c, e, "upload"); }
+  const int32_t saved_warm = c->warm_batch;
+  c->warm_batch = warm ? (int32_t)P.interleave_batch : 0;
   rc = boa_decompress_device(c, d_pay, offs.data(), lens.data(), P.first.data(), (int32_t)nc,
                              P.hdr.chunk_len, nc ? P.hdr.last_chunk_len : 0, d_out);
+  c->warm_batch = saved_warm;
   if (rc) { dfree(d_pay); dfree(d_out); return rc; }
   uint8_t* o = (uint8_t*)malloc((size_t)std::max<int64_t>(total, 1));
   if (!o) { dfree(d_pay); dfree(d_out); return fail(c, BOA_E_NOMEM, "host allocation failed"); }

@@ -5,10 +5,12 @@
 //   boa <compress|decompress> <model.bin> <input> <output> [d_model=256]
 //       [n_layers=1] [--gpu-batch B] [--max-chunks C] [--chunk-size S]
 //       [--tile T] [--temperature T] [--backbone mamba] [--show-timings]
-//       [--no-graph] [--d-state N] [--precision fp32|bf16]
+//       [--no-graph] [--warm-start] [--d-state N] [--precision fp32|bf16]
 // --gpu-batch 0 (default) sizes the batch from free device memory like
-// auto_size_params (boa.cpp:109-156).  --warm-start is rejected (see the
-// design notes); --measure-energy is not provided.
+// auto_size_params (boa.cpp:109-156).  --warm-start interleaves chunks over
+// the batch's lanes and carries state across them (boa.cpp:310-319); the
+// decoder takes the interleave batch from the container.  --measure-energy
+// is not provided.
 #include <hip/hip_runtime.h>
 
 #include <chrono>
@@ -24,7 +26,7 @@ static int usage() {
   fprintf(stderr,
           "Usage: boa <compress|decompress> <model> <input> <output> [d_model] [n_layers] "
           "[--gpu-batch B] [--max-chunks C] [--chunk-size S] [--tile T] [--temperature T] "
-          "[--d-state N] [--precision fp32|bf16] [--show-timings]\n");
+          "[--warm-start] [--d-state N] [--precision fp32|bf16] [--show-timings]\n");
   return 1;
 }
 
@@ -59,7 +61,7 @@ int main(int argc, char** argv) {
   int gpu_batch = 0, max_chunks = -1, tile = 0, d_state = 16, precision = 0;
   long long chunk = 4096;
   float temperature = 1.0f;
-  bool show_timings = false;
+  bool show_timings = false, warm_start = false;
   for (int i = 1; i < argc; ++i) {
     std::string s = argv[i];
     auto next = [&](const char* name) -> const char* {
@@ -85,10 +87,8 @@ int main(int argc, char** argv) {
       }
     } else if (s == "--show-timings") show_timings = true;
     else if (s == "--no-graph" || s == "--gpu") continue;
-    else if (s == "--warm-start") {
-      fprintf(stderr, "--warm-start is not supported by this build\n");
-      return 1;
-    } else if (s.rfind("--", 0) == 0) fprintf(stderr, "Warning: Unknown flag '%s' ignored.\n", s.c_str());
+    else if (s == "--warm-start") warm_start = true;
+    else if (s.rfind("--", 0) == 0) fprintf(stderr, "Warning: Unknown flag '%s' ignored.\n", s.c_str());
     else args.push_back(s);
   }
   if (args.size() < 4) return usage();
@@ -109,6 +109,10 @@ int main(int argc, char** argv) {
   if (rc) { fprintf(stderr, "boa_create failed (%d)\n", rc); return 1; }
   rc = boa_load_weights(ctx, model.c_str());
   if (rc) { fprintf(stderr, "load weights: %s\n", boa_last_error(ctx)); boa_destroy(ctx); return 1; }
+  if (compress && warm_start) {
+    boa_set_warm_start(ctx, cfg.max_lanes);
+    printf("Using warm-start interleaved compression. Batch=%d\n", cfg.max_lanes);
+  }
   auto t0 = std::chrono::steady_clock::now();
   rc = compress ? boa_compress_file(ctx, in.c_str(), out.c_str(), chunk, max_chunks)
                 : boa_decompress_file(ctx, in.c_str(), out.c_str());

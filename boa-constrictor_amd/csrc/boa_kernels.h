@@ -43,8 +43,9 @@ struct RcDec {
 // gives the last, short chunk).
 struct TokenSrc {
   const uint8_t* base;  // first byte of lane 0's chunk
-  int64_t stride;       // bytes between lanes' chunks
+  int64_t stride;       // bytes between lanes' chunks (a multiple of len with warm-start)
   int64_t total;        // valid bytes counted from base
+  int64_t len;          // positions per lane's chunk; bytes past total read as 0
 };
 
 struct LayerW {
@@ -171,6 +172,9 @@ hipError_t launch_rc_finish(RcEnc* st, uint32_t* out, int64_t pitch_words, int32
                             int lanes, hipStream_t s);
 hipError_t launch_compact(const uint32_t* words, int64_t pitch_words, const int32_t* sizes_words,
                           int lanes, uint64_t* offsets_words, uint32_t* payload, hipStream_t s);
+hipError_t launch_gather_streams(const uint32_t* src, const uint64_t* src_off,
+                                 const uint64_t* dst_off, const int32_t* sizes, int64_t n,
+                                 uint32_t* dst, hipStream_t s);
 hipError_t launch_rc_dec_init(RcDec* st, const uint32_t* payload, const uint64_t* offsets_words,
                               const int32_t* sizes_words, int lanes, hipStream_t s);
 hipError_t launch_decode_step(const float* logits, const float* head_b2, float inv_temp,

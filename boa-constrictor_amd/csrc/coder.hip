@@ -192,7 +192,7 @@ __device__ __forceinline__ uint32_t q_high(const double* s_cdf, int k) {
 
 __device__ __forceinline__ uint32_t token_at(const TokenSrc& tok, int lane, int64_t pos_in_chunk) {
   const int64_t pos = (int64_t)lane * tok.stride + pos_in_chunk;
-  return (pos_in_chunk < tok.stride && pos < tok.total) ? tok.base[pos] : 0u;
+  return (pos_in_chunk < tok.len && pos < tok.total) ? tok.base[pos] : 0u;
 }
 
 // (low, prob) of the next byte for every row (lane b, position t0+t) of a
@@ -268,7 +268,7 @@ __global__ void rc_encode_tile_kernel(const uint2* __restrict__ lowprob, TokenSr
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= lanes) return;
   int64_t len = tok.total - (int64_t)b * tok.stride;
-  len = len < 0 ? 0 : (len > tok.stride ? tok.stride : len);
+  len = len < 0 ? 0 : (len > tok.len ? tok.len : len);
   int64_t end = len - 1;
   if (end > (int64_t)t0 + T) end = (int64_t)t0 + T;
   if (end <= t0) return;
@@ -360,6 +360,31 @@ hipError_t launch_compact(const uint32_t* words, int64_t pitch_words, const int3
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(compact_kernel, dim3(16, lanes), dim3(256), 0, s, words, pitch_words,
                      sizes_words, offsets_words, payload);
+  return hipGetLastError();
+}
+
+// Warm-start compaction leaves streams in lane-iteration order; this moves
+// stream i (sizes[i] words at src + src_off[i]) to dst + dst_off[i], one
+// block per stream at a time.
+__global__ __launch_bounds__(256) void gather_streams_kernel(const uint32_t* __restrict__ src,
+                                                             const uint64_t* __restrict__ src_off,
+                                                             const uint64_t* __restrict__ dst_off,
+                                                             const int32_t* __restrict__ sizes,
+                                                             int64_t n, uint32_t* __restrict__ dst) {
+  for (int64_t i = blockIdx.x; i < n; i += gridDim.x) {
+    const uint32_t* a = src + src_off[i];
+    uint32_t* b = dst + dst_off[i];
+    for (int k = threadIdx.x; k < sizes[i]; k += blockDim.x) b[k] = a[k];
+  }
+}
+
+hipError_t launch_gather_streams(const uint32_t* src, const uint64_t* src_off,
+                                 const uint64_t* dst_off, const int32_t* sizes, int64_t n,
+                                 uint32_t* dst, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  const unsigned blocks = (unsigned)(n < 8192 ? n : 8192);
+  hipLaunchKernelGGL(gather_streams_kernel, dim3(blocks), dim3(256), 0, s, src, src_off, dst_off,
+                     sizes, n, dst);
   return hipGetLastError();
 }
 

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
   if (use_tok) {
     const int lane = row / T, t = row % T;
     const int64_t pos = (int64_t)lane * tok.stride + t0 + t;
-    const uint32_t token = (t0 + t < tok.stride && pos < tok.total) ? tok.base[pos] : 0u;
+    const uint32_t token = (t0 + t < tok.len && pos < tok.total) ? tok.base[pos] : 0u;
     src = emb + (size_t)token * d;
     xc = x + (size_t)row * d;
   } else {

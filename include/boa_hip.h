@@ -63,6 +63,18 @@ int boa_set_stream(boa_ctx* ctx, void* hip_stream);
 int boa_use_own_stream(boa_ctx* ctx);
 /* gpu_set_temperature (range_coder_kernels.cu:9-12). */
 int boa_set_temperature(boa_ctx* ctx, float temperature);
+/* Warm-start interleave (--warm-start; boa.cpp:310-319, 395-435, 690-693).
+ * With interleave_batch B > 0, boa_compress_device / boa_decompress_device
+ * run W = min(B, n_chunks) units of S = ceil(n_chunks / W) consecutive
+ * chunks each, unit u taking chunks u*S + i, and carry the recurrent state
+ * from one chunk of a unit to the next (reset only before the first).
+ * Units are run max_lanes at a time.  Streams stay in chunk order.  The
+ * buffer and file calls write flags bit 0 and W to the BOA2 header, and
+ * take W from the header when reading (whatever this setting is).  The
+ * decoder feeds each chunk's last byte before the unit's next chunk, as the
+ * compressor's forward consumed it.  0 (default) = every chunk starts from
+ * zero state. */
+int boa_set_warm_start(boa_ctx* ctx, int32_t interleave_batch);
 
 /* Weights in the convert_boa_weights.py layout: "BOA\0" fp32, "BOA\1" fp16 or
  * headerless fp32.  Replaces BoaPredictorGPU::load_weights
@@ -134,7 +146,8 @@ int boa_decompress_device(boa_ctx* ctx, const uint32_t* d_payload, const uint64_
 
 /* ---- path level (host buffers / files, BOA2 container) ------------------ */
 /* Compress a host buffer into a BOA2 container (malloc'd; free with
- * boa_free).  Replaces compress_v2 (boa.cpp:280-582) without warm-start. */
+ * boa_free).  Replaces compress_v2 (boa.cpp:280-582); warm-start per
+ * boa_set_warm_start. */
 int boa_compress_buffer(boa_ctx* ctx, const uint8_t* h_in, int64_t n, int64_t chunk_size,
                         int32_t max_chunks, uint8_t** h_out, int64_t* out_len);
 /* Decompress a BOA2 container; replaces decompress_v2 (boa.cpp:584-817). */

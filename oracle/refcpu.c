@@ -996,20 +996,33 @@ int32_t ref_boa2_parse(const uint8_t* buf, int64_t n, ref_boa2_info* info, uint8
 }
 
 /* =====================================================================
- * End-to-end compress / decompress (boa.cpp:280-582, :584-817) without
- * warm-start.  Lanes are independent, so every chunk is encoded on its
- * own: tiling and batching do not change a single bit of the output.
+ * End-to-end compress / decompress (boa.cpp:280-582, :584-817).
+ * Without warm-start lanes are independent, so every chunk is encoded on
+ * its own: tiling and batching do not change a single bit of the output.
+ * With warm-start (boa.cpp:310-319, 395-435) the B = min(gpu_batch, n)
+ * lanes each run S = ceil(n / B) chunks in a row, lane b taking chunks
+ * b*S + i, and the recurrent state carries from one chunk to the next:
+ * compress forwards every byte of a chunk (boa.cpp:441-469 walks tiles up
+ * to chunk_size), so the state that starts chunk b*S + i + 1 has consumed
+ * all of chunk b*S + i.  The decoder here consumes the chunk's last byte
+ * with one more step before the next chunk, which keeps it in step with
+ * that compressor (boa.cpp:717-740 stops after chunk_size - 1 steps).
  * ===================================================================== */
 void ref_free(void* p) { free(p); }
 
 static int64_t pitch_words_for(int64_t chunk) { return (chunk * 10 + 4096 + 3) / 4; }
 
-int32_t ref_encode_chunk(const ref_model* m, const uint8_t* chunk, int32_t len, int32_t tile,
-                         float temperature, uint32_t* words, int32_t cap_words) {
-    if (len <= 1) return 0;
+/* Codes bytes 1..len-1 of one chunk with the state in lane 0 of `s`
+ * (boa.cpp:441-469 with range_coder_kernels.cu:854-858).  feed_all also
+ * forwards the last byte so the state ends having consumed the whole chunk
+ * (warm-start). */
+static int32_t encode_with_state(const ref_model* m, ref_state* s, const uint8_t* chunk,
+                                 int32_t len, int32_t tile, float temperature, uint32_t* words,
+                                 int32_t cap_words, int feed_all) {
+    int n_fwd = feed_all ? len : len - 1; /* positions forwarded */
+    if (n_fwd <= 0) return 0;
     int T = tile > 0 ? tile : 256;
     if (T > 256) T = 256;
-    ref_state* s = ref_state_new(m, 1);
     scratch_t sc;
     scratch_init(&sc, m, T);
     float* logits = (float*)malloc(sizeof(float) * (size_t)T * 256);
@@ -1018,23 +1031,31 @@ int32_t ref_encode_chunk(const ref_model* m, const uint8_t* chunk, int32_t len, 
     float inv_t = 1.0f / temperature;
     double s_cdf[257];
     int n_pos = len - 1; /* positions whose prediction is coded */
-    for (int t0 = 0; t0 < n_pos; t0 += T) {
-        int n = n_pos - t0 < T ? n_pos - t0 : T;
+    for (int t0 = 0; t0 < n_fwd; t0 += T) {
+        int n = n_fwd - t0 < T ? n_fwd - t0 : T;
         forward_lane(m, s, 0, chunk + t0, n, logits, &sc);
-        for (int i = 0; i < n; ++i) {
+        for (int i = 0; i < n && t0 + i < n_pos; ++i) {
             ref_cdf_build(logits + (size_t)i * 256, NULL, inv_t, s_cdf);
             uint32_t lo, hi;
             ref_cdf_interval(s_cdf, chunk[t0 + i + 1], &lo, &hi);
             ref_rc_enc_put(&st, lo, hi - lo, words);
             if (st.write_idx_words > cap_words - 16) { /* cannot happen below 3 B/symbol */
-                free(logits); scratch_free(&sc); ref_state_free(s);
+                free(logits); scratch_free(&sc);
                 return -1;
             }
         }
     }
-    int32_t nw = ref_rc_enc_finish(&st, words);
+    int32_t nw = n_pos > 0 ? ref_rc_enc_finish(&st, words) : 0;
     free(logits);
     scratch_free(&sc);
+    return nw;
+}
+
+int32_t ref_encode_chunk(const ref_model* m, const uint8_t* chunk, int32_t len, int32_t tile,
+                         float temperature, uint32_t* words, int32_t cap_words) {
+    if (len <= 1) return 0;
+    ref_state* s = ref_state_new(m, 1);
+    int32_t nw = encode_with_state(m, s, chunk, len, tile, temperature, words, cap_words, 0);
     ref_state_free(s);
     return nw;
 }
@@ -1054,15 +1075,32 @@ int32_t ref_compress(const ref_model* m, const uint8_t* data, int64_t n, const r
     int err = 0;
     int nt = pick_threads(o->n_threads);
     float temp = o->temperature > 0 ? o->temperature : 1.0f;
+    /* warm-start: B lanes of S consecutive chunks each (boa.cpp:310-319) */
+    int B = 0, S = 1;
+    if (o->warm_start && nc > 0) {
+        B = o->gpu_batch > 0 ? o->gpu_batch : 64;
+        if (B > nc) B = nc;
+        S = (nc + B - 1) / B;
+    }
+    int units = o->warm_start ? B : nc;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nt)
-    for (int c = 0; c < nc; ++c) {
-        int64_t start = (int64_t)c * chunk;
-        int64_t len = n - start < chunk ? n - start : chunk;
-        first[c] = len > 0 ? data[start] : 0;
-        streams[c] = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)pitch);
-        nwords[c] = ref_encode_chunk(m, data + start, (int32_t)len, o->tile, temp, streams[c],
-                                     (int32_t)pitch);
-        if (nwords[c] < 0) err = 1;
+    for (int u = 0; u < units; ++u) {
+        ref_state* s = ref_state_new(m, 1);
+        for (int i = 0; i < (o->warm_start ? S : 1); ++i) {
+            int c = o->warm_start ? u * S + i : u;
+            if (c >= nc) break;
+            int64_t start = (int64_t)c * chunk;
+            int64_t len = n - start < chunk ? n - start : chunk;
+            first[c] = len > 0 ? data[start] : 0;
+            streams[c] = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)pitch);
+            if (!o->warm_start) ref_state_reset(s);
+            nwords[c] = len > 1 || o->warm_start
+                ? encode_with_state(m, s, data + start, (int32_t)len, o->tile, temp, streams[c],
+                                    (int32_t)pitch, o->warm_start)
+                : 0;
+            if (nwords[c] < 0) err = 1;
+        }
+        ref_state_free(s);
     }
     if (err) {
         for (int c = 0; c < nc; ++c) free(streams[c]);
@@ -1077,12 +1115,17 @@ int32_t ref_compress(const ref_model* m, const uint8_t* data, int64_t n, const r
     uint32_t u32;
     memcpy(buf + p, "BOA2", 4); p += 4;
     u32 = 1; memcpy(buf + p, &u32, 4); p += 4;
-    u32 = 0; memcpy(buf + p, &u32, 4); p += 4;
+    u32 = o->warm_start ? 1u : 0u; memcpy(buf + p, &u32, 4); p += 4; /* flags */
     uint64_t ps = (uint64_t)processed; memcpy(buf + p, &ps, 8); p += 8;
     u32 = (uint32_t)chunk; memcpy(buf + p, &u32, 4); p += 4;
     u32 = (uint32_t)nc; memcpy(buf + p, &u32, 4); p += 4;
     u32 = (uint32_t)last_len; memcpy(buf + p, &u32, 4); p += 4;
-    buf[p++] = 0;
+    if (o->warm_start) { /* fp_len 4: the interleave batch (boa.cpp:546-559) */
+        buf[p++] = 4;
+        u32 = (uint32_t)B; memcpy(buf + p, &u32, 4); p += 4;
+    } else {
+        buf[p++] = 0;
+    }
     for (int c = 0; c < nc; ++c) {
         memcpy(buf + p, streams[c], (size_t)nwords[c] * 4);
         p += (int64_t)nwords[c] * 4;
@@ -1105,8 +1148,10 @@ int32_t ref_decompress(const ref_model* m, const uint8_t* boa, int64_t n, const 
     ref_boa2_info info;
     int rc = ref_boa2_parse(boa, n, &info, NULL, NULL, NULL);
     if (rc) return rc;
-    if (info.flags & 1u) return -20; /* warm-start containers are not decoded here */
+    const int warm = (info.flags & 1u) != 0;
     uint32_t nc = info.n_chunks;
+    /* warm-start: the interleave batch comes from the header (boa.cpp:608-610) */
+    if (warm && nc > 0 && info.interleave_batch == 0) return -20;
     uint8_t* first = (uint8_t*)malloc(nc ? nc : 1);
     uint64_t* offs = (uint64_t*)malloc(sizeof(uint64_t) * (nc ? nc : 1));
     uint64_t* lens = (uint64_t*)malloc(sizeof(uint64_t) * (nc ? nc : 1));
@@ -1123,11 +1168,13 @@ int32_t ref_decompress(const ref_model* m, const uint8_t* boa, int64_t n, const 
     const uint8_t* payload = boa + info.payload_off;
     enum { GMAX = 8 };
     int nt = pick_threads(o->n_threads);
-    /* lanes stepped together per thread: up to 8, fewer when that would leave
-     * threads idle */
-    int G = (int)(nc / (uint32_t)(nt > 0 ? nt : 1));
+    /* Units stepped as one group: chunks (cold) or lanes of S chunks (warm).
+     * Up to 8 per group, fewer when that would leave threads idle. */
+    const int B = warm ? (int)(info.interleave_batch < nc ? info.interleave_batch : nc) : (int)nc;
+    const int S = warm && B > 0 ? (int)((nc + (uint32_t)B - 1) / (uint32_t)B) : 1;
+    int G = B / (nt > 0 ? nt : 1);
     G = G < 1 ? 1 : (G > GMAX ? GMAX : G);
-    int groups = (int)((nc + G - 1) / G);
+    int groups = (B + G - 1) / G;
     float inv_t = 1.0f / (o->temperature > 0 ? o->temperature : 1.0f);
 #pragma omp parallel num_threads(nt)
     {
@@ -1143,39 +1190,54 @@ int32_t ref_decompress(const ref_model* m, const uint8_t* boa, int64_t n, const 
         double s_cdf[257];
 #pragma omp for schedule(dynamic, 1)
         for (int g = 0; g < groups; ++g) {
-            int c0 = g * G, cnt = (int)nc - c0 < G ? (int)nc - c0 : G;
-            int maxlen = 0;
+            int u0 = g * G, gl = B - u0 < G ? B - u0 : G;
             ref_state_reset(s);
-            for (int i = 0; i < cnt; ++i) {
-                int c = c0 + i;
-                len[i] = (c == (int)nc - 1) ? (int32_t)info.last_chunk_len : (int32_t)chunk;
-                nw[i] = (int32_t)(lens[c] / 4);
-                words[i] = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(nw[i] ? nw[i] : 1));
-                memcpy(words[i], payload + offs[c], (size_t)nw[i] * 4);
-                ref_rc_dec_init(&dec[i], words[i], nw[i]);
-                o_ptr[i] = dst + (int64_t)c * chunk;
-                if (len[i] > 0) o_ptr[i][0] = first[c];
-                tok[i] = first[c];
-                if (len[i] > maxlen) maxlen = len[i];
-            }
-            for (int t = 1; t < maxlen; ++t) {
-                /* step every lane of the group (the reference steps all
-                 * lanes each time; finished lanes only stop decoding) */
-                embed_rows(m, tok, cnt, sc.x);
-                for (int l = 0; l < m->L; ++l) block_rows(m, s, l, &sc, cnt, 0, 0);
-                head_rows(m, &sc, cnt, 0, logits);
+            for (int it = 0; it < S; ++it) {
+                /* active lanes lead: unit u runs chunk u*S + it while that is < nc */
+                int cnt = 0;
+                while (cnt < gl && (int64_t)(u0 + cnt) * S + it < (int64_t)nc) ++cnt;
+                if (cnt == 0) break;
+                int maxlen = 0;
                 for (int i = 0; i < cnt; ++i) {
-                    if (t >= len[i]) continue;
-                    ref_cdf_build(logits + (size_t)i * 256, m->hb2, inv_t, s_cdf);
-                    uint32_t q = ref_rc_dec_target(&dec[i]);
-                    uint32_t lo, hi;
-                    int sym = ref_cdf_search(s_cdf, q, &lo, &hi);
-                    ref_rc_dec_advance(&dec[i], lo, hi, words[i], nw[i]);
-                    o_ptr[i][t] = (uint8_t)sym;
-                    tok[i] = (uint8_t)sym;
+                    int c = warm ? (u0 + i) * S + it : u0 + i;
+                    len[i] = (c == (int)nc - 1) ? (int32_t)info.last_chunk_len : (int32_t)chunk;
+                    nw[i] = (int32_t)(lens[c] / 4);
+                    words[i] = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(nw[i] ? nw[i] : 1));
+                    memcpy(words[i], payload + offs[c], (size_t)nw[i] * 4);
+                    ref_rc_dec_init(&dec[i], words[i], nw[i]);
+                    o_ptr[i] = dst + (int64_t)c * chunk;
+                    if (len[i] > 0) o_ptr[i][0] = first[c];
+                    tok[i] = first[c];
+                    if (len[i] > maxlen) maxlen = len[i];
+                }
+                for (int t = 1; t < maxlen; ++t) {
+                    /* step every lane of the group (the reference steps all
+                     * lanes each time; finished lanes only stop decoding) */
+                    embed_rows(m, tok, cnt, sc.x);
+                    for (int l = 0; l < m->L; ++l) block_rows(m, s, l, &sc, cnt, 0, 0);
+                    head_rows(m, &sc, cnt, 0, logits);
+                    for (int i = 0; i < cnt; ++i) {
+                        if (t >= len[i]) continue;
+                        ref_cdf_build(logits + (size_t)i * 256, m->hb2, inv_t, s_cdf);
+                        uint32_t q = ref_rc_dec_target(&dec[i]);
+                        uint32_t lo, hi;
+                        int sym = ref_cdf_search(s_cdf, q, &lo, &hi);
+                        ref_rc_dec_advance(&dec[i], lo, hi, words[i], nw[i]);
+                        o_ptr[i][t] = (uint8_t)sym;
+                        tok[i] = (uint8_t)sym;
+                    }
+                }
+                for (int i = 0; i < cnt; ++i) free(words[i]);
+                if (warm && it + 1 < S) {
+                    /* the lanes that go on consume their chunk's last byte */
+                    int next = 0;
+                    while (next < cnt && (int64_t)(u0 + next) * S + it + 1 < (int64_t)nc) ++next;
+                    if (next > 0) {
+                        embed_rows(m, tok, next, sc.x);
+                        for (int l = 0; l < m->L; ++l) block_rows(m, s, l, &sc, next, 0, 0);
+                    }
                 }
             }
-            for (int i = 0; i < cnt; ++i) free(words[i]);
         }
         free(logits);
         ref_state_free(s);

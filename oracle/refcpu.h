@@ -147,6 +147,7 @@ typedef struct {
     int32_t max_chunks;    /* <=0: all */
     int32_t n_threads;     /* OpenMP threads (0 = default) */
     float temperature;     /* 1.0 default */
+    int32_t warm_start;    /* --warm-start: lanes carry state over gpu_batch-interleaved chunks */
 } ref_codec_opts;
 
 /* Returns 0 on success; *out is malloc'd (free with ref_free). */

@@ -34,7 +34,8 @@ class RcDec(C.Structure):
 
 class CodecOpts(C.Structure):
     _fields_ = [("chunk_size", C.c_int64), ("gpu_batch", C.c_int32), ("tile", C.c_int32),
-                ("max_chunks", C.c_int32), ("n_threads", C.c_int32), ("temperature", C.c_float)]
+                ("max_chunks", C.c_int32), ("n_threads", C.c_int32), ("temperature", C.c_float),
+                ("warm_start", C.c_int32)]
 
 
 class Boa2Info(C.Structure):
@@ -174,8 +175,10 @@ class Model:
         return State(self, lanes)
 
     def compress(self, data: bytes, chunk_size=4096, tile=0, max_chunks=0, n_threads=0,
-                 temperature=1.0) -> bytes:
-        o = CodecOpts(chunk_size, 64, tile, max_chunks, n_threads, temperature)
+                 temperature=1.0, warm_start=False, gpu_batch=64) -> bytes:
+        """boa.cpp compress_v2; warm_start interleaves chunks over gpu_batch lanes."""
+        o = CodecOpts(chunk_size, gpu_batch, tile, max_chunks, n_threads, temperature,
+                      1 if warm_start else 0)
         out = C.c_void_p()
         n = C.c_int64()
         buf = np.frombuffer(data, np.uint8)
@@ -187,7 +190,7 @@ class Model:
         return res
 
     def decompress(self, blob: bytes, n_threads=0, temperature=1.0) -> bytes:
-        o = CodecOpts(0, 64, 0, 0, n_threads, temperature)
+        o = CodecOpts(0, 64, 0, 0, n_threads, temperature, 0)
         out = C.c_void_p()
         n = C.c_int64()
         buf = np.frombuffer(blob, np.uint8)
