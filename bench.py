@@ -110,6 +110,9 @@ def main() -> int:
     ap.add_argument("--cpu-sample-chunks", type=int, default=0)
     ap.add_argument("--cpu-sample-len", type=int, default=4096)
     ap.add_argument("--no-decompress", action="store_true")
+    ap.add_argument("--warm-start", type=int, default=0, metavar="B",
+                    help="warm-start interleave over B lanes (boa.cpp --warm-start with "
+                         "--gpu-batch B); not the metric config")
     ap.add_argument("--host-path", action="store_true",
                     help="also time the host-buffer path (bytes in host memory -> BOA2 container "
                          "in host memory, PCIe transfers included)")
@@ -144,6 +147,8 @@ def main() -> int:
         chunk = args.chunk_len
         data = b"".join(data[c * full: c * full + chunk] for c in range(n_chunks))
         workload = f"{args.config}-probe-{chunk}B-chunks"
+    if args.warm_start:
+        workload += f"-warm{args.warm_start}"
     n = len(data)
     n_chunks = math.ceil(n / chunk)
     print(f"[bench] {workload}: {n} bytes, {n_chunks} chunks of {chunk} B", file=sys.stderr, flush=True)
@@ -161,6 +166,7 @@ def main() -> int:
     prime = min(n, n_chunks * 64)
     codec.compress_device(d_data, prime, 64, d_pay, cap)
     torch.cuda.synchronize()
+    codec.set_warm_start(args.warm_start)
 
     def step(profile: bool):
         torch.cuda.synchronize()
@@ -283,7 +289,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": workload, "d_model": d, "n_layers": L, "d_state": ds,
                    "chunks": n_chunks, "chunk_len": chunk, "input_bytes": n,
-                   "precision": prec, "weights": "random-init seed 0",
+                   "precision": prec, "warm_start": args.warm_start,
+                   "weights": "random-init seed 0",
                    "input": f"synth.gen_{args.config}"},
         "compress_mb_s": round(comp_mb_s, 4),
         "decompress_mb_s": round(dec_mb_s, 4) if dec_mb_s else None,
