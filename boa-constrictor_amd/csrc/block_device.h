@@ -90,7 +90,7 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
   float y = 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; ++n) {
-    float dA = exp_sel<BR>(sc.na[n] * dt);
+    float dA = scan_exp(sc.na[n] * dt);
     float dB = dt * Bv[n];
     sc.h[n] = dA * sc.h[n] + dB * u;
     y = y + sc.h[n] * Cv[n];

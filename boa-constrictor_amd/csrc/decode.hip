@@ -267,11 +267,13 @@ hipError_t launch_dec_scan_params(const float* w_dt, const float* na, float* wdt
 }
 
 // -------------------------------------------------------------- LayerNorm
-// A 256-thread block normalises 16 lanes.  Thread t loads float4 t % 4 of
-// lane t / 4 % 16's feature block t / 64 + 4 it (a wavefront reads one
-// contiguous 1 KB per load), the slab is kept in LDS in natural feature
-// order, the statistics follow the reference's order, and each thread
-// normalises and stores the float4s it loaded.
+// A block of 16 LANES threads normalises LANES lanes.  Thread t loads
+// float4 t % 4 of lane t / 4 % LANES's feature block t / (4 LANES) + 4 it
+// (a wavefront reads 64 LANES contiguous bytes per feature block), the slab
+// is kept in LDS in natural feature order, the statistics follow the
+// reference's order, and each thread normalises and stores the float4s it
+// loaded.  Small blocks spread the 1000-odd lanes of a decode step over
+// more CUs.
 //   LN1 (MODE 1): 16 threads per lane; thread l sums features l, l+32, ...
 //     and l+16, l+48, ... (the partials of lanes l and l+16 of the
 //     reference's warp-per-row reduction), adds them (the shuffle step 16)
@@ -279,10 +281,10 @@ hipError_t launch_dec_scan_params(const float* w_dt, const float* na, float* wdt
 //     compress LN1 kernel.
 //   LN2 (MODE 2): one thread per lane sums all features in order.
 // Layer 0's LN1 reads the embedding rows instead (and stores them as x).
-constexpr int DEC_LN_LANES = 16;
+constexpr int DEC_LN_LANES = 4;
 
-template <int MODE, int NB, bool EMB>
-__global__ __launch_bounds__(256) void dec_ln_kernel(const float* __restrict__ emb,
+template <int MODE, int NB, bool EMB, int LANES>
+__global__ __launch_bounds__(16 * LANES) void dec_ln_kernel(const float* __restrict__ emb,
                                                      const uint8_t* __restrict__ tok, float* xt,
                                                      const float* src, float* xnt,
                                                      const float* __restrict__ w,
@@ -291,12 +293,12 @@ __global__ __launch_bounds__(256) void dec_ln_kernel(const float* __restrict__ e
   constexpr int d = NB * 16;
   constexpr int S = d + 4;                 // LDS row stride (floats)
   constexpr int IT = (NB + 3) / 4;         // feature blocks per thread
-  __shared__ __align__(16) float tile[DEC_LN_LANES * S];
-  __shared__ float stats[2 * DEC_LN_LANES];
+  __shared__ __align__(16) float tile[LANES * S];
+  __shared__ float stats[2 * LANES];
   if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
   const int t = threadIdx.x;
-  const int j = (t >> 2) & 15, a4 = t & 3, kb0 = t >> 6;
-  const int m0 = blockIdx.x * DEC_LN_LANES;
+  const int j = (t >> 2) % LANES, a4 = t & 3, kb0 = t / (4 * LANES);
+  const int m0 = blockIdx.x * LANES;
   const int m = min(m0 + j, M - 1);
   const float* erow = EMB ? emb + (size_t)tok[m] * d : nullptr;
   float4 v[IT];
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(256) void dec_ln_kernel(const float* __restrict__ e
       stats[2 * lj] = mean;
       stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
-  } else if (t < DEC_LN_LANES) {
+  } else if (t < LANES) {
     const float4* row = reinterpret_cast<const float4*>(tile + t * S);
     float sum = 0.0f, sq = 0.0f;
 #pragma unroll 8
@@ -390,14 +392,15 @@ template <int MODE>
 hipError_t dec_ln_launch(const float* emb, const uint8_t* tok, float* xt, const float* src,
                          float* xnt, const float* w, const float* b, int M, int d, int ld,
                          int* t_counter, hipStream_t s) {
-  const dim3 grid((M + DEC_LN_LANES - 1) / DEC_LN_LANES), block(256);
-#define BOA_DEC_LN(NBv)                                                                        \
-  if (emb)                                                                                     \
-    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, true>), grid, block, 0, s, emb, tok, xt, src, \
-                       xnt, w, b, M, ld, t_counter);                                           \
-  else                                                                                         \
-    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, false>), grid, block, 0, s, emb, tok, xt, src, \
-                       xnt, w, b, M, ld, t_counter);
+  constexpr int LN = DEC_LN_LANES;
+  const dim3 grid((M + LN - 1) / LN), block(16 * LN);
+#define BOA_DEC_LN(NBv)                                                                      \
+  if (emb)                                                                                   \
+    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, true, LN>), grid, block, 0, s, emb, tok, xt, \
+                       src, xnt, w, b, M, ld, t_counter);                                    \
+  else                                                                                       \
+    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, false, LN>), grid, block, 0, s, emb, tok,   \
+                       xt, src, xnt, w, b, M, ld, t_counter);
   switch (d) {
     case 64: BOA_DEC_LN(4) break;
     case 128: BOA_DEC_LN(8) break;

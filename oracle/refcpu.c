@@ -46,10 +46,7 @@ static void bf16_round(float* p, size_t n) {
  * into a float head and tail; e^r by its degree-7 Taylor polynomial in
  * Horner form (fused multiply-adds); 2^k assembled in the exponent field.
  * Inputs below -87 return 0 so every non-zero result is a normal float. */
-float ref_expf(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return INFINITY;
-    if (x < -87.0f) return 0.0f;
+static float exp_core(float x) {
     const float LOG2E = 1.44269504088896340736f;
     const float LN2_HI = 0.693147182464599609375f;
     const float LN2_LO = -1.904654323148236e-09f;
@@ -67,6 +64,21 @@ float ref_expf(float x) {
     int k = (int)kf;
     if (k > 127) return (p * u2f((uint32_t)(127 + 127) << 23)) * 2.0f;
     return p * u2f((uint32_t)(k + 127) << 23);
+}
+
+float ref_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -87.0f) return 0.0f;
+    return exp_core(x);
+}
+
+/* exp(x) on the selective scan's domain x = -exp(A_log) * dt <= 0: x is
+ * clamped into [-87, 0] first (fmaxf turns a NaN into -87) and x < -87
+ * gives 0.  Equal to ref_expf on [-87, 0]. */
+float ref_scan_exp(float x) {
+    float e = exp_core(fminf(fmaxf(x, -87.0f), 0.0f));
+    return x < -87.0f ? 0.0f : e;
 }
 
 /* log(y) for y > 0: y = 2^e * m with m in [sqrt(1/2), sqrt(2)],
@@ -730,7 +742,7 @@ static inline float scan_row(const ref_layer* Ly, const ref_model* m, int dch, c
     const float* na = Ly->neg_exp_a + (size_t)dch * ds;
     float y = 0.0f;
     for (int n = 0; n < ds; ++n) {
-        float dA = ref_expf(na[n] * dt);
+        float dA = ref_scan_exp(na[n] * dt);
         float dB = dt * Bv[n];
         h[n] = dA * h[n] + dB * u;
         y = y + h[n] * Cv[n];

@@ -46,6 +46,7 @@ extern "C" {
 
 /* ---------------------------------------------------------------- math */
 float ref_expf(float x);
+float ref_scan_exp(float x);      /* exp on the scan's domain x <= 0 (clamped, NaN -> -87) */
 float ref_logf(float x);
 float ref_repro_exp(float x);     /* activations.hpp:33-84 (device branch) */
 float ref_repro_tanh(float x);    /* activations.hpp:87-98 */

@@ -43,6 +43,22 @@ def test_expf_ulp_bound(oracle):
     assert np.isnan(L.ref_expf(float("nan")))
 
 
+def test_scan_exp_domain(oracle):
+    """The scan's exp equals ref_expf on [-87, 0] bit for bit (so the ulp
+    bound above carries over), is 0 below -87, saturates at exp(0) above 0
+    and maps a NaN to exp(-87)."""
+    L = oracle.lib()
+    xs = np.concatenate([np.linspace(-87.0, 0.0, 50001, dtype=np.float32),
+                         -np.geomspace(1e-30, 87.0, 20001).astype(np.float32),
+                         np.array([-0.0, -87.0], np.float32)])
+    a = vec(L.ref_scan_exp, xs)
+    b = vec(L.ref_expf, xs)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert L.ref_scan_exp(-87.00001) == 0.0 and L.ref_scan_exp(float("-inf")) == 0.0
+    assert L.ref_scan_exp(3.0) == 1.0
+    assert L.ref_scan_exp(float("nan")) == L.ref_expf(-87.0)
+
+
 def test_logf_ulp_bound(oracle):
     L = oracle.lib()
     xs = np.concatenate([np.geomspace(1e-30, 1e30, 40001).astype(np.float32),
