@@ -9,7 +9,7 @@ namespace boa {
 
 // value = bias + x[t-3] w0 + x[t-2] w1 + x[t-1] w2 + x[t] w3 (unfused, k
 // order), then SiLU.  The state holds the last four inputs, most recent last.
-template <bool BR = false>
+template <int M = MATH_BF>
 __device__ __forceinline__ float conv_value(float bias, float xm3, float xm2, float xm1, float x0,
                                             const float4 w) {
   float v = bias;
@@ -17,13 +17,13 @@ __device__ __forceinline__ float conv_value(float bias, float xm3, float xm2, fl
   v = v + xm2 * w.y;
   v = v + xm1 * w.z;
   v = v + x0 * w.w;
-  return silu<BR>(v);
+  return silu<M>(v);
 }
 
 // Step form: state s = (x[t-4], x[t-3], x[t-2], x[t-1]), new input x0.
-template <bool BR = false>
+template <int M = MATH_BF>
 __device__ __forceinline__ float conv_step_value(float bias, float4 s, float x0, const float4 w) {
-  return conv_value<BR>(bias, s.y, s.z, s.w, x0, w);
+  return conv_value<M>(bias, s.y, s.z, s.w, x0, w);
 }
 
 // Decode-step activation layouts, lane capacity ld:
@@ -76,27 +76,28 @@ __device__ __forceinline__ void scan_store(const ScanCtx<DS, RB>& sc, float* ssm
 
 // One token of one channel: dt = softplus(delta[0:r] . w_dt[:, c] + b_dt),
 // h_n = exp(-exp(A_log) dt) h_n + (dt B_n) u, y = sum_n h_n C_n + D u,
-// out = y * (z * sigmoid(z)).  BR selects the exp/log form (same results).
-template <int DS, int RB, bool BR = false>
+// out = y * (z * sigmoid(z)).  M selects the exp/log form (MATH_BF and
+// MATH_BR give the same results).
+template <int DS, int RB, int M = MATH_BF>
 __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt_in,
                                             const float* bc, int r, float u, float z) {
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < RB; ++j)
     if (j < r) acc = __builtin_fmaf(dt_in[j], sc.wdt[j], acc);
-  const float dt = softplus<BR>(acc + sc.bdt);
+  const float dt = softplus<M>(acc + sc.bdt);
   const float* Bv = bc;
   const float* Cv = bc + DS;
   float y = 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; ++n) {
-    float dA = scan_exp(sc.na[n] * dt);
+    float dA = scan_exp_sel<M>(sc.na[n] * dt);
     float dB = dt * Bv[n];
     sc.h[n] = dA * sc.h[n] + dB * u;
     y = y + sc.h[n] * Cv[n];
   }
   y = y + sc.dd * u;
-  float sg = 1.0f / (1.0f + exp_sel<BR>(-z));
+  float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));
   return y * (z * sg);
 }
 

@@ -132,10 +132,25 @@ BOA_DEV float logf_br(float y) {
   return log_core(y);
 }
 
-template <bool BR>
-BOA_DEV float exp_sel(float x) { return BR ? expf_br(x) : expf_(x); }
-template <bool BR>
-BOA_DEV float log_sel(float x) { return BR ? logf_br(x) : logf_(x); }
+// Forms of the transcendental activations.  MATH_BF and MATH_BR give
+// identical results (branch-free vs early-return special cases; the
+// oracle's functions).  MATH_HW uses the hardware exp2/log2/reciprocal
+// (v_exp_f32, v_log_f32, v_rcp_f32, about 1 ulp): the bf16 precision runs on
+// it in compress and decode alike, so its two passes still agree bit for
+// bit while its logits are compared with the oracle within the bf16
+// tolerance.
+enum { MATH_BF = 0, MATH_BR = 1, MATH_HW = 2 };
+
+BOA_DEV float hw_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896340736f); }
+BOA_DEV float hw_log(float x) { return __builtin_amdgcn_logf(x) * 0.69314718055994530942f; }
+BOA_DEV float hw_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+template <int M>
+BOA_DEV float exp_sel(float x) { return M == MATH_HW ? hw_exp(x) : M == MATH_BR ? expf_br(x) : expf_(x); }
+template <int M>
+BOA_DEV float log_sel(float x) { return M == MATH_HW ? hw_log(x) : M == MATH_BR ? logf_br(x) : logf_(x); }
+template <int M>
+BOA_DEV float rcp_sel(float x) { return M == MATH_HW ? hw_rcp(x) : 1.0f / x; }
 
 // activations.hpp:33-84 (device branch); core for x in [-88, 88]
 BOA_DEV float repro_exp_core(float x) {
@@ -151,9 +166,10 @@ BOA_DEV float repro_exp_core(float x) {
   return t * u2f((uint32_t)((k + 127) << 23));
 }
 
-template <bool BR>
+template <int M>
 BOA_DEV float repro_exp(float x) {
-  if (BR) {
+  if (M == MATH_HW) return hw_exp(x);
+  if (M == MATH_BR) {
     if (x <= -88.0f) return 0.0f;
     return repro_exp_core(x >= 88.0f ? 88.0f : x);
   }
@@ -162,33 +178,37 @@ BOA_DEV float repro_exp(float x) {
 }
 
 // activations.hpp:87-98
-template <bool BR>
+template <int M>
 BOA_DEV float repro_tanh(float x) {
   const float ax = x < 0.0f ? -x : x;
-  if (BR && ax > 10.0f) return (x > 0.0f) ? 1.0f : -1.0f;
-  const float e2x = repro_exp<BR>(2.0f * x);
-  const float th = (e2x + -1.0f) / (e2x + 1.0f);
+  if (M == MATH_BR && ax > 10.0f) return (x > 0.0f) ? 1.0f : -1.0f;
+  const float e2x = repro_exp<M>(2.0f * x);
+  const float th = M == MATH_HW ? 1.0f - 2.0f * hw_rcp(e2x + 1.0f) : (e2x + -1.0f) / (e2x + 1.0f);
   return ax > 10.0f ? ((x > 0.0f) ? 1.0f : -1.0f) : th;
 }
 
 // activations.hpp:105-117 (tanh GELU used by the FF epilogue)
-template <bool BR = false>
+template <int M = MATH_BF>
 BOA_DEV float gelu(float x) {
   float cube = (x * x) * x;
   float inner = 0.79788456080286535588f * (x + 0.044715f * cube);
-  float th = repro_tanh<BR>(inner);
+  float th = repro_tanh<M>(inner);
   return 0.5f * (x * (1.0f + th));
 }
 
 // SiLU in the form v * (1 / (1 + exp(-v))) (mamba_kernels.cu:188-189)
-template <bool BR = false>
+template <int M = MATH_BF>
 BOA_DEV float silu(float x) {
-  float sg = 1.0f / (1.0f + exp_sel<BR>(-x));
+  float sg = rcp_sel<M>(1.0f + exp_sel<M>(-x));
   return x * sg;
 }
 
 // unthresholded softplus log(1 + exp(x)) (inference_kernels.cu:376-382)
-template <bool BR = false>
-BOA_DEV float softplus(float x) { return log_sel<BR>(1.0f + exp_sel<BR>(x)); }
+template <int M = MATH_BF>
+BOA_DEV float softplus(float x) { return log_sel<M>(1.0f + exp_sel<M>(x)); }
+
+// exp on the scan's domain (see scan_exp) in the chosen form
+template <int M>
+BOA_DEV float scan_exp_sel(float x) { return M == MATH_HW ? hw_exp(x) : scan_exp(x); }
 
 }  // namespace boa

@@ -49,7 +49,7 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
   for (int e = 0; e < 4; ++e) {
     const int n = min(nf[e], a.N - 1);
     float r = acc[e] + (a.bias ? a.bias[n] : 0.0f);
-    if (a.act == ACT_GELU) r = gelu<true>(r);
+    if (a.act == ACT_GELU) r = gelu<MATH_BR>(r);
     else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
     v[e] = r;
   }
@@ -72,7 +72,7 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
       float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
       const float4 s0 = *st;
       const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
-      cv[e] = conv_step_value<true>(a.conv_b[n], s0, v[e], wv);
+      cv[e] = conv_step_value<MATH_BR>(a.conv_b[n], s0, v[e], wv);
       *st = make_float4(s0.y, s0.z, s0.w, v[e]);
     }
     float* o = a.conv_out + ((size_t)(n0 >> 4) * a.ldc + m) * 16 + 4 * g;
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
   const size_t cm = dblk(c, m, ld);
   const float u = cvt[cm];
   const float z = zt[cm];
-  yt[cm] = scan_token<DS, RB, true>(sc, row, row + RB, r, u, z);
+  yt[cm] = scan_token<DS, RB, MATH_BR>(sc, row, row + RB, r, u, z);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
     h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl] =

@@ -29,7 +29,7 @@ __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floa
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float r = acc[e] + (a.bias ? a.bias[min(nb + e, a.N - 1)] : 0.0f);
-    if (a.act == ACT_GELU) r = gelu<true>(r);
+    if (a.act == ACT_GELU) r = gelu<MATH_HW>(r);
     else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
     v[e] = r;
   }
@@ -70,7 +70,7 @@ __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floa
       float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
       const float4 s0 = *st;
       const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
-      o[e] = f32_to_bf16(conv_step_value<true>(a.conv_b[n], s0, x0, wv));
+      o[e] = f32_to_bf16(conv_step_value<MATH_HW>(a.conv_b[n], s0, x0, wv));
       *st = make_float4(s0.y, s0.z, s0.w, x0);
     }
     *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) = make_ushort4(o[0], o[1], o[2], o[3]);
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   const size_t cm = dblk32(c, m, ld);
   const float u = bf16_to_f32(cvt[cm]);
   const float z = bf16_to_f32(zt[cm]);
-  yt[cm] = f32_to_bf16(scan_token<DS, RB, true>(sc, row, row + RB, r, u, z));
+  yt[cm] = f32_to_bf16(scan_token<DS, RB, MATH_HW>(sc, row, row + RB, r, u, z));
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
     h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl] =

@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float t = acc[p][q][e] + (a.bias ? a.bias[min(n + e, a.N - 1)] : 0.0f);
-        if (a.act == ACT_GELU) t = gelu(t);
+        if (a.act == ACT_GELU) t = gelu<MATH_HW>(t);
         else if (a.act == ACT_RELU) t = fmaxf(0.0f, t);
         if (a.res) t = t + (n + e < a.N ? a.res[(size_t)m * a.ldr + n + e] : 0.0f);
         v[e] = t;

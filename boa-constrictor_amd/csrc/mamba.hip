@@ -197,7 +197,8 @@ __global__ __launch_bounds__(256) void conv_chunk_kernel(const TA* __restrict__ 
   TA* op = out + (size_t)b * T * di + c;
   for (int t = 0; t < T; ++t) {
     float x0 = ldv(xp + (size_t)t * 2 * di);
-    stv(op + (size_t)t * di, conv_value(bias, xm3, xm2, xm1, x0, wv));
+    // bf16 activations run on the hardware transcendentals (MATH_HW)
+    stv(op + (size_t)t * di, conv_value<sizeof(TA) == 2 ? MATH_HW : MATH_BF>(bias, xm3, xm2, xm1, x0, wv));
     xm4 = xm3; xm3 = xm2; xm2 = xm1; xm1 = x0;
   }
   *st = make_float4(xm4, xm3, xm2, xm1);
@@ -243,7 +244,8 @@ __global__ __launch_bounds__(256) void scan_chunk_kernel(Dims D, LayerW Lw,
       const size_t row = (size_t)b * T + t0 + tt;
       const float u = ldv(conv + row * di + c);
       const float z = ldv(xz + row * 2 * di + di + c);
-      stv(y + row * di + c, scan_token<DS, RB>(sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z));
+      stv(y + row * di + c, scan_token<DS, RB, sizeof(TA) == 2 ? MATH_HW : MATH_BF>(
+                                 sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z));
     }
   }
   scan_store<DS, RB>(sc, ssm);
