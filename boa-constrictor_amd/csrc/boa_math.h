@@ -27,12 +27,8 @@ BOA_DEV float u2f(uint32_t u) { return __uint_as_float(u); }
 BOA_DEV uint32_t f2u(float f) { return __float_as_uint(f); }
 
 // bfloat16 storage (uint16_t): the upper half of a float32, rounded to
-// nearest even; a NaN stays a quiet NaN.
-BOA_DEV uint16_t f32_to_bf16(float x) {
-  const uint32_t u = f2u(x);
-  const uint32_t r = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-  return (uint16_t)(((u & 0x7FFFFFFFu) > 0x7F800000u) ? ((u >> 16) | 0x40u) : r);
-}
+// nearest even by gfx950's v_cvt_pk_bf16_f32; a NaN stays a quiet NaN.
+BOA_DEV uint16_t f32_to_bf16(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 BOA_DEV float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 BOA_DEV float bf16r(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 

@@ -24,7 +24,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int NBUF = 2>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB16Args a,
                                                                            int swizzle) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
@@ -34,8 +34,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
   constexpr int XQ = BM * BK / 8, WQ = BN * BK / 8;  // 16-byte chunks per tile
   constexpr int XL = (XQ + NT - 1) / NT, WL = (WQ + NT - 1) / NT;
   static_assert(BK % 32 == 0, "BK must be a multiple of the MFMA k-step");
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][BM * S];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * S];
+  // NBUF = 1 keeps one LDS stage (the next k-tile waits in registers), so
+  // two workgroups fit in a CU's LDS and one's epilogue overlaps the
+  // other's main loop.
+  __shared__ __attribute__((aligned(16))) uint16_t xs[NBUF][BM * S];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[NBUF][BN * S];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
   BOA_B16_STORE(0)
   __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
-    const int cur = kt & 1;
+    const int cur = NBUF == 2 ? (kt & 1) : 0;
     if (kt + 1 < n_kt) { BOA_B16_LOAD((kt + 1) * BK) }
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
@@ -110,7 +113,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
         for (int q = 0; q < TN; ++q)
           acc[p][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[q], bf[p], acc[p][q], 0, 0, 0);
     }
-    if (kt + 1 < n_kt) { BOA_B16_STORE(cur ^ 1) }
+    if (NBUF == 1 && kt + 1 < n_kt) __syncthreads();
+    if (kt + 1 < n_kt) { BOA_B16_STORE(NBUF == 2 ? (cur ^ 1) : 0) }
     __syncthreads();
   }
 #undef BOA_B16_LOAD
@@ -158,12 +162,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
   }
 }
 
-template <int BM, int BN, int WM_, int WN_, int BK>
+template <int BM, int BN, int WM_, int WN_, int BK, int NBUF = 2>
 static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 1) {
   if (a.K % BK || a.ldx % 8 || a.ldw % 8 || a.ldw < a.K) return hipErrorInvalidValue;
   const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, BK>), dim3((unsigned)tiles),
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, BK, NBUF>), dim3((unsigned)tiles),
                      dim3(64 * WM_ * WN_), 0, s, a, swizzle);
   return hipGetLastError();
 }
@@ -187,6 +191,12 @@ hipError_t gemm_bf16_sweep(int cfg, const GemmB16Args& a, hipStream_t s) {
     case 3: return launch_b16<128, 128, 2, 2, 64>(a, s);
     case 4: return launch_b16<128, 256, 4, 4, 32>(a, s);
     case 5: return launch_b16<256, 128, 4, 4, 64>(a, s);
+    case 6: return launch_b16<256, 256, 2, 4, 64>(a, s);
+    case 7: return launch_b16<256, 256, 4, 2, 64>(a, s);
+    case 8: return launch_b16<256, 256, 4, 4, 32>(a, s);
+    case 9: return launch_b16<256, 256, 4, 4, 64, 1>(a, s);
+    case 10: return launch_b16<128, 256, 4, 4, 64, 1>(a, s);
+    case 11: return launch_b16<256, 256, 4, 4, 32, 1>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
