@@ -32,7 +32,7 @@ METRIC = ("compress & decompress input MB/s at d256×8L, 1000 chunks; "
 PEAK_TFLOPS = {"fp32": 157.3, "bf16": 2500.0}  # MI355X dense matrix peaks
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E peak
 GEMM_KERNEL = {"fp32": "boa::gemm_f32_kernel<128, 256, 4, 4, 16>",
-               "bf16": "boa::gemm_bf16_kernel<256, 256, 4, 4, 64>"}
+               "bf16": "boa::gemm_bf16_kernel<256, 256, 4, 4, 64, 1|2>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_c2_traffic.json")
 
 
@@ -99,7 +99,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1)
     ap.add_argument("--warmup", type=int, default=0)
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c5"],
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="BASELINE config (c2 is the metric's config)")
     ap.add_argument("--chunks", type=int, default=0)
     ap.add_argument("--chunk-len", type=int, default=0,
@@ -124,7 +124,8 @@ def main() -> int:
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the codec shards by chunk across GPUs, see DESIGN.md)", file=sys.stderr)
+              "(the path would shard by chunk across GPUs; no multi-GPU code is built)",
+              file=sys.stderr)
         return 2
 
     import numpy as np

@@ -173,11 +173,15 @@ static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 
 }
 
 // W must hold round_up(N, 256) rows (zero padded) for every configuration.
-// Chosen from a sweep on MI355X at compress shapes (M ~ 10^6): 256x256 with
+// Chosen from sweeps on MI355X at compress shapes (M ~ 10^6): 256x256 with
 // 16 waves of 64x64 (the LDS traffic per MFMA halves against 32x64 waves) for
-// N >= 256, 128x64 with 8 waves for the narrow x_proj.
+// N >= 256 -- one LDS stage where K or N is at least 512 (3-8 % faster
+// there), two for the 256x256 head GEMMs -- and 128x64 with 8 waves for the
+// narrow x_proj.  Smaller tiles (128x128, 8-wave 256x256) were 25-45 %
+// slower.
 hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
+  if (a.N >= 256 && (a.N >= 512 || a.K >= 512)) return launch_b16<256, 256, 4, 4, 64, 1>(a, s);
   if (a.N >= 256) return launch_b16<256, 256, 4, 4, 64>(a, s);
   return launch_b16<128, 64, 4, 2, 64>(a, s);
 }
@@ -197,6 +201,10 @@ hipError_t gemm_bf16_sweep(int cfg, const GemmB16Args& a, hipStream_t s) {
     case 9: return launch_b16<256, 256, 4, 4, 64, 1>(a, s);
     case 10: return launch_b16<128, 256, 4, 4, 64, 1>(a, s);
     case 11: return launch_b16<256, 256, 4, 4, 32, 1>(a, s);
+    case 12: return launch_b16<128, 128, 2, 2, 64, 1>(a, s);
+    case 13: return launch_b16<128, 128, 2, 2, 32, 2>(a, s);
+    case 14: return launch_b16<128, 256, 2, 4, 64, 1>(a, s);
+    case 15: return launch_b16<256, 128, 4, 2, 64, 1>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

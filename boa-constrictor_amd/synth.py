@@ -175,18 +175,37 @@ def gen_c3(n_blocks: int = 65536) -> bytes:
     return b"".join(parts)
 
 
-def gen_c4(n: int = 268_435_456) -> bytes:
+def _markov_fill():
+    """synth_markov_fill from libsynth.so (built next to this file), or None."""
+    import ctypes as C
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libsynth.so")
+    if not os.path.exists(path):
+        return None
+    fn = C.CDLL(path).synth_markov_fill
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p]
+    return fn
+
+
+def gen_c4(n: int = 268_435_456, block: int = 1 << 24) -> bytes:
     """First-order Markov bytes: rows of a 256x256 transition matrix are
-    Dirichlet(0.05) draws (seed 4), x0 = 0."""
+    Dirichlet(0.05) draws (seed 4), x0 = 0; x_{t+1} is the inverse-CDF draw
+    of row x_t at u_t, the uniforms taken from the same generator in blocks
+    (the same stream as one rng.random(n) call)."""
     rng = np.random.default_rng(4)
     P = rng.dirichlet(np.full(256, 0.05), size=256)
-    cum = np.cumsum(P, axis=1)
-    u = rng.random(n)
+    cum = np.ascontiguousarray(np.cumsum(P, axis=1))
     out = np.empty(n, np.uint8)
+    fill = _markov_fill()
     x = 0
-    for t in range(n):
-        out[t] = x
-        x = min(int(np.searchsorted(cum[x], u[t])), 255)
+    for s in range(0, n, block):
+        u = rng.random(min(block, n - s))
+        if fill is not None:
+            x = fill(cum.ctypes.data, u.ctypes.data, len(u), x, out[s:].ctypes.data)
+            continue
+        for t in range(len(u)):
+            out[s + t] = x
+            x = min(int(np.searchsorted(cum[x], u[t])), 255)
     return out.tobytes()
 
 

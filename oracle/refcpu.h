@@ -31,8 +31,9 @@
  *     every frequency >= 1; the reference's lock-step fix-up can leave a
  *     zero-frequency symbol (ref_cdf_build_mode documents both).
  *
- * Parity pinning of every function here is listed in DESIGN.md; functions
- * without an independent check say "parity unpinned" there.
+ * Every function here is pinned by tests/test_oracle_*.py and
+ * tests/test_golden.py: known-answer vectors, closed forms, invariants and
+ * independent restatements (float64 numpy, exact integer models).
  */
 #ifndef BOA_REFCPU_H
 #define BOA_REFCPU_H
