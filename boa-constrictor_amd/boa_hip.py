@@ -74,6 +74,7 @@ def lib():
             "boa_forward_chunk": (C.c_int, [P, P, i32, i32, P]),
             "boa_step_batch": (C.c_int, [P, P, i32, P, i32]),
             "boa_cdf_from_logits": (C.c_int, [P, P, P, i32, P]),
+            "boa_cdf_from_probs": (C.c_int, [P, P, i32, i32, P]),
             "boa_rc_encode_cdf": (C.c_int, [P, P, P, i32, i32, P, i64, P]),
             "boa_rc_decode_cdf": (C.c_int, [P, P, i32, i32, P, i64, P, P]),
             "boa_compress_device": (C.c_int, [P, P, i64, i64, i32, P, i64, P, P, P]),
@@ -155,6 +156,10 @@ class Codec:
     def cdf_from_logits(self, d_logits, d_bias, rows, d_qcdf):
         self._check(lib().boa_cdf_from_logits(self.h, _ptr(d_logits), _ptr(d_bias), rows,
                                               _ptr(d_qcdf)), "cdf_from_logits")
+
+    def cdf_from_probs(self, d_probs, rows, K, d_qcdf):
+        self._check(lib().boa_cdf_from_probs(self.h, _ptr(d_probs), rows, K, _ptr(d_qcdf)),
+                    "cdf_from_probs")
 
     def rc_encode_cdf(self, d_cdf, d_syms, n_sym, lanes, d_words, pitch_words, d_sizes):
         self._check(lib().boa_rc_encode_cdf(self.h, _ptr(d_cdf), _ptr(d_syms), n_sym, lanes,

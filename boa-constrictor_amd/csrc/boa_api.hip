@@ -1053,6 +1053,13 @@ int boa_cdf_from_logits(boa_ctx* c, const float* d_logits, const float* d_bias, 
   return BOA_OK;
 }
 
+int boa_cdf_from_probs(boa_ctx* c, const float* d_probs, int32_t rows, int32_t K,
+                       uint32_t* d_qcdf) {
+  if (!c || !d_probs || !d_qcdf || rows < 1 || K < 1 || K > 1024) return BOA_E_ARG;
+  HIP_TRY(c, launch_cdf_probs(d_probs, rows, K, d_qcdf, c->stream));
+  return BOA_OK;
+}
+
 int boa_rc_encode_cdf(boa_ctx* c, const uint32_t* d_cdf, const uint8_t* d_syms, int32_t n_sym,
                       int32_t lanes, uint32_t* d_words, int64_t pitch_words, int32_t* d_sizes) {
   if (!c || !d_cdf || !d_syms || !d_words || !d_sizes || n_sym < 0 || lanes < 1 ||

@@ -183,6 +183,8 @@ hipError_t launch_decode_step(const float* logits, const float* head_b2, float i
                               const uint64_t* offsets_words, const int32_t* sizes_words, int lanes,
                               hipStream_t s);
 // Test hooks: quantised CDFs of logits rows, and coder runs on explicit CDFs.
+// build_cdf_fast of the Python GPU codec: probs [rows][K] -> out [rows][K+1]
+hipError_t launch_cdf_probs(const float* probs, int rows, int K, uint32_t* out, hipStream_t s);
 hipError_t launch_cdf_rows(const float* logits, const float* bias, float inv_temp, int rows,
                            uint32_t* qcdf, hipStream_t s);
 hipError_t launch_rc_encode_cdf(const uint32_t* cdf, const uint8_t* syms, int n_sym, int lanes,

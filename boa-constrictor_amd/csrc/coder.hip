@@ -237,6 +237,48 @@ __global__ __launch_bounds__(256) void cdf_rows_kernel(const float* __restrict__
   }
 }
 
+// Integer CDF of a probability row the way the Python GPU codec builds it
+// (gpu_range_coder.py:57-79, build_cdf_fast): free weight 2^24 - K, the row
+// sum and the running sum in double in index order, low(i) =
+// trunc(running * (free / sum)) + i, low(K) = 2^24; a row whose sum is not
+// positive and finite gets the uniform CDF.  One thread per row (a plug-in
+// for probabilities computed elsewhere, not the codec's hot path).  A
+// negative scaled running sum, which valid probabilities never produce, is
+// taken as 0 here where the reference's conversion is undefined.
+__global__ void cdf_probs_kernel(const float* __restrict__ probs, int rows, int K,
+                                 uint32_t* __restrict__ out) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const float* p = probs + (size_t)r * K;
+  uint32_t* c = out + (size_t)r * (K + 1);
+  const uint32_t free_w = TOTAL - (uint32_t)K;
+  double norm = 0.0;
+  for (int i = 0; i < K; ++i) norm += (double)p[i];
+  if (!(norm > 0.0) || !__builtin_isfinite(norm)) {
+    const uint32_t step = free_w / (uint32_t)K + 1u;
+    uint32_t acc = 0;
+    for (int i = 0; i < K; ++i) {
+      c[i] = acc;
+      acc += step;
+    }
+  } else {
+    const double scale = (double)free_w / norm;
+    double cum = 0.0;
+    for (int i = 0; i < K; ++i) {
+      const double v = cum * scale;
+      c[i] = (uint32_t)(v > 0.0 ? v : 0.0) + (uint32_t)i;
+      cum += (double)p[i];
+    }
+  }
+  c[K] = TOTAL;
+}
+
+hipError_t launch_cdf_probs(const float* probs, int rows, int K, uint32_t* out, hipStream_t s) {
+  if (rows < 1 || K < 1 || K > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(cdf_probs_kernel, dim3((rows + 63) / 64), dim3(64), 0, s, probs, rows, K, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_cdf_rows(const float* logits, const float* bias, float inv_temp, int rows,
                            uint32_t* qcdf, hipStream_t s) {
   hipLaunchKernelGGL(cdf_rows_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, bias, inv_temp,

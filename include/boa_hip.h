@@ -111,6 +111,14 @@ int boa_step_batch(boa_ctx* ctx, const uint8_t* d_tokens, int32_t lanes, float* 
  * (range_coder_kernels.cu:856-932, 504-570). */
 int boa_cdf_from_logits(boa_ctx* ctx, const float* d_logits, const float* d_bias, int32_t rows,
                         uint32_t* d_qcdf);
+/* Alternate CDF plug-in: the integer CDF the Python GPU codec builds from
+ * probabilities (gpu_range_coder.py:57-79, build_cdf_fast), d_probs
+ * [rows][K] -> d_qcdf [rows][K+1], K in [1, 1024].  The range coder of that
+ * codec (gpu_range_coder.py:84-182) is the one behind boa_rc_encode_cdf /
+ * boa_rc_decode_cdf (which take K = 256 rows), so probabilities computed
+ * elsewhere can be coded into the Python codec's streams. */
+int boa_cdf_from_probs(boa_ctx* ctx, const float* d_probs, int32_t rows, int32_t K,
+                       uint32_t* d_qcdf);
 /* Range-code explicit integer CDFs, one stream per lane: d_cdf
  * [lanes][n_sym][257], d_syms [lanes][n_sym] -> words at d_words + lane *
  * pitch_words, word counts in d_sizes.  Replaces gpu_rc_init +

@@ -423,6 +423,29 @@ void ref_cdf_interval(const double* s_cdf, int32_t k, uint32_t* low, uint32_t* h
     *high = q_high(s_cdf, k);
 }
 
+/* gpu_range_coder.py:57-79 (build_cdf_fast, the Python GPU codec's CDF):
+ * double sums in index order; a negative scaled running sum (impossible for
+ * valid probabilities) is taken as 0. */
+void ref_cdf_from_probs(const float* probs, int32_t K, uint32_t* cdf) {
+    const uint32_t total = TOTAL_FREQ, free_w = total - (uint32_t)K;
+    double norm = 0.0;
+    for (int i = 0; i < K; ++i) norm += (double)probs[i];
+    if (!(norm > 0.0) || !isfinite(norm)) {
+        const uint32_t step = free_w / (uint32_t)K + 1u;
+        uint32_t acc = 0;
+        for (int i = 0; i < K; ++i) { cdf[i] = acc; acc += step; }
+    } else {
+        const double scale = (double)free_w / norm;
+        double cum = 0.0;
+        for (int i = 0; i < K; ++i) {
+            const double v = cum * scale;
+            cdf[i] = (uint32_t)(v > 0.0 ? v : 0.0) + (uint32_t)i;
+            cum += (double)probs[i];
+        }
+    }
+    cdf[K] = total;
+}
+
 void ref_cdf_quantize(const double* s_cdf, uint32_t* qcdf) {
     for (int k = 0; k < VOCAB; ++k) qcdf[k] = q_low(s_cdf, k);
     qcdf[256] = TOTAL_FREQ;

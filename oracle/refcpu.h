@@ -104,6 +104,8 @@ void ref_cdf_build_mode(const float* logits, const float* bias, float inv_temper
 void ref_cdf_interval(const double* s_cdf, int32_t k, uint32_t* low, uint32_t* high);
 /* all 257 integer boundaries low_0..low_255, 2^24 */
 void ref_cdf_quantize(const double* s_cdf, uint32_t* qcdf);
+/* gpu_range_coder.py:57-79 (build_cdf_fast): probs[K] -> cdf[K+1] */
+void ref_cdf_from_probs(const float* probs, int32_t K, uint32_t* cdf);
 /* first k with low_k <= target < high_k (0,0,0 if none) */
 int32_t ref_cdf_search(const double* s_cdf, uint32_t target, uint32_t* low, uint32_t* high);
 

@@ -81,6 +81,7 @@ def lib():
             "ref_cdf_build_mode": (None, [f32p, P, C.c_float, f64p, C.c_int32]),
             "ref_cdf_interval": (None, [f64p, C.c_int32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
             "ref_cdf_quantize": (None, [f64p, u32p]),
+            "ref_cdf_from_probs": (None, [f32p, C.c_int32, u32p]),
             "ref_cdf_search": (C.c_int32, [f64p, C.c_uint32, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
             "ref_model_load": (P, [C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.c_char_p, C.c_int32]),
             "ref_model_set_bf16": (C.c_int32, [P]),
@@ -127,6 +128,13 @@ def cdf_quantize(s_cdf):
     q = np.empty(257, np.uint32)
     lib().ref_cdf_quantize(np.ascontiguousarray(s_cdf, dtype=np.float64), q)
     return q
+
+
+def cdf_from_probs(probs):
+    p = np.ascontiguousarray(probs, dtype=np.float32)
+    out = np.empty(len(p) + 1, np.uint32)
+    lib().ref_cdf_from_probs(p, len(p), out)
+    return out
 
 
 def encode_cdf_stream(cdf, syms):

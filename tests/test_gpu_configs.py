@@ -112,6 +112,12 @@ def test_container_edges(torch_dev, oracle, w_c1, n, chunk, lanes, max_chunks):
     _same_container(oracle, w_c1, 64, 2, 16, data, chunk, lanes=lanes, max_chunks=max_chunks)
 
 
+def test_container_4096_lanes(torch_dev, oracle, w_c1):
+    """C4's lane count (4096 chunks decoded in one batch) at a short chunk."""
+    data = synth.gen_c4(4096 * 40 + 17)
+    _same_container(oracle, w_c1, 64, 2, 16, data, 40, lanes=4096)
+
+
 def test_cli_round_trip_matches_oracle(torch_dev, oracle, w_c1, tmp_path):
     """The C++ CLI (boa.cpp's command line) writes the oracle's container."""
     exe = os.path.join(os.path.dirname(__file__), "..", "boa-constrictor_amd", "boa")
