@@ -24,6 +24,52 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+// Epilogue of one tile: lane owns C[m][n .. n+3], m = m_blk + wm0 + 16p + j,
+// n = n_blk + wn0 + 16q + 4g.
+template <int TM, int TN>
+__device__ __forceinline__ void b16_epilogue(const GemmB16Args& a, const floatx4 (&acc)[TM][TN],
+                                             int m_blk, int n_blk, int wm0, int wn0, int j, int g) {
+#pragma unroll
+  for (int p = 0; p < TM; ++p) {
+    const int m = m_blk + wm0 + 16 * p + j;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int q = 0; q < TN; ++q) {
+      const int n = n_blk + wn0 + 16 * q + 4 * g;
+      if (n >= a.N) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = acc[p][q][e] + (a.bias ? a.bias[min(n + e, a.N - 1)] : 0.0f);
+        if (a.act == ACT_GELU) t = gelu<MATH_HW>(t);
+        else if (a.act == ACT_RELU) t = fmaxf(0.0f, t);
+        if (a.res) t = t + (n + e < a.N ? a.res[(size_t)m * a.ldr + n + e] : 0.0f);
+        v[e] = t;
+      }
+      const size_t o = (size_t)m * a.ldc + n;
+      if (n + 4 <= a.N) {
+        if (a.c_bf16)
+          *reinterpret_cast<ushort4*>(reinterpret_cast<uint16_t*>(a.C) + o) =
+              make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+        else
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.C) + o) =
+              make_float4(v[0], v[1], v[2], v[3]);
+        if (a.C2)
+          *reinterpret_cast<ushort4*>(a.C2 + o) =
+              make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (n + e >= a.N) break;
+          if (a.c_bf16) reinterpret_cast<uint16_t*>(a.C)[o + e] = f32_to_bf16(v[e]);
+          else reinterpret_cast<float*>(a.C)[o + e] = v[e];
+          if (a.C2) a.C2[o + e] = f32_to_bf16(v[e]);
+        }
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int NBUF = 2>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB16Args a,
                                                                            int swizzle) {
@@ -120,46 +166,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
 #undef BOA_B16_LOAD
 #undef BOA_B16_STORE
 
-  // Epilogue: lane owns C[m][n .. n+3], m = wm0 + 16p + j, n = wn0 + 16q + 4g.
-#pragma unroll
-  for (int p = 0; p < TM; ++p) {
-    const int m = m_blk + wm0 + 16 * p + j;
-    if (m >= a.M) continue;
-#pragma unroll
-    for (int q = 0; q < TN; ++q) {
-      const int n = n_blk + wn0 + 16 * q + 4 * g;
-      if (n >= a.N) continue;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float t = acc[p][q][e] + (a.bias ? a.bias[min(n + e, a.N - 1)] : 0.0f);
-        if (a.act == ACT_GELU) t = gelu<MATH_HW>(t);
-        else if (a.act == ACT_RELU) t = fmaxf(0.0f, t);
-        if (a.res) t = t + (n + e < a.N ? a.res[(size_t)m * a.ldr + n + e] : 0.0f);
-        v[e] = t;
-      }
-      const size_t o = (size_t)m * a.ldc + n;
-      if (n + 4 <= a.N) {
-        if (a.c_bf16)
-          *reinterpret_cast<ushort4*>(reinterpret_cast<uint16_t*>(a.C) + o) =
-              make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
-        else
-          *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.C) + o) =
-              make_float4(v[0], v[1], v[2], v[3]);
-        if (a.C2)
-          *reinterpret_cast<ushort4*>(a.C2 + o) =
-              make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (n + e >= a.N) break;
-          if (a.c_bf16) reinterpret_cast<uint16_t*>(a.C)[o + e] = f32_to_bf16(v[e]);
-          else reinterpret_cast<float*>(a.C)[o + e] = v[e];
-          if (a.C2) a.C2[o + e] = f32_to_bf16(v[e]);
-        }
-      }
-    }
-  }
+  b16_epilogue<TM, TN>(a, acc, m_blk, n_blk, wm0, wn0, j, g);
 }
 
 template <int BM, int BN, int WM_, int WN_, int BK, int NBUF = 2>
