@@ -195,10 +195,24 @@ __global__ __launch_bounds__(256) void conv_chunk_kernel(const TA* __restrict__ 
   float xm4 = s0.x, xm3 = s0.y, xm2 = s0.z, xm1 = s0.w;
   const TA* xp = xz + (size_t)b * T * (2 * di) + c;
   TA* op = out + (size_t)b * T * di + c;
-  for (int t = 0; t < T; ++t) {
-    float x0 = ldv(xp + (size_t)t * 2 * di);
-    // bf16 activations run on the hardware transcendentals (MATH_HW)
-    stv(op + (size_t)t * di, conv_value<sizeof(TA) == 2 ? MATH_HW : MATH_BF>(bias, xm3, xm2, xm1, x0, wv));
+  // bf16 activations run on the hardware transcendentals (MATH_HW)
+  constexpr int M = sizeof(TA) == 2 ? MATH_HW : MATH_BF;
+  // eight inputs are loaded before any is used, so eight loads of the
+  // wave are in flight instead of one
+  int t = 0;
+  for (; t + 8 <= T; t += 8) {
+    float xv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) xv[u] = ldv(xp + (size_t)(t + u) * 2 * di);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      stv(op + (size_t)(t + u) * di, conv_value<M>(bias, xm3, xm2, xm1, xv[u], wv));
+      xm4 = xm3; xm3 = xm2; xm2 = xm1; xm1 = xv[u];
+    }
+  }
+  for (; t < T; ++t) {
+    const float x0 = ldv(xp + (size_t)t * 2 * di);
+    stv(op + (size_t)t * di, conv_value<M>(bias, xm3, xm2, xm1, x0, wv));
     xm4 = xm3; xm3 = xm2; xm2 = xm1; xm1 = x0;
   }
   *st = make_float4(xm4, xm3, xm2, xm1);
