@@ -18,8 +18,6 @@
 
 namespace boa {
 
-constexpr int LN_MAXE = 16;  // d_model <= 512
-
 // four consecutive activations (fp32 or bf16 storage)
 __device__ __forceinline__ void ld4(const float* p, float* v) {
   const float4 t = *reinterpret_cast<const float4*>(p);
@@ -38,143 +36,183 @@ __device__ __forceinline__ void st4(uint16_t* p, const float* v) {
 }
 
 // -------------------------------------------------------------- LayerNorm
-// One 32-lane half-wave per row: lane l accumulates elements l, l+32, ...
-// in order, then lanes combine by the shuffle-down tree 16, 8, 4, 2, 1 and
-// lane 0's totals are broadcast (the reference's warp-per-row order).
-template <typename TO>
-__device__ __forceinline__ void ln_halfwave_row(const float* src, float* x_copy, TO* dst,
-                                                const float* __restrict__ w,
-                                                const float* __restrict__ b, int d, int l) {
-  float v[LN_MAXE];
-  float s = 0.0f, q = 0.0f;
-#pragma unroll
-  for (int e = 0; e < LN_MAXE; ++e) {
-    int idx = l + 32 * e;
-    if (idx < d) {
-      float val = src[idx];
-      v[e] = val;
-      s = s + val;
-      q = q + val * val;
-      if (x_copy) x_copy[idx] = val;
-    }
-  }
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) {
-    s = s + __shfl_down(s, off, 32);
-    q = q + __shfl_down(q, off, 32);
-  }
-  s = __shfl(s, 0, 32);
-  q = __shfl(q, 0, 32);
-  float mean = s / (float)d;
-  float var = q / (float)d - mean * mean;
-  float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
-#pragma unroll
-  for (int e = 0; e < LN_MAXE; ++e) {
-    int idx = l + 32 * e;
-    if (idx < d) stv(dst + idx, ((v[e] - mean) * inv_std) * w[idx] + b[idx]);
-  }
-}
+// Both kernels stage a block of rows in LDS with 16-byte loads (every load of
+// a thread issued before the first is used), take the statistics in the
+// reference's order from LDS, and store 16-byte (fp32) or 8-byte (bf16)
+// groups of the normalised rows.
 
-template <typename TO>
+// LN1: 8 rows per 256-thread block; half-wave h sums row h as the
+// reference's warp-per-row reduction does: lane l accumulates elements l,
+// l+32, ... in order, then the shuffle-down tree 16, 8, 4, 2, 1, lane 0's
+// totals broadcast.  Layer 0 gathers the embedding rows of the tile's
+// tokens and also stores them as x.
+template <typename TO, int D>
 __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb, TokenSrc tok,
                                                   int use_tok, int T, int t0, float* x, TO* xn,
                                                   const float* __restrict__ w,
-                                                  const float* __restrict__ b, int rows, int d) {
-  const int row = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
-  const int l = threadIdx.x & 31;
-  if (row >= rows) return;  // whole half-waves exit together
-  const float* src;
-  float* xc = nullptr;
-  if (use_tok) {
-    const int lane = row / T, t = row % T;
-    const int64_t pos = (int64_t)lane * tok.stride + t0 + t;
-    const uint32_t token = (t0 + t < tok.len && pos < tok.total) ? tok.base[pos] : 0u;
-    src = emb + (size_t)token * d;
-    xc = x + (size_t)row * d;
-  } else {
-    src = x + (size_t)row * d;
+                                                  const float* __restrict__ b, int rows) {
+  constexpr int RPB = 8, S = D + 4, DQ = D / 4;
+  constexpr int NQ = (RPB * DQ + 255) / 256;
+  __shared__ __align__(16) float tile[RPB * S];
+  const int r0 = blockIdx.x * RPB, tid = threadIdx.x;
+  float4 buf[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = tid + 256 * i, r = q / DQ, c4 = q % DQ;
+    if (q < RPB * DQ && r0 + r < rows) {
+      const float* src = x + (size_t)(r0 + r) * D;
+      if (use_tok) {
+        const int row = r0 + r, lane = row / T, t = row % T;
+        const int64_t pos = (int64_t)lane * tok.stride + t0 + t;
+        const uint32_t token = (t0 + t < tok.len && pos < tok.total) ? tok.base[pos] : 0u;
+        src = emb + (size_t)token * D;
+      }
+      buf[i] = *reinterpret_cast<const float4*>(src + 4 * c4);
+    }
   }
-  ln_halfwave_row(src, xc, xn + (size_t)row * d, w, b, d, l);
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = tid + 256 * i, r = q / DQ, c4 = q % DQ;
+    if (q < RPB * DQ && r0 + r < rows) {
+      *reinterpret_cast<float4*>(tile + r * S + 4 * c4) = buf[i];
+      if (use_tok) *reinterpret_cast<float4*>(x + (size_t)(r0 + r) * D + 4 * c4) = buf[i];
+    }
+  }
+  __syncthreads();
+  const int h = tid >> 5, l = tid & 31;
+  float* row = tile + h * S;
+  float sum = 0.0f, sq = 0.0f;
+#pragma unroll
+  for (int e = 0; e < D / 32; ++e) {
+    const float v = row[l + 32 * e];
+    sum = sum + v;
+    sq = sq + v * v;
+  }
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) {
+    sum = sum + __shfl_down(sum, off, 32);
+    sq = sq + __shfl_down(sq, off, 32);
+  }
+  sum = __shfl(sum, 0, 32);
+  sq = __shfl(sq, 0, 32);
+  const float mean = sum / (float)D;
+  const float var = sq / (float)D - mean * mean;
+  const float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
+#pragma unroll
+  for (int e = 0; e < D / 32; ++e) {
+    const int idx = l + 32 * e;
+    row[idx] = ((row[idx] - mean) * inv_std) * w[idx] + b[idx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = tid + 256 * i, r = q / DQ, c4 = q % DQ;
+    if (q < RPB * DQ && r0 + r < rows) st4(xn + (size_t)(r0 + r) * D + 4 * c4, tile + r * S + 4 * c4);
+  }
 }
 
 hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, void* xn,
                       const float* w, const float* b, int rows, int d, bool bf16, hipStream_t s) {
-  if (d > 32 * LN_MAXE) return hipErrorInvalidValue;
-  int blocks = (rows + 7) / 8;
-  if (bf16)
-    hipLaunchKernelGGL(ln1_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T,
-                       t0, x, (uint16_t*)xn, w, b, rows, d);
-  else
-    hipLaunchKernelGGL(ln1_kernel<float>, dim3(blocks), dim3(256), 0, s, emb, tok, emb ? 1 : 0, T,
-                       t0, x, (float*)xn, w, b, rows, d);
+  const dim3 grid((rows + 7) / 8), block(256);
+  const int ut = emb ? 1 : 0;
+#define BOA_LN1(Dv)                                                                          \
+  if (bf16)                                                                                  \
+    hipLaunchKernelGGL((ln1_kernel<uint16_t, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x, \
+                       (uint16_t*)xn, w, b, rows);                                           \
+  else                                                                                       \
+    hipLaunchKernelGGL((ln1_kernel<float, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x,    \
+                       (float*)xn, w, b, rows);
+  switch (d) {
+    case 64: BOA_LN1(64) break;
+    case 128: BOA_LN1(128) break;
+    case 256: BOA_LN1(256) break;
+    case 512: BOA_LN1(512) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BOA_LN1
   return hipGetLastError();
 }
 
 // LN2: per-row sums in element order (the reference's thread-per-row order).
-// A 256-thread block stages `rows_per_block` rows in LDS with coalesced
-// loads (row stride d+1 keeps the per-row sequential reads conflict-free),
-// one thread per row runs the sequential sums, then all threads normalise
-// and store coalesced.  In place is allowed.
-template <typename T>
-__global__ __launch_bounds__(256) void ln2_kernel(const T* x, T* out,
-                                                  const float* __restrict__ w,
-                                                  const float* __restrict__ b, int rows, int d,
-                                                  int rows_per_block) {
-  extern __shared__ float lds[];
-  float* tile = lds;                                   // [rows_per_block][d+1]
-  float* stats = lds + (size_t)rows_per_block * (d + 1);  // mean, inv_std per row
-  const int r0 = blockIdx.x * rows_per_block;
-  const int nr = min(rows_per_block, rows - r0);
-  const int dq = d / 4, S = d + 1;
-  for (int q = threadIdx.x; q < nr * dq; q += blockDim.x) {
-    const int r = q / dq, c4 = q % dq;
-    float v[4];
-    ld4(x + (size_t)(r0 + r) * d + 4 * c4, v);
-    float* dst = tile + r * S + 4 * c4;
-    dst[0] = v[0]; dst[1] = v[1]; dst[2] = v[2]; dst[3] = v[3];
+// RPB rows per 256-thread block; thread t < RPB runs row t's sequential
+// sums over the LDS copy (row stride D + 1 keeps those reads conflict-free).
+// In place is allowed.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void ln2_kernel(const T* x, T* out, const float* __restrict__ w,
+                                                  const float* __restrict__ b, int rows) {
+  constexpr int RPB = D <= 256 ? 32 : 16, S = D + 1, DQ = D / 4;
+  constexpr int NQ = (RPB * DQ + 255) / 256;
+  __shared__ float tile[RPB * S];
+  __shared__ float stats[2 * RPB];
+  const int r0 = blockIdx.x * RPB, tid = threadIdx.x;
+  float v[NQ][4];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = tid + 256 * i, r = q / DQ, c4 = q % DQ;
+    if (q < RPB * DQ && r0 + r < rows) ld4(x + (size_t)(r0 + r) * D + 4 * c4, v[i]);
   }
-  __syncthreads();
-  if (threadIdx.x < nr) {
-    const float* row = tile + threadIdx.x * S;
-    float s = 0.0f, q = 0.0f;
-    for (int i = 0; i < d; ++i) {
-      const float v = row[i];
-      s = s + v;
-      q = q + v * v;
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = tid + 256 * i, r = q / DQ, c4 = q % DQ;
+    if (q < RPB * DQ && r0 + r < rows) {
+      float* dst = tile + r * S + 4 * c4;
+      dst[0] = v[i][0]; dst[1] = v[i][1]; dst[2] = v[i][2]; dst[3] = v[i][3];
     }
-    const float mean = s / (float)d;
-    const float var = q / (float)d - mean * mean;
-    stats[2 * threadIdx.x] = mean;
-    stats[2 * threadIdx.x + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
   }
   __syncthreads();
-  for (int q = threadIdx.x; q < nr * dq; q += blockDim.x) {
-    const int r = q / dq, c4 = q % dq;
-    const float mean = stats[2 * r], inv_std = stats[2 * r + 1];
-    const float* src = tile + r * S + 4 * c4;
-    const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c4);
-    const float4 bv = *reinterpret_cast<const float4*>(b + 4 * c4);
-    float o[4];
-    o[0] = ((src[0] - mean) * inv_std) * wv.x + bv.x;
-    o[1] = ((src[1] - mean) * inv_std) * wv.y + bv.y;
-    o[2] = ((src[2] - mean) * inv_std) * wv.z + bv.z;
-    o[3] = ((src[3] - mean) * inv_std) * wv.w + bv.w;
-    st4(out + (size_t)(r0 + r) * d + 4 * c4, o);
+  if (tid < RPB && r0 + tid < rows) {
+    const float* row = tile + tid * S;
+    float s = 0.0f, q = 0.0f;
+    for (int i = 0; i < D; ++i) {
+      const float e = row[i];
+      s = s + e;
+      q = q + e * e;
+    }
+    const float mean = s / (float)D;
+    const float var = q / (float)D - mean * mean;
+    stats[2 * tid] = mean;
+    stats[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int q = tid + 256 * i, r = q / DQ, c4 = q % DQ;
+    if (q < RPB * DQ && r0 + r < rows) {
+      const float mean = stats[2 * r], inv_std = stats[2 * r + 1];
+      const float* src = tile + r * S + 4 * c4;
+      const float4 wv = *reinterpret_cast<const float4*>(w + 4 * c4);
+      const float4 bv = *reinterpret_cast<const float4*>(b + 4 * c4);
+      float o[4];
+      o[0] = ((src[0] - mean) * inv_std) * wv.x + bv.x;
+      o[1] = ((src[1] - mean) * inv_std) * wv.y + bv.y;
+      o[2] = ((src[2] - mean) * inv_std) * wv.z + bv.z;
+      o[3] = ((src[3] - mean) * inv_std) * wv.w + bv.w;
+      st4(out + (size_t)(r0 + r) * D + 4 * c4, o);
+    }
   }
 }
 
 hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, int rows, int d,
                       bool bf16, hipStream_t s) {
-  if (d % 4 || d > 512) return hipErrorInvalidValue;
-  // at most ~48 KB of LDS per block
-  const int rpb = std::min(64, (48 * 1024) / (4 * (d + 1)));
-  const size_t lds = sizeof(float) * ((size_t)rpb * (d + 1) + 2 * rpb);
-  if (bf16)
-    hipLaunchKernelGGL(ln2_kernel<uint16_t>, dim3((rows + rpb - 1) / rpb), dim3(256), lds, s,
-                       (const uint16_t*)x, (uint16_t*)out, w, b, rows, d, rpb);
-  else
-    hipLaunchKernelGGL(ln2_kernel<float>, dim3((rows + rpb - 1) / rpb), dim3(256), lds, s,
-                       (const float*)x, (float*)out, w, b, rows, d, rpb);
+#define BOA_LN2(Dv)                                                                             \
+  {                                                                                             \
+    constexpr int RPB = Dv <= 256 ? 32 : 16;                                                    \
+    const dim3 grid((rows + RPB - 1) / RPB), block(256);                                        \
+    if (bf16)                                                                                   \
+      hipLaunchKernelGGL((ln2_kernel<uint16_t, Dv>), grid, block, 0, s, (const uint16_t*)x,     \
+                         (uint16_t*)out, w, b, rows);                                           \
+    else                                                                                        \
+      hipLaunchKernelGGL((ln2_kernel<float, Dv>), grid, block, 0, s, (const float*)x,           \
+                         (float*)out, w, b, rows);                                              \
+  }
+  switch (d) {
+    case 64: BOA_LN2(64) break;
+    case 128: BOA_LN2(128) break;
+    case 256: BOA_LN2(256) break;
+    case 512: BOA_LN2(512) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BOA_LN2
   return hipGetLastError();
 }
 
