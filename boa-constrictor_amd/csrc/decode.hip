@@ -205,11 +205,26 @@ hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s) {
     case 8: return dec_launch<1, 2, 2, 4>(a, s);
     case 9: return dec_launch<2, 2, 1, 6>(a, s);
     case 10: return dec_launch<1, 1, 1, 2>(a, s);
+    case 11: return dec_launch<1, 4, 1, 4>(a, s);
+    case 12: return dec_launch<1, 4, 2, 2>(a, s);
+    case 13: return dec_launch<4, 1, 1, 4>(a, s);
+    case 14: return dec_launch<2, 1, 1, 8>(a, s);
+    case 15: return dec_launch<1, 2, 1, 8>(a, s);
+    case 16: return dec_launch<1, 2, 2, 2>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) { return dec_gemm_cfg(a, 0, s); }
+// Wave tiles by shape, from a sweep on MI355X (all configurations give the
+// same bits): K = 256 x N >= 1024 (in_proj, FF1) runs fastest on the smallest
+// register ring; from 2048 lanes on, 32 x 32 tiles halve the operand loads of
+// the K >= 512 projections and 64-lane tiles those of the heads.
+hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
+  int cfg = 4;
+  if (a.K <= 256 && a.N >= 1024) cfg = 10;
+  else if (a.M >= 2048 && a.N >= 256) cfg = a.K >= 512 ? 9 : 13;
+  return dec_gemm_cfg(a, cfg, s);
+}
 
 // Weight relayout for decode: W [K][ldw_in] row-major (the compress layout)
 // -> k-blocked [K/16][ldn][16].  Logical output column j maps to source
