@@ -58,7 +58,7 @@ __device__ __forceinline__ void scan_load(ScanCtx<DS, RB>& sc, const LayerW& Lw,
   for (int j = 0; j < RB; ++j) sc.wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; n += 4) {
-    float4 a = *reinterpret_cast<const float4*>(Lw.neg_exp_a + (size_t)c * DS + n);
+    float4 a = *reinterpret_cast<const float4*>(Lw.na2 + (size_t)c * DS + n);
     sc.na[n] = a.x; sc.na[n + 1] = a.y; sc.na[n + 2] = a.z; sc.na[n + 3] = a.w;
     float4 hv = *reinterpret_cast<const float4*>(ssm + n);
     sc.h[n] = hv.x; sc.h[n + 1] = hv.y; sc.h[n + 2] = hv.z; sc.h[n + 3] = hv.w;
@@ -76,6 +76,7 @@ __device__ __forceinline__ void scan_store(const ScanCtx<DS, RB>& sc, float* ssm
 
 // One token of one channel: dt = softplus(delta[0:r] . w_dt[:, c] + b_dt),
 // h_n = exp(-exp(A_log) dt) h_n + (dt B_n) u, y = sum_n h_n C_n + D u,
+// (the decay taken as 2^(na2_n dt), na2 = -exp(A_log) log2(e)),
 // out = y * (z * sigmoid(z)).  M selects the exp/log form (MATH_BF and
 // MATH_BR give the same results).
 template <int DS, int RB, int M = MATH_BF>
@@ -91,7 +92,7 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
   float y = 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; ++n) {
-    float dA = scan_exp_sel<M>(sc.na[n] * dt);
+    float dA = scan_exp2_sel<M>(sc.na[n] * dt);
     float dB = dt * Bv[n];
     sc.h[n] = dA * sc.h[n] + dB * u;
     y = y + sc.h[n] * Cv[n];

@@ -65,7 +65,7 @@ struct boa_ctx {
   struct DecW {
     const float *w_in, *w_x, *w_out, *w1, *w2;
     const float* w_dt;  // dt_proj weights, scan quad layout (decode.hip)
-    const float* na;    // -exp(A_log), scan quad layout
+    const float* na;    // -exp(A_log) log2(e), scan quad layout
   };
   int n_xdec = 0;  // decode x_proj width: dec_rb(r) + 2 ds
   float* dwbuf = nullptr;
@@ -574,9 +574,9 @@ __global__ void gather_first_kernel(const uint8_t* base, int64_t stride, int64_t
   first[b] = pos < total ? base[pos] : 0;
 }
 
-__global__ void neg_exp_kernel(const float* a_log, float* out, int n) {
+__global__ void na2_kernel(const float* a_log, float* out, int n) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = -expf_(a_log[i]);
+  if (i < n) out[i] = scan_na2(a_log[i]);
 }
 
 __global__ void decode_init_kernel(const uint8_t* first, const int32_t* lens, uint8_t* tok,
@@ -816,7 +816,7 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
     return place(std::move(v));
   };
   struct LayerOff {
-    size_t ln1_w, ln1_b, w_in, b_in, conv_w, conv_b, w_x, w_dt, b_dt, a_log, neg_a, dd, w_out, b_out,
+    size_t ln1_w, ln1_b, w_in, b_in, conv_w, conv_b, w_x, w_dt, b_dt, a_log, na2, dd, w_out, b_out,
         ln2_w, ln2_b, w1, b1, w2, b2;
   };
   std::vector<LayerOff> lo(D.L);
@@ -841,7 +841,7 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
     }
     o.b_dt = raw(D.di);
     o.a_log = raw((size_t)D.di * D.ds);
-    o.neg_a = place(std::vector<float>((size_t)D.di * D.ds, 0.0f));
+    o.na2 = place(std::vector<float>((size_t)D.di * D.ds, 0.0f));
     o.dd = raw(D.di);
     o.w_out = linear_t(D.d, D.di, D.ld_out);
     o.b_out = raw(D.d);
@@ -875,14 +875,14 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
     LayerW& L = c->layers[l];
     L.ln1_w = w + o.ln1_w; L.ln1_b = w + o.ln1_b; L.w_in = w + o.w_in; L.b_in = w + o.b_in;
     L.conv_w = w + o.conv_w; L.conv_b = w + o.conv_b; L.w_x = w + o.w_x; L.w_dt = w + o.w_dt;
-    L.b_dt = w + o.b_dt; L.neg_exp_a = w + o.neg_a; L.dd = w + o.dd; L.w_out = w + o.w_out;
+    L.b_dt = w + o.b_dt; L.na2 = w + o.na2; L.dd = w + o.dd; L.w_out = w + o.w_out;
     L.b_out = w + o.b_out; L.ln2_w = w + o.ln2_w; L.ln2_b = w + o.ln2_b; L.w1 = w + o.w1;
     L.b1 = w + o.b1; L.w2 = w + o.w2; L.b2 = w + o.b2;
-    // -exp(A_log) once per load (mamba_kernels.cu:430-437), on the device so
+    // -exp(A_log) log2(e) once per load (mamba_kernels.cu:430-437), on the device so
     // that it is the same exp the kernels use.
     const int nA = D.di * D.ds;
-    hipLaunchKernelGGL(neg_exp_kernel, dim3((nA + 255) / 256), dim3(256), 0, c->stream,
-                       w + o.a_log, w + o.neg_a, nA);
+    hipLaunchKernelGGL(na2_kernel, dim3((nA + 255) / 256), dim3(256), 0, c->stream,
+                       w + o.a_log, w + o.na2, nA);
     HIP_TRY(c, hipGetLastError());
   }
   // k-blocked copies of the Linear weights for the decode step; x_proj's
@@ -926,7 +926,7 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
   for (int l = 0; l < D.L; ++l) {
     float* wq = c->dwbuf + wdt_off + (size_t)l * D.di * (rb + D.ds);
     float* nq = wq + (size_t)D.di * rb;
-    HIP_TRY(c, launch_dec_scan_params(c->layers[l].w_dt, c->layers[l].neg_exp_a, wq, nq, D.r, rb,
+    HIP_TRY(c, launch_dec_scan_params(c->layers[l].w_dt, c->layers[l].na2, wq, nq, D.r, rb,
                                       D.ds, D.di, c->stream));
     c->dlayers[l].w_dt = wq;
     c->dlayers[l].na = nq;

@@ -49,7 +49,7 @@ struct TokenSrc {
 };
 
 struct LayerW {
-  const float *ln1_w, *ln1_b, *w_in, *b_in, *conv_w, *conv_b, *w_x, *w_dt, *b_dt, *neg_exp_a, *dd,
+  const float *ln1_w, *ln1_b, *w_in, *b_in, *conv_w, *conv_b, *w_x, *w_dt, *b_dt, *na2, *dd,
       *w_out, *b_out, *ln2_w, *ln2_b, *w1, *b1, *w2, *b2;
 };
 

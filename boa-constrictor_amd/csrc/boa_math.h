@@ -73,13 +73,26 @@ BOA_DEV float expf_(float x) {
   return x != x ? x : res;
 }
 
-// exp(x) on the selective scan's domain x = -exp(A_log) * dt <= 0: x is
-// clamped into [-87, 0] first (fmaxf turns a NaN into -87) and x < -87
-// gives 0.  Equal to expf_ on [-87, 0], with one clamp and one select
-// instead of expf_'s clamp and three selects.
-BOA_DEV float scan_exp(float x) {
-  const float e = exp_core(__builtin_fminf(__builtin_fmaxf(x, -87.0f), 0.0f));
-  return x < -87.0f ? 0.0f : e;
+// The selective scan's decay exp(-exp(A_log) dt) in base 2: the weights
+// hold na2 = -exp(A_log) * log2(e) (two fp32 roundings, done once at load)
+// and the scan takes 2^t of t = na2 * dt <= 0.  t is clamped into
+// [-126, 0] (fmaxf turns a NaN into -126), split as k + r with k = rint(t)
+// and r = t - k in [-1/2, 1/2] (exact); 2^r comes from a degree-6
+// polynomial with 2^0 = 1 exact, fitted to the relative error of 2^r on
+// [-1/2, 1/2] (under one ulp with fp32 fma evaluation), and 2^k is applied
+// with ldexp.  The least result is 2^-126: no subnormal is produced.
+BOA_DEV float scan_exp2(float t) {
+  const float s = __builtin_fminf(__builtin_fmaxf(t, -126.0f), 0.0f);
+  const float k = __builtin_rintf(s);
+  const float r = s - k;
+  float p = 0x1.41fbbap-13f;
+  p = __builtin_fmaf(p, r, 0x1.5f3e54p-10f);
+  p = __builtin_fmaf(p, r, 0x1.3b2d4cp-7f);
+  p = __builtin_fmaf(p, r, 0x1.c6aee8p-5f);
+  p = __builtin_fmaf(p, r, 0x1.ebfbdcp-3f);
+  p = __builtin_fmaf(p, r, 0x1.62e430p-1f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)k);
 }
 
 BOA_DEV float expf_br(float x) {
@@ -203,8 +216,13 @@ BOA_DEV float silu(float x) {
 template <int M = MATH_BF>
 BOA_DEV float softplus(float x) { return log_sel<M>(1.0f + exp_sel<M>(x)); }
 
-// exp on the scan's domain (see scan_exp) in the chosen form
+// 2^t on the scan's domain (see scan_exp2) in the chosen form
 template <int M>
-BOA_DEV float scan_exp_sel(float x) { return M == MATH_HW ? hw_exp(x) : scan_exp(x); }
+BOA_DEV float scan_exp2_sel(float t) {
+  return M == MATH_HW ? __builtin_amdgcn_exp2f(t) : scan_exp2(t);
+}
+
+// the scan's base-2 decay coefficient from A_log (see scan_exp2)
+BOA_DEV float scan_na2(float a_log) { return -expf_(a_log) * 1.44269504088896340736f; }
 
 }  // namespace boa

@@ -253,7 +253,7 @@ hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* o
 
 // Per-channel scan parameters in the decode scan's quad layout: element
 // (c, j) of a [di][n] table at (((c/16) n/4 + j/4) 16 + c%16) 4 + j%4.
-// dt_proj weights come from [r][di] (zero padded to rb), -exp(A) from
+// dt_proj weights come from [r][di] (zero padded to rb), -exp(A_log) log2(e) from
 // [di][ds].
 __device__ __forceinline__ size_t quad_idx(int c, int j, int n) {
   return ((size_t)((c >> 4) * (n >> 2) + (j >> 2)) * 16 + (c & 15)) * 4 + (j & 3);
@@ -453,7 +453,7 @@ __device__ __forceinline__ void dec_load16(const float* p, float* f) {
 // The decode x_proj writes its row with dt_in at features [0, r), zeros up
 // to RB, B at [RB, RB + DS) and C at [RB + DS, RB + 2 DS), so the thread
 // loads whole 16-feature blocks (float4) and indexes them at compile time.
-// State, -exp(A) and dt_proj weights are stored in quads of four n (or j)
+// State, -exp(A_log) log2(e) and dt_proj weights are stored in quads of four n (or j)
 // with the 16 channels of a channel block innermost, so that every float4
 // load of a wavefront reads one contiguous 1 KB (state) or 256 B span:
 //   h[c][n] of lane m at ((((c/16) DS/4 + n/4) ld_state + m) 16 + c%16) 4 + n%4

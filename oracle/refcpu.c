@@ -73,13 +73,30 @@ float ref_expf(float x) {
     return exp_core(x);
 }
 
-/* exp(x) on the selective scan's domain x = -exp(A_log) * dt <= 0: x is
- * clamped into [-87, 0] first (fmaxf turns a NaN into -87) and x < -87
- * gives 0.  Equal to ref_expf on [-87, 0]. */
-float ref_scan_exp(float x) {
-    float e = exp_core(fminf(fmaxf(x, -87.0f), 0.0f));
-    return x < -87.0f ? 0.0f : e;
+/* The selective scan's decay exp(-exp(A_log) dt) in base 2: the layer
+ * holds na2 = -exp(A_log) * log2(e) (ref_scan_na2) and the scan takes
+ * 2^t of t = na2 * dt <= 0.  t is clamped into [-126, 0] (fmaxf turns a
+ * NaN into -126) and split as k + r, k = rint(t), r = t - k in [-1/2, 1/2]
+ * (exact); 2^r is a degree-6 polynomial with 2^0 = 1 exact (coefficients
+ * fitted to the relative error of 2^r on [-1/2, 1/2]) and 2^k is applied
+ * with ldexpf, exact here.  The least result is 2^-126.  This is the exp
+ * of the HIP scan kernels, operation for operation. */
+float ref_scan_exp2(float t) {
+    float s = fminf(fmaxf(t, -126.0f), 0.0f);
+    float k = rintf(s);
+    float r = s - k;
+    float p = 0x1.41fbbap-13f;
+    p = fmaf(p, r, 0x1.5f3e54p-10f);
+    p = fmaf(p, r, 0x1.3b2d4cp-7f);
+    p = fmaf(p, r, 0x1.c6aee8p-5f);
+    p = fmaf(p, r, 0x1.ebfbdcp-3f);
+    p = fmaf(p, r, 0x1.62e430p-1f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)k);
 }
+
+/* the scan's base-2 decay coefficient -exp(A_log) * log2(e) */
+float ref_scan_na2(float a_log) { return -ref_expf(a_log) * 1.44269504088896340736f; }
 
 /* log(y) for y > 0: y = 2^e * m with m in [sqrt(1/2), sqrt(2)],
  * log(m) = 2 atanh(s), s = (m-1)/(m+1), series to s^11. */
@@ -477,7 +494,7 @@ typedef struct {
     float *ln2_w, *ln2_b;
     float *w1, *b1;          /* [d][4d], [4d] */
     float *w2, *b2;          /* [4d][d], [d] */
-    float *neg_exp_a;        /* -exp(A_log), [di][ds] (mamba_kernels.cu:430-437) */
+    float *na2;              /* -exp(A_log) log2(e), [di][ds] (mamba_kernels.cu:430-437) */
 } ref_layer;
 
 struct ref_model {
@@ -591,8 +608,8 @@ ref_model* ref_model_load(const char* path, int32_t d, int32_t L, int32_t ds, ch
         rd_linear_t(&rd, y->w1, 4 * d, d); rd_vec(&rd, y->b1, 4 * d);
         y->w2 = fa((size_t)4 * d * d); y->b2 = fa(d);
         rd_linear_t(&rd, y->w2, d, 4 * d); rd_vec(&rd, y->b2, d);
-        y->neg_exp_a = fa((size_t)di * ds);
-        for (int i = 0; i < di * ds; ++i) y->neg_exp_a[i] = -ref_expf(y->a_log[i]);
+        y->na2 = fa((size_t)di * ds);
+        for (int i = 0; i < di * ds; ++i) y->na2[i] = ref_scan_na2(y->a_log[i]);
     }
     m->hw1 = fa((size_t)d * d); m->hb1 = fa(d);
     rd_linear_t(&rd, m->hw1, d, d); rd_vec(&rd, m->hb1, d);
@@ -613,7 +630,7 @@ void ref_model_free(ref_model* m) {
         ref_layer* y = &m->layers[l];
         float* ps[] = {y->ln1_w, y->ln1_b, y->w_in, y->b_in, y->conv_w, y->conv_b, y->w_x,
                        y->w_dt, y->b_dt, y->a_log, y->dd, y->w_out, y->b_out, y->ln2_w,
-                       y->ln2_b, y->w1, y->b1, y->w2, y->b2, y->neg_exp_a};
+                       y->ln2_b, y->w1, y->b1, y->w2, y->b2, y->na2};
         for (size_t i = 0; i < sizeof ps / sizeof ps[0]; ++i) free(ps[i]);
     }
     free(m->layers);
@@ -762,10 +779,10 @@ static inline float scan_row(const ref_layer* Ly, const ref_model* m, int dch, c
     float dt = ref_softplus(acc + Ly->b_dt[dch]);
     const float* Bv = delta_row + r;
     const float* Cv = delta_row + r + ds;
-    const float* na = Ly->neg_exp_a + (size_t)dch * ds;
+    const float* na = Ly->na2 + (size_t)dch * ds;
     float y = 0.0f;
     for (int n = 0; n < ds; ++n) {
-        float dA = ref_scan_exp(na[n] * dt);
+        float dA = ref_scan_exp2(na[n] * dt);
         float dB = dt * Bv[n];
         h[n] = dA * h[n] + dB * u;
         y = y + h[n] * Cv[n];

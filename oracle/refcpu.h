@@ -47,7 +47,8 @@ extern "C" {
 
 /* ---------------------------------------------------------------- math */
 float ref_expf(float x);
-float ref_scan_exp(float x);      /* exp on the scan's domain x <= 0 (clamped, NaN -> -87) */
+float ref_scan_exp2(float t);     /* 2^t on the scan's domain t <= 0 (clamped to [-126, 0], NaN -> -126) */
+float ref_scan_na2(float a_log);  /* -exp(A_log) * log2(e), the scan's base-2 decay coefficient */
 float ref_logf(float x);
 float ref_repro_exp(float x);     /* activations.hpp:33-84 (device branch) */
 float ref_repro_tanh(float x);    /* activations.hpp:87-98 */

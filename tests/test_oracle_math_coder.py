@@ -43,20 +43,45 @@ def test_expf_ulp_bound(oracle):
     assert np.isnan(L.ref_expf(float("nan")))
 
 
-def test_scan_exp_domain(oracle):
-    """The scan's exp equals ref_expf on [-87, 0] bit for bit (so the ulp
-    bound above carries over), is 0 below -87, saturates at exp(0) above 0
-    and maps a NaN to exp(-87)."""
+def test_scan_exp2(oracle):
+    """The scan's base-2 exp: within one ulp of float64 2^t on [-126, 0],
+    exact at integers (2^0 = 1 and ldexp are exact), clamped below -126 and
+    above 0, NaN mapped to 2^-126."""
     L = oracle.lib()
-    xs = np.concatenate([np.linspace(-87.0, 0.0, 50001, dtype=np.float32),
-                         -np.geomspace(1e-30, 87.0, 20001).astype(np.float32),
-                         np.array([-0.0, -87.0], np.float32)])
-    a = vec(L.ref_scan_exp, xs)
-    b = vec(L.ref_expf, xs)
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
-    assert L.ref_scan_exp(-87.00001) == 0.0 and L.ref_scan_exp(float("-inf")) == 0.0
-    assert L.ref_scan_exp(3.0) == 1.0
-    assert L.ref_scan_exp(float("nan")) == L.ref_expf(-87.0)
+    ts = np.concatenate([np.linspace(-126.0, 0.0, 200001, dtype=np.float32),
+                         -np.geomspace(1e-30, 126.0, 40001).astype(np.float32),
+                         np.linspace(-0.5, 0.5, 20001, dtype=np.float32).clip(None, 0)])
+    got = vec(L.ref_scan_exp2, ts)
+    err = ulp_err(got, np.exp2(ts.astype(np.float64)))
+    assert err.max() <= 1.0, f"max ulp error {err.max()}"
+    for k in range(127):
+        assert L.ref_scan_exp2(float(-k)) == 2.0 ** -k
+    tiny = 2.0 ** -126
+    for t in (-126.5, -200.0, float("-inf"), float("nan")):
+        assert L.ref_scan_exp2(t) == tiny
+    assert L.ref_scan_exp2(3.0) == 1.0 and L.ref_scan_exp2(-0.0) == 1.0
+
+
+def test_scan_decay_against_float64(oracle):
+    """exp(-exp(A_log) dt) taken as 2^(na2 dt): the three fp32 roundings
+    before the exp (exp(A_log), the log2(e) product, the dt product) bound
+    the error by a few ulp times |t|, against float64 exp(-exp(a) dt)."""
+    L = oracle.lib()
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-4, 4, 4000).astype(np.float32)
+    dt = np.exp(rng.uniform(-8, 3, 4000)).astype(np.float32)
+    got = np.array([L.ref_scan_exp2(np.float32(np.float32(L.ref_scan_na2(float(x))) * np.float32(d)))
+                    for x, d in zip(a, dt)])
+    x64 = -np.exp(a.astype(np.float64)) * dt.astype(np.float64)
+    want = np.exp(x64)
+    keep = x64 > -87.0
+    t = np.abs(x64[keep]) / np.log(2.0)
+    rel = np.abs(got[keep] - want[keep]) / want[keep]
+    assert np.all(rel <= 2.0 ** -23 * (2.0 + 4.0 * t)), rel.max()
+    # the decay coefficient itself: two fp32 roundings of -exp(a) log2(e)
+    na2 = np.array([L.ref_scan_na2(float(x)) for x in a])
+    want_na2 = -np.exp(a.astype(np.float64)) / np.log(2.0)
+    assert np.all(np.abs(na2 - want_na2) <= 4 * 2.0 ** -24 * np.abs(want_na2))
 
 
 def test_logf_ulp_bound(oracle):
