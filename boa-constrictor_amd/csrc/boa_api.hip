@@ -441,22 +441,33 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
   hipStream_t saved = c->stream;
   c->stream = s;  // dgemm and timed() launch on c->stream
   hipError_t e = hipSuccess;
+  // LayerNorm fused into in_proj and FF1 up to 2048 lanes; above that the
+  // separate kernels spread the work better (MI355X sweep)
+  const bool fuse_ln =
+      lanes <= 2048 && dec_ln_gemm_fits(D.d, 2 * D.di) && dec_ln_gemm_fits(D.d, 4 * D.d);
   for (int l = 0; l < D.L && !e; ++l) {
     const LayerW& W = c->layers[l];
     const boa_ctx::DecW& DW = c->dlayers[l];
     float* conv = dec_conv_of(c, l) + (size_t)lane0 * 4;
     float* ssm = dec_ssm_of(c, l) + (size_t)lane0 * 64;
-    e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
-      return launch_dec_ln1(l == 0 ? c->emb : nullptr, tok, xt, xnt, W.ln1_w, W.ln1_b, lanes, D.d,
-                            ld, l == 0 ? t_counter : nullptr, s);
-    });
-    if (!e) {
-      DecGemmArgs a{};
-      a.Xt = xnt; a.ldx = ld; a.W = DW.w_in; a.ldw = 2 * D.di; a.C = zt; a.ldc = ld;
-      a.bias = W.b_in; a.M = lanes; a.N = 2 * D.di; a.K = D.d; a.act = ACT_NONE;
-      a.conv_di = D.di; a.conv_state = conv; a.ld_state = ld; a.conv_w = W.conv_w;
-      a.conv_b = W.conv_b; a.conv_out = cvt;
-      e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
+    DecGemmArgs a{};
+    a.Xt = xnt; a.ldx = ld; a.W = DW.w_in; a.ldw = 2 * D.di; a.C = zt; a.ldc = ld;
+    a.bias = W.b_in; a.M = lanes; a.N = 2 * D.di; a.K = D.d; a.act = ACT_NONE;
+    a.conv_di = D.di; a.conv_state = conv; a.ld_state = ld; a.conv_w = W.conv_w;
+    a.conv_b = W.conv_b; a.conv_out = cvt;
+    if (fuse_ln) {  // LN1 in front of in_proj, in one kernel
+      a.Xt = xt;
+      e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * a.N * a.K, [&] {
+        return launch_dec_ln_gemm(1, a, l == 0 ? c->emb : nullptr, tok, xt, W.ln1_w, W.ln1_b,
+                                  l == 0 ? t_counter : nullptr, s);
+      });
+    } else {
+      e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
+        return launch_dec_ln1(l == 0 ? c->emb : nullptr, tok, xt, xnt, W.ln1_w, W.ln1_b, lanes,
+                              D.d, ld, l == 0 ? t_counter : nullptr, s);
+      });
+      if (!e)
+        e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
     }
     if (!e) e = dgemm(c, cvt, DW.w_x, rows, ld, nullptr, nullptr, lanes, c->n_xdec, D.di, ACT_NONE);
     if (!e)
@@ -464,10 +475,18 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
         return launch_dec_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, s);
       });
     if (!e) e = dgemm(c, yt, DW.w_out, ot, ld, W.b_out, nullptr, lanes, D.d, D.di, ACT_NONE);
-    if (!e)
+    if (!e && fuse_ln) {  // LN2 in front of FF1, in one kernel
+      DecGemmArgs f{};
+      f.Xt = ot; f.ldx = ld; f.W = DW.w1; f.ldw = 4 * D.d; f.C = hidt; f.ldc = ld;
+      f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU;
+      e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * f.N * f.K, [&] {
+        return launch_dec_ln_gemm(2, f, nullptr, nullptr, nullptr, W.ln2_w, W.ln2_b, nullptr, s);
+      });
+    } else if (!e) {
       e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d,
                 [&] { return launch_dec_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
-    if (!e) e = dgemm(c, xnt, DW.w1, hidt, ld, W.b1, nullptr, lanes, 4 * D.d, D.d, ACT_GELU);
+      if (!e) e = dgemm(c, xnt, DW.w1, hidt, ld, W.b1, nullptr, lanes, 4 * D.d, D.d, ACT_GELU);
+    }
     if (!e) e = dgemm(c, hidt, DW.w2, xt, ld, W.b2, xt, lanes, D.d, 4 * D.d, ACT_NONE);
   }
   if (!e) e = dgemm(c, xt, c->dhw1, ot, ld, c->hb1, nullptr, lanes, D.d, D.d, ACT_RELU);

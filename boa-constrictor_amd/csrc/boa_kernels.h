@@ -111,6 +111,14 @@ struct DecGemmArgs {
   const float* conv_w; const float* conv_b; float* conv_out;
 };
 hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s);
+// LayerNorm (mode 1: LN1, mode 2: LN2; weights lw, lb) of the K = d features
+// of a.Xt fused in front of the GEMM a (in_proj or FF1).  With emb, layer
+// 0's LN1: rows are emb[tok[m]] and are also stored as x (k-blocked, xt),
+// and *t_counter is incremented.  Needs d in {64, 128, 256} and N % 64 == 0.
+bool dec_ln_gemm_fits(int d, int N);
+hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, const uint8_t* tok,
+                              float* xt, const float* lw, const float* lb, int* t_counter,
+                              hipStream_t s);
 // explicit wave-tile configuration (tile sweeps)
 hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s);
 hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* out, int K, int ldn,

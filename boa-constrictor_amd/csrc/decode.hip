@@ -226,6 +226,201 @@ hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
   return dec_gemm_cfg(a, cfg, s);
 }
 
+// ------------------------------------------------ LayerNorm + GEMM (K = d)
+// in_proj (after LN1) and FF1 (after LN2) take the normalised d features of
+// a lane as their whole K.  A block of 1024 threads owns 64 lanes x 64 output
+// features:
+//   1. it copies the 64 lanes' k-blocked rows and the 64 weight rows into
+//      LDS (per 16-k block one contiguous 4 KB span each; every load of the
+//      block is issued before the first use);
+//   2. it computes each lane's mean and rstd in the LayerNorm's reduction
+//      order (dec_ln_kernel) and normalises the rows in LDS with the same
+//      operations, so the operands are the bits the LayerNorm would store;
+//   3. each of the 16 waves runs one 16 x 16 tile from LDS, k in the order
+//      of dec_mainloop (one fma chain per output, the same bits);
+//   4. the epilogue is dec_epilogue (conv step, activation, stores).
+// Against LayerNorm + dec_gemm this removes a launch and the normalised
+// rows' round trip through memory, and the block's waves share their
+// operand loads.  Layer 0's LN1 gathers the embedding rows and the n-block
+// 0 blocks store them as x.
+template <int MODE, int NB, bool EMB>
+__global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const float* __restrict__ emb,
+                                                           const uint8_t* __restrict__ tok, float* xt,
+                                                           const float* __restrict__ lw,
+                                                           const float* __restrict__ lb,
+                                                           int* t_counter) {
+  constexpr int d = NB * 16;
+  constexpr int TILE = NB * 64 * 16;  // floats of a 64-row k-blocked tile
+  constexpr int SQ = NB / 4;          // staged float4s per thread and operand
+  static_assert(NB % 4 == 0, "d must be a multiple of 64");
+  __shared__ __align__(16) float xs[TILE];
+  __shared__ __align__(16) float ws[TILE];
+  __shared__ float lwb[2 * d];
+  __shared__ float stats[2 * 64];
+  if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
+  const int tid = threadIdx.x;
+  const int n_blocks = a.N / 64;
+  const int m0 = (blockIdx.x / n_blocks) * 64, n0 = (blockIdx.x % n_blocks) * 64;
+
+  // 1. stage weights, LayerNorm parameters and rows: float4 r = tid % 256 of
+  // 16-k block q = 4 it + tid / 256 (row r / 4, quarter r % 4)
+  const int r = tid & 255, ml = r >> 2, a4 = r & 3;
+  const int m = min(m0 + ml, a.M - 1);  // rows past M are normalised, never stored
+  float4 wr[SQ], xr[SQ];
+  const float4* W4 = reinterpret_cast<const float4*>(a.W);
+#pragma unroll
+  for (int it = 0; it < SQ; ++it) {
+    const int q = 4 * it + (tid >> 8);
+    wr[it] = W4[((size_t)q * a.ldw + n0) * 4 + r];
+  }
+  const float* erow = EMB ? emb + (size_t)tok[m] * d : nullptr;
+#pragma unroll
+  for (int it = 0; it < SQ; ++it) {
+    const int q = 4 * it + (tid >> 8);
+    xr[it] = EMB ? *reinterpret_cast<const float4*>(erow + 16 * q + 4 * a4)
+                 : reinterpret_cast<const float4*>(a.Xt)[((size_t)q * a.ldx + m) * 4 + a4];
+  }
+  for (int k = tid; k < d; k += 1024) { lwb[k] = lw[k]; lwb[d + k] = lb[k]; }
+#pragma unroll
+  for (int it = 0; it < SQ; ++it) {
+    const int q = 4 * it + (tid >> 8);
+    reinterpret_cast<float4*>(ws)[q * 256 + r] = wr[it];
+    float* row = xs + (q * 64 + ml) * 16;
+    if (EMB) {  // natural feature order in, k-blocked positions out
+      const float e4[4] = {xr[it].x, xr[it].y, xr[it].z, xr[it].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) row[dperm(4 * a4 + e)] = e4[e];
+    } else {
+      reinterpret_cast<float4*>(row)[a4] = xr[it];
+    }
+  }
+  __syncthreads();
+  if (EMB && n0 == 0 && m0 + ml < a.M) {  // layer 0: x = embedding rows
+#pragma unroll
+    for (int it = 0; it < SQ; ++it) {
+      const int q = 4 * it + (tid >> 8);
+      reinterpret_cast<float4*>(xt)[((size_t)q * a.ldx + m0 + ml) * 4 + a4] =
+          reinterpret_cast<const float4*>(xs + (q * 64 + ml) * 16)[a4];
+    }
+  }
+
+  // 2. statistics (the orders of dec_ln_kernel) and normalisation
+  if (MODE == 1) {
+    const int lj = tid >> 4, l = tid & 15;
+    auto xat = [&](int f) { return xs[((f >> 4) * 64 + lj) * 16 + dperm(f & 15)]; };
+    float s0 = 0.0f, q0 = 0.0f, s1 = 0.0f, q1 = 0.0f;
+#pragma unroll
+    for (int f = l; f < d; f += 32) {
+      const float x = xat(f);
+      s0 = s0 + x;
+      q0 = q0 + x * x;
+    }
+#pragma unroll
+    for (int f = l + 16; f < d; f += 32) {
+      const float x = xat(f);
+      s1 = s1 + x;
+      q1 = q1 + x * x;
+    }
+    float sum = s0 + s1, sq = q0 + q1;
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+      sum = sum + __shfl_down(sum, off, 16);
+      sq = sq + __shfl_down(sq, off, 16);
+    }
+    if (l == 0) {
+      const float mean = sum / (float)d;
+      const float var = sq / (float)d - mean * mean;
+      stats[2 * lj] = mean;
+      stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    }
+  } else if (tid < 64) {
+    float sum = 0.0f, sq = 0.0f;
+#pragma unroll 2
+    for (int q = 0; q < NB; ++q) {
+      const float4* row = reinterpret_cast<const float4*>(xs + (q * 64 + tid) * 16);
+      const float4 c0 = row[0], c1 = row[1], c2 = row[2], c3 = row[3];
+      // position p holds feature dperm(p): features 16q + 0, 1, 2, ... sit at
+      // positions 0, 4, 8, 12, 1, 5, ...
+      const float fv[16] = {c0.x, c1.x, c2.x, c3.x, c0.y, c1.y, c2.y, c3.y,
+                            c0.z, c1.z, c2.z, c3.z, c0.w, c1.w, c2.w, c3.w};
+#pragma unroll
+      for (int j = 0; j < 16; ++j) { sum = sum + fv[j]; sq = sq + fv[j] * fv[j]; }
+    }
+    const float mean = sum / (float)d;
+    const float var = sq / (float)d - mean * mean;
+    stats[2 * tid] = mean;
+    stats[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+  }
+  __syncthreads();
+  {
+    const float mean = stats[2 * ml], rstd = stats[2 * ml + 1];
+#pragma unroll
+    for (int it = 0; it < SQ; ++it) {
+      const int q = 4 * it + (tid >> 8);
+      float4* p4 = reinterpret_cast<float4*>(xs + (q * 64 + ml) * 16) + a4;
+      const float4 v = *p4;
+      const float x[4] = {v.x, v.y, v.z, v.w};
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int f = 16 * q + dperm(4 * a4 + e);
+        o[e] = ((x[e] - mean) * rstd) * lwb[f] + lwb[d + f];
+      }
+      *p4 = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  __syncthreads();
+
+  // 3. MFMAs from LDS: wave w runs lanes 16 (w / 4) .. + 15 x features
+  // 16 (w % 4) .. + 15 of the tile
+  const int lane = tid & 63, wv = tid >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int lr = 16 * (wv >> 2) + i, fr = 16 * (wv & 3) + i;
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NB; ++q) {
+    const float4 bv = reinterpret_cast<const float4*>(xs + (q * 64 + lr) * 16)[g];
+    const float4 av = reinterpret_cast<const float4*>(ws + (q * 64 + fr) * 16)[g];
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.x, bv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.y, bv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.z, bv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
+  }
+  // 4. epilogue
+  dec_epilogue(a, acc, n0 + 16 * (wv & 3), m0 + lr, g);
+}
+
+bool dec_ln_gemm_fits(int d, int N) { return (d == 64 || d == 128 || d == 256) && N % 64 == 0; }
+
+hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, const uint8_t* tok,
+                              float* xt, const float* lw, const float* lb, int* t_counter,
+                              hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (!dec_ln_gemm_fits(a.K, a.N) || (mode != 1 && mode != 2) || (emb && mode != 1) ||
+      a.ldw < a.N || a.ldx < a.M || a.ldc < (a.row_major ? a.N : a.M) ||
+      (a.res && a.ldr < a.M) || (a.conv_di % 16))
+    return hipErrorInvalidValue;
+  const dim3 grid(((a.M + 63) / 64) * (a.N / 64)), block(1024);
+#define BOA_LNG(NBv)                                                                          \
+  if (emb)                                                                                    \
+    hipLaunchKernelGGL((dec_ln_gemm_kernel<1, NBv, true>), grid, block, 0, s, a, emb, tok, xt,  \
+                       lw, lb, t_counter);                                                    \
+  else if (mode == 1)                                                                         \
+    hipLaunchKernelGGL((dec_ln_gemm_kernel<1, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
+                       lw, lb, t_counter);                                                    \
+  else                                                                                        \
+    hipLaunchKernelGGL((dec_ln_gemm_kernel<2, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
+                       lw, lb, t_counter);
+  switch (a.K) {
+    case 64: BOA_LNG(4) break;
+    case 128: BOA_LNG(8) break;
+    case 256: BOA_LNG(16) break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BOA_LNG
+  return hipGetLastError();
+}
+
 // Weight relayout for decode: W [K][ldw_in] row-major (the compress layout)
 // -> k-blocked [K/16][ldn][16].  Logical output column j maps to source
 // column j (j < zs), to a zero column (zs <= j < ze) or to source column
