@@ -89,13 +89,15 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
   const float dt = softplus<M>(acc + sc.bdt);
   const float* Bv = bc;
   const float* Cv = bc + DS;
+  // h_n = fma(dA, h_n, B_n (dt u)) and y = fma(h_n, C_n, y): the update in
+  // fused form, dt u formed once
+  const float dtu = dt * u;
   float y = 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; ++n) {
-    float dA = scan_exp2_sel<M>(sc.na[n] * dt);
-    float dB = dt * Bv[n];
-    sc.h[n] = dA * sc.h[n] + dB * u;
-    y = y + sc.h[n] * Cv[n];
+    const float dA = scan_exp2_sel<M>(sc.na[n] * dt);
+    sc.h[n] = __builtin_fmaf(dA, sc.h[n], Bv[n] * dtu);
+    y = __builtin_fmaf(sc.h[n], Cv[n], y);
   }
   y = y + sc.dd * u;
   float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));

@@ -272,10 +272,11 @@ hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, 
 // Thread per (lane, channel); a block never straddles two lanes, so the
 // delta rows (dt_in | B | C of one token) are shared by the whole block: they
 // are staged in LDS SCAN_TB timesteps at a time and read as broadcasts.
-// d_state 16 with dt_rank <= 16 fits 80 VGPRs without spills, which lets
-// six waves share a SIMD instead of five.
+// d_state 16 with dt_rank <= 16: the fp32 kernel runs five waves per SIMD
+// (96 VGPRs); the bf16 kernel runs six (80 VGPRs with a few spilled, which
+// measured faster on MI355X than five without).
 template <int DS, int RB, typename TA>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DS == 16 && RB <= 16 ? 6 : 1, 8)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DS == 16 && RB <= 16 ? (sizeof(TA) == 2 ? 6 : 5) : 1, 8)))
 void scan_chunk_kernel(Dims D, LayerW Lw,
                                                          const TA* __restrict__ xz,
                                                          const TA* __restrict__ conv,

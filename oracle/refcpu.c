@@ -780,12 +780,15 @@ static inline float scan_row(const ref_layer* Ly, const ref_model* m, int dch, c
     const float* Bv = delta_row + r;
     const float* Cv = delta_row + r + ds;
     const float* na = Ly->na2 + (size_t)dch * ds;
+    /* h_n = dA h_n + (dt B_n) u as fmaf(dA, h_n, B_n (dt u)), y by fmaf:
+     * the contraction nvcc applies to the reference's expressions, with
+     * dt u formed once per element */
+    const float dtu = dt * u;
     float y = 0.0f;
     for (int n = 0; n < ds; ++n) {
         float dA = ref_scan_exp2(na[n] * dt);
-        float dB = dt * Bv[n];
-        h[n] = dA * h[n] + dB * u;
-        y = y + h[n] * Cv[n];
+        h[n] = fmaf(dA, h[n], Bv[n] * dtu);
+        y = fmaf(h[n], Cv[n], y);
     }
     y = y + Ly->dd[dch] * u;
     float sg = 1.0f / (1.0f + ref_expf(-z));
