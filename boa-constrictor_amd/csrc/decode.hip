@@ -26,6 +26,16 @@ namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// Streaming (nontemporal) access to the recurrent state, which every step
+// reads and rewrites once per layer.
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+  const floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st_stream(float4* p, float4 v) {
+  __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(p));
+}
+
 
 // ------------------------------------------------------------------- GEMM
 // A wave computes TN x TM MFMA tiles of 16 output features x 16 lanes.  Lane
@@ -70,10 +80,10 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
     for (int e = 0; e < 4; ++e) {
       const int n = nf[e];
       float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
-      const float4 s0 = *st;
+      const float4 s0 = ld_stream(st);
       const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
       cv[e] = conv_step_value<MATH_BR>(a.conv_b[n], s0, v[e], wv);
-      *st = make_float4(s0.y, s0.z, s0.w, v[e]);
+      st_stream(st, make_float4(s0.y, s0.z, s0.w, v[e]));
     }
     float* o = a.conv_out + ((size_t)(n0 >> 4) * a.ldc + m) * 16 + 4 * g;
     *reinterpret_cast<float4*>(o) = make_float4(cv[0], cv[1], cv[2], cv[3]);
@@ -371,8 +381,8 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
   }
   __syncthreads();
 
-  // 3. MFMAs from LDS: wave w runs lanes 16 (w / 4) .. + 15 x features
-  // 16 (w % 4) .. + 15 of the tile
+  // 3. MFMAs from LDS: wave w runs the 16 x 16 tile of lanes 16 (w / 4) + i,
+  // features 16 (w % 4) + i
   const int lane = tid & 63, wv = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
   const int lr = 16 * (wv >> 2) + i, fr = 16 * (wv & 3) + i;
@@ -674,7 +684,7 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
   const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 hv = h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl];
+    const float4 hv = ld_stream(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl);
     sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
     const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
     sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
@@ -700,8 +710,8 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
   yt[cm] = scan_token<DS, RB, MATH_BR>(sc, row, row + RB, r, u, z);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
-    h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl] =
-        make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]);
+    st_stream(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
+              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]));
 }
 
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
