@@ -645,15 +645,6 @@ hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const flo
 }
 
 // ------------------------------------------------------------------- scan
-__device__ __forceinline__ void dec_load16(const float* p, float* f) {
-  const float4* q = reinterpret_cast<const float4*>(p);
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const float4 t = q[a];
-    f[4 * a] = t.x; f[4 * a + 1] = t.y; f[4 * a + 2] = t.z; f[4 * a + 3] = t.w;
-  }
-}
-
 // Thread t of block (x, y): channel c = 16 y + t % 16, lane m = 16 x + t / 16.
 // The decode x_proj writes its row with dt_in at features [0, r), zeros up
 // to RB, B at [RB, RB + DS) and C at [RB + DS, RB + 2 DS), so the thread
@@ -673,11 +664,22 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
                                                        float* ssm, float* yt, int M, int ld,
                                                        int ld_state, int r) {
   constexpr int NB = (RB + 2 * DS + 15) / 16;
+  // the block's 16 lanes' x_proj rows (NB k-blocked 16-feature blocks each),
+  // loaded once and read by the 16 channel threads of each lane
+  __shared__ __align__(16) float4 srow[16 * NB * 4];
   const int cl = threadIdx.x & 15;
   const int cb = blockIdx.y;
   const int c = cb * 16 + cl;
-  const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (m >= M) return;
+  const int m0 = blockIdx.x * 16;
+  for (int q = threadIdx.x; q < 16 * NB * 4; q += 256) {
+    const int lm = q / (NB * 4), kb = (q / 4) % NB, c4 = q % 4;
+    const int mq = min(m0 + lm, M - 1);
+    srow[q] = reinterpret_cast<const float4*>(rows)[((size_t)kb * ld + mq) * 4 + c4];
+  }
+  __syncthreads();
+  const int lm = threadIdx.x >> 4;
+  const int m = m0 + lm;
+  if (m >= M) return;  // after the block's only barrier
   ScanCtx<DS, RB> sc;
   float4* h4 = reinterpret_cast<float4*>(ssm);
   const float4* na4 = reinterpret_cast<const float4*>(na_q);
@@ -700,7 +702,11 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
 #pragma unroll
   for (int kb = 0; kb < NB; ++kb) {
     float f[16];
-    dec_load16(rows + ((size_t)kb * ld + m) * 16, f);
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      const float4 t = srow[(lm * NB + kb) * 4 + a4];
+      f[4 * a4] = t.x; f[4 * a4 + 1] = t.y; f[4 * a4 + 2] = t.z; f[4 * a4 + 3] = t.w;
+    }
 #pragma unroll
     for (int j = 0; j < 16; ++j) row[16 * kb + j] = f[dperm(j)];
   }
