@@ -343,27 +343,34 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
       stats[2 * lj] = mean;
       stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
-  } else if (tid < 64) {
-    float sum = 0.0f, sq = 0.0f;
+  } else if (tid < 128) {  // LN2: lane tid % 64's sum (wave 0) and sum of squares (wave 1)
+    const int lj = tid & 63;
+    const bool squares = tid >= 64;
+    float acc = 0.0f;
 #pragma unroll 2
     for (int q = 0; q < NB; ++q) {
-      const float4* row = reinterpret_cast<const float4*>(xs + (q * 64 + tid) * 16);
+      const float4* row = reinterpret_cast<const float4*>(xs + (q * 64 + lj) * 16);
       const float4 c0 = row[0], c1 = row[1], c2 = row[2], c3 = row[3];
       // position p holds feature dperm(p): features 16q + 0, 1, 2, ... sit at
       // positions 0, 4, 8, 12, 1, 5, ...
       const float fv[16] = {c0.x, c1.x, c2.x, c3.x, c0.y, c1.y, c2.y, c3.y,
                             c0.z, c1.z, c2.z, c3.z, c0.w, c1.w, c2.w, c3.w};
 #pragma unroll
-      for (int j = 0; j < 16; ++j) { sum = sum + fv[j]; sq = sq + fv[j] * fv[j]; }
+      for (int j = 0; j < 16; ++j) acc = acc + (squares ? fv[j] * fv[j] : fv[j]);
     }
-    const float mean = sum / (float)d;
-    const float var = sq / (float)d - mean * mean;
-    stats[2 * tid] = mean;
-    stats[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    stats[2 * lj + (squares ? 1 : 0)] = acc;
   }
   __syncthreads();
   {
-    const float mean = stats[2 * ml], rstd = stats[2 * ml + 1];
+    float mean, rstd;
+    if (MODE == 1) {
+      mean = stats[2 * ml];
+      rstd = stats[2 * ml + 1];
+    } else {  // from the two sums, as dec_ln_kernel
+      mean = stats[2 * ml] / (float)d;
+      const float var = stats[2 * ml + 1] / (float)d - mean * mean;
+      rstd = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    }
 #pragma unroll
     for (int it = 0; it < SQ; ++it) {
       const int q = 4 * it + (tid >> 8);
