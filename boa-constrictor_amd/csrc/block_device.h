@@ -33,6 +33,18 @@ __device__ __forceinline__ float conv_step_value(float bias, float4 s, float x0,
 //   bf16 "32-blocked": feature k of lane m at ((k/32) ld + m) 32 + k%32, so
 //     that the 8 k of a 16x16x32 bf16 MFMA operand slot group are 16 bytes.
 __device__ __forceinline__ int dperm(int j) { return ((j & 3) << 2) | ((j >> 2) & 3); }
+
+// Streaming (nontemporal) access to the decode step's recurrent state, which
+// every step reads and rewrites once per layer (more than the last-level
+// cache holds), so that it does not evict the weights and activations.
+typedef float stream_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_stream(const float4* p) {
+  const stream_f4 v = __builtin_nontemporal_load(reinterpret_cast<const stream_f4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st_stream(float4* p, float4 v) {
+  __builtin_nontemporal_store(stream_f4{v.x, v.y, v.z, v.w}, reinterpret_cast<stream_f4*>(p));
+}
 __device__ __forceinline__ size_t dblk(int k, int m, int ld) {
   return ((size_t)(k >> 4) * ld + m) * 16 + dperm(k & 15);
 }

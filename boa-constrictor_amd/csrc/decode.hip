@@ -26,16 +26,6 @@ namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// Streaming (nontemporal) access to the recurrent state, which every step
-// reads and rewrites once per layer.
-__device__ __forceinline__ float4 ld_stream(const float4* p) {
-  const floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(p));
-  return make_float4(v[0], v[1], v[2], v[3]);
-}
-__device__ __forceinline__ void st_stream(float4* p, float4 v) {
-  __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, reinterpret_cast<floatx4*>(p));
-}
-
 
 // ------------------------------------------------------------------- GEMM
 // A wave computes TN x TM MFMA tiles of 16 output features x 16 lanes.  Lane

@@ -68,10 +68,10 @@ __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floa
       const int n = nb + e;
       const float x0 = bf16r(v[e]);  // the compress pass reads xz in bf16
       float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
-      const float4 s0 = *st;
+      const float4 s0 = ld_stream(st);
       const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
       o[e] = f32_to_bf16(conv_step_value<MATH_HW>(a.conv_b[n], s0, x0, wv));
-      *st = make_float4(s0.y, s0.z, s0.w, x0);
+      st_stream(st, make_float4(s0.y, s0.z, s0.w, x0));
     }
     *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) = make_ushort4(o[0], o[1], o[2], o[3]);
     return;
@@ -326,18 +326,29 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
                                                            float* ssm, uint16_t* yt, int M, int ld,
                                                            int ld_state, int r) {
   constexpr int NB = (RB + 2 * DS + 31) / 32;
+  // the block's 16 lanes' x_proj rows (NB 32-blocked 32-feature blocks
+  // each), loaded once and read by the 16 channel threads of each lane
+  __shared__ u32x4 srow[16 * NB * 4];
   const int cl = threadIdx.x & 15;
   const int cb = blockIdx.y;
   const int c = cb * 16 + cl;
-  const int m = blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (m >= M) return;
+  const int m0 = blockIdx.x * 16;
+  for (int qi = threadIdx.x; qi < 16 * NB * 4; qi += 256) {
+    const int lm = qi / (NB * 4), kb = (qi / 4) % NB, q4 = qi % 4;
+    const int mq = min(m0 + lm, M - 1);
+    srow[qi] = reinterpret_cast<const u32x4*>(rows)[((size_t)kb * ld + mq) * 4 + q4];
+  }
+  __syncthreads();
+  const int lm = threadIdx.x >> 4;
+  const int m = m0 + lm;
+  if (m >= M) return;  // after the block's only barrier
   ScanCtx<DS, RB> sc;
   float4* h4 = reinterpret_cast<float4*>(ssm);
   const float4* na4 = reinterpret_cast<const float4*>(na_q);
   const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 hv = h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl];
+    const float4 hv = ld_stream(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl);
     sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
     const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
     sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
@@ -354,7 +365,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(rows + dblk32(32 * kb + 8 * q, m, ld));
+      const u32x4 v = srow[(lm * NB + kb) * 4 + q];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         row[32 * kb + 8 * q + 2 * e] = u2f(v[e] << 16);
@@ -367,8 +378,8 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   yt[cm] = f32_to_bf16(scan_token<DS, RB, MATH_HW>(sc, row, row + RB, r, u, z));
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
-    h4[((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl] =
-        make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]);
+    st_stream(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
+              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]));
 }
 
 hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
