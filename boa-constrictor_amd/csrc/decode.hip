@@ -38,8 +38,27 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // its 16-row tile), so row 4g+v is feature 4v+g and lands at in-block
 // position 4g+v: each lane stores one float4.  Row-major outputs (the
 // logits) use unpermuted weights: row 4g+v is feature 4g+v.
+// Epilogue operands that do not depend on the GEMM (bias, residual), loaded
+// before the K loop so that their latency hides behind it.
+struct EpiPre {
+  float b[4];
+  float4 r;
+};
+
+__device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, int m, int g,
+                                                 EpiPre& p) {
+  if (m >= a.M || n0 >= a.N) return;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int nf = a.row_major ? n0 + 4 * g + e : n0 + 4 * e + g;
+    p.b[e] = a.bias ? a.bias[min(nf, a.N - 1)] : 0.0f;
+  }
+  if (a.res && !a.row_major && !(a.conv_di > 0))
+    p.r = *reinterpret_cast<const float4*>(a.res + ((size_t)(n0 >> 4) * a.ldr + m) * 16 + 4 * g);
+}
+
 __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4 acc, int n0, int m,
-                                             int g) {
+                                             int g, const EpiPre* pre = nullptr) {
   if (m >= a.M || n0 >= a.N) return;
   int nf[4];
 #pragma unroll
@@ -48,7 +67,7 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int n = min(nf[e], a.N - 1);
-    float r = acc[e] + (a.bias ? a.bias[n] : 0.0f);
+    float r = acc[e] + (pre ? pre->b[e] : (a.bias ? a.bias[n] : 0.0f));
     if (a.act == ACT_GELU) r = gelu<MATH_BR>(r);
     else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
     v[e] = r;
@@ -82,8 +101,8 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
   const int row0 = a.conv_di > 0 ? n0 - a.conv_di : n0;
   float* o = a.C + ((size_t)(row0 >> 4) * a.ldc + m) * 16 + 4 * g;
   if (a.res) {
-    const float4 rv =
-        *reinterpret_cast<const float4*>(a.res + ((size_t)(n0 >> 4) * a.ldr + m) * 16 + 4 * g);
+    const float4 rv = pre ? pre->r
+        : *reinterpret_cast<const float4*>(a.res + ((size_t)(n0 >> 4) * a.ldr + m) * 16 + 4 * g);
     v[0] = v[0] + rv.x; v[1] = v[1] + rv.y; v[2] = v[2] + rv.z; v[3] = v[3] + rv.w;
   }
   if (n0 + 16 <= a.N) {
@@ -158,6 +177,13 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
   const int n0 = (wid % n_tiles) * 16 * TN;
   const int m0 = (wid / n_tiles) * 16 * TM;
   floatx4 acc[TM][TN];
+  if (TM == 1 && TN == 1) {  // one tile: its bias and residual load ahead of the K loop
+    EpiPre pre;
+    dec_epi_prefetch(a, n0, m0 + i, g, pre);
+    dec_mainloop<KS, TM, TN, UQ, PD>(a, n0, m0, i, g, acc);
+    dec_epilogue(a, acc[0][0], n0, m0 + i, g, &pre);
+    return;
+  }
   dec_mainloop<KS, TM, TN, UQ, PD>(a, n0, m0, i, g, acc);
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
