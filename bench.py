@@ -94,6 +94,43 @@ def cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, sample_len, thre
                 blob=blob)
 
 
+def decode_step_profile(codec, lanes: int, ds: int, d: int, bf16: bool, steps: int = 32) -> dict:
+    """Per-class kernel times of `steps` decode steps over `lanes` lanes,
+    launched directly (not graph-replayed) with HIP events around every
+    kernel; the scan's algorithmic bytes give its HBM roofline."""
+    import torch
+    tok = torch.randint(0, 256, (lanes,), dtype=torch.uint8, device="cuda")
+    logits = torch.empty(lanes, 256, device="cuda")
+    codec.reset_state(lanes)
+    for _ in range(3):
+        codec.step_batch(tok.data_ptr(), lanes, logits.data_ptr())
+    torch.cuda.synchronize()
+    codec.profile(True)
+    codec.profile_reset()
+    for _ in range(steps):
+        codec.step_batch(tok.data_ptr(), lanes, logits.data_ptr())
+    torch.cuda.synchronize()
+    p = codec.profile_read()
+    codec.profile(False)
+    sc = p["scan"]
+    gbs = sc["work"] / (sc["ms"] * 1e-3) / 1e9 if sc["ms"] > 0 else 0.0
+    di = 2 * d
+    return {
+        "lanes": lanes, "steps": steps, "launch": "direct (HIP events per kernel)",
+        "kernel_us_per_step": {k: round(v["ms"] * 1e3 / steps, 2) for k, v in p.items() if v["ms"] > 0},
+        "roofline_scan": {
+            "bound": "hbm",
+            "kernel": f"boa::{'dec_b16_scan_kernel' if bf16 else 'dec_scan_kernel'}"
+                      f"<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>",
+            "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "avg_launch_us": round(sc["ms"] * 1e3 / max(sc["launches"], 1), 2),
+            "bytes_per_launch": round(sc["work"] / max(sc["launches"], 1)),
+            "bytes_per_lane_layer": f"8*di*ds + {2 if bf16 else 4}*(3*di + R), di = {di}, ds = {ds}",
+        },
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,6 +283,27 @@ def main() -> int:
         "bytes_per_launch": round(sc["work"] / max(sc["launches"], 1)),
     }
 
+    cd_ = prof["cdf"]
+    cdf_gbs = cd_["work"] / (cd_["ms"] * 1e-3) / 1e9 if cd_["ms"] > 0 else 0.0
+    roofline_coder = {
+        "bound": "hbm",
+        "kernel": "boa::cdf_targets_kernel",
+        "achieved": round(cdf_gbs, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(cdf_gbs / PEAK_HBM_GBS, 4),
+        "launches": cd_["launches"],
+        "avg_launch_ms": round(cd_["ms"] / max(cd_["launches"], 1), 4),
+        "bytes_per_launch": round(cd_["work"] / max(cd_["launches"], 1)),
+    }
+
+    # The decode step's kernels, timed with HIP events on a few directly
+    # launched steps (boa_step_batch) after the timed region; the decode
+    # scan is the step's HBM-bound kernel.
+    dec_step = None
+    if not args.no_decompress:
+        dec_step = decode_step_profile(codec, n_chunks, ds, d, prec == "bf16")
+
     host = None
     if args.host_path:
         torch.cuda.synchronize()
@@ -300,6 +358,8 @@ def main() -> int:
         "compress_kernel_ms": kernel_ms,
         "roofline": roofline,
         "roofline_scan": roofline_scan,
+        "roofline_coder": roofline_coder,
+        "decode_step": dec_step,
         "cpu_baseline": cpu,
     }
     if host:

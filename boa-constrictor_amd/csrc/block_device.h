@@ -107,7 +107,7 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
   float y = 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; ++n) {
-    const float dA = scan_exp2_sel<M>(sc.na[n] * dt);
+    const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
     sc.h[n] = __builtin_fmaf(dA, sc.h[n], Bv[n] * dtu);
     y = __builtin_fmaf(sc.h[n], Cv[n], y);
   }

@@ -1168,7 +1168,7 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
         const int Tt = (int)std::min<int64_t>(T, chunk - t0);
         e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
         if (!e)
-          e = timed(c, BOA_K_CDF, 1024.0 * lanes * Tt, [&] {
+          e = timed(c, BOA_K_CDF, 1032.0 * lanes * Tt, [&] {
             return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
                                              c->lowprob, s);
           });

@@ -73,15 +73,17 @@ BOA_DEV float expf_(float x) {
   return x != x ? x : res;
 }
 
-// The selective scan's decay exp(-exp(A_log) dt) in base 2: the weights
-// hold na2 = -exp(A_log) * log2(e) (two fp32 roundings, done once at load)
-// and the scan takes 2^t of t = na2 * dt <= 0.  t is clamped into
+// 2^t for t <= 0, the exponentials whose argument is never positive: the
+// selective scan's decay exp(-exp(A_log) dt), taken in base 2 (the weights
+// hold na2 = -exp(A_log) * log2(e), two fp32 roundings done once at load,
+// and the scan takes 2^t of t = na2 * dt), and the CDF's exp(l - max),
+// taken as 2^((l - max) log2(e)).  t is clamped into
 // [-126, 0] (fmaxf turns a NaN into -126), split as k + r with k = rint(t)
 // and r = t - k in [-1/2, 1/2] (exact); 2^r comes from a degree-6
 // polynomial with 2^0 = 1 exact, fitted to the relative error of 2^r on
 // [-1/2, 1/2] (under one ulp with fp32 fma evaluation), and 2^k is applied
 // with ldexp.  The least result is 2^-126: no subnormal is produced.
-BOA_DEV float scan_exp2(float t) {
+BOA_DEV float exp2_neg(float t) {
   const float s = __builtin_fminf(__builtin_fmaxf(t, -126.0f), 0.0f);
   const float k = __builtin_rintf(s);
   const float r = s - k;
@@ -216,13 +218,13 @@ BOA_DEV float silu(float x) {
 template <int M = MATH_BF>
 BOA_DEV float softplus(float x) { return log_sel<M>(1.0f + exp_sel<M>(x)); }
 
-// 2^t on the scan's domain (see scan_exp2) in the chosen form
+// 2^t for t <= 0 (see exp2_neg) in the chosen form
 template <int M>
-BOA_DEV float scan_exp2_sel(float t) {
-  return M == MATH_HW ? __builtin_amdgcn_exp2f(t) : scan_exp2(t);
+BOA_DEV float exp2_neg_sel(float t) {
+  return M == MATH_HW ? __builtin_amdgcn_exp2f(t) : exp2_neg(t);
 }
 
-// the scan's base-2 decay coefficient from A_log (see scan_exp2)
+// the scan's base-2 decay coefficient from A_log (see exp2_neg)
 BOA_DEV float scan_na2(float a_log) { return -expf_(a_log) * 1.44269504088896340736f; }
 
 }  // namespace boa

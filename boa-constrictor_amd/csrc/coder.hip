@@ -115,10 +115,10 @@ __device__ __forceinline__ void dec_advance(RcDec& st, uint32_t low, uint32_t hi
 }
 
 // ------------------------------------------------------------------- CDF
-// Every thread of the block must call this (it contains block barriers).
-// `s_cdf` is this half-wave's 257-entry LDS region; `lg` its logits row.
-__device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias, float inv_t,
-                                             double* s_cdf, int l) {
+// The cumulative probabilities of one logits row `lg` on a half-wave: lane
+// l ends with the exclusive running sums r[i] of symbols 8l + i.
+__device__ __forceinline__ void cdf_halfwave_regs(const float* lg, const float* bias, float inv_t,
+                                                  int l, double (&r)[8]) {
   float v[8];
   float mx = -1e30f;
 #pragma unroll
@@ -134,7 +134,7 @@ __device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias,
   double sd = 0.0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float e = expf_((v[i] - mx) * inv_t);
+    const float e = exp2_neg(((v[i] - mx) * inv_t) * 1.44269504088896340736f);
     v[i] = e;
     sd += (double)e;
   }
@@ -150,7 +150,6 @@ __device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias,
     const double tmp = __shfl_up(pre, off, 32);
     if (l >= off) pre = pre + tmp;
   }
-  double r[8];
   double run = pre - ts;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -177,10 +176,28 @@ __device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias,
       }
     }
   }
+}
+
+// The same into LDS.  Every thread of the block must call this (it contains
+// a block barrier).  `s_cdf` is this half-wave's 257-entry LDS region.
+__device__ __forceinline__ void cdf_halfwave(const float* lg, const float* bias, float inv_t,
+                                             double* s_cdf, int l) {
+  double r[8];
+  cdf_halfwave_regs(lg, bias, inv_t, l, r);
 #pragma unroll
   for (int i = 0; i < 8; ++i) s_cdf[8 * l + i] = r[i];
   if (l == 31) s_cdf[256] = 1.0;
   __syncthreads();
+}
+
+// Entry k of a half-wave's cumulative row held in registers (lane k / 8,
+// element k % 8), broadcast to every lane of the half-wave.
+__device__ __forceinline__ double cdf_entry(const double (&r)[8], int k) {
+  const int e = k & 7;
+  double mine = r[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) mine = e == i ? r[i] : mine;
+  return __shfl(mine, k >> 3, 32);
 }
 
 __device__ __forceinline__ uint32_t q_low(const double* s_cdf, int k) {
@@ -196,19 +213,23 @@ __device__ __forceinline__ uint32_t token_at(const TokenSrc& tok, int lane, int6
 }
 
 // (low, prob) of the next byte for every row (lane b, position t0+t) of a
-// tile.  8 rows per 256-thread block.
+// tile.  8 rows per 256-thread block; the two entries a row needs are
+// shuffled out of the registers that hold its cumulative sums.
 __global__ __launch_bounds__(256) void cdf_targets_kernel(const float* __restrict__ logits,
                                                           TokenSrc tok, int T, int t0, int rows,
                                                           float inv_t, uint2* lowprob) {
-  __shared__ double s_cdf[8][260];
   const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
   const int row = blockIdx.x * 8 + half;
   const int rr = row < rows ? row : rows - 1;
-  cdf_halfwave(logits + (size_t)rr * 256, nullptr, inv_t, s_cdf[half], l);
+  double r[8];
+  cdf_halfwave_regs(logits + (size_t)rr * 256, nullptr, inv_t, l, r);
+  const int b = rr / T, t = rr % T;
+  const int sym = (int)token_at(tok, b, (int64_t)t0 + t + 1);
+  const double c_lo = cdf_entry(r, sym);
+  const double c_hi = cdf_entry(r, sym + 1 > 255 ? 255 : sym + 1);
   if (row < rows && l == 0) {
-    const int b = row / T, t = row % T;
-    const int sym = (int)token_at(tok, b, (int64_t)t0 + t + 1);
-    const uint32_t lo = q_low(s_cdf[half], sym), hi = q_high(s_cdf[half], sym);
+    const uint32_t lo = (uint32_t)(c_lo * CDF_SCALE) + (uint32_t)sym;
+    const uint32_t hi = sym == 255 ? TOTAL : (uint32_t)(c_hi * CDF_SCALE) + (uint32_t)(sym + 1);
     lowprob[row] = make_uint2(lo, hi - lo);
   }
 }

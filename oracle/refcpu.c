@@ -73,15 +73,16 @@ float ref_expf(float x) {
     return exp_core(x);
 }
 
-/* The selective scan's decay exp(-exp(A_log) dt) in base 2: the layer
- * holds na2 = -exp(A_log) * log2(e) (ref_scan_na2) and the scan takes
- * 2^t of t = na2 * dt <= 0.  t is clamped into [-126, 0] (fmaxf turns a
+/* 2^t for t <= 0: the selective scan's decay exp(-exp(A_log) dt) in base
+ * 2 (the layer holds na2 = -exp(A_log) * log2(e), ref_scan_na2, and the
+ * scan takes 2^t of t = na2 * dt) and the CDF's exp(l - max) as
+ * 2^((l - max) log2(e)).  t is clamped into [-126, 0] (fmaxf turns a
  * NaN into -126) and split as k + r, k = rint(t), r = t - k in [-1/2, 1/2]
  * (exact); 2^r is a degree-6 polynomial with 2^0 = 1 exact (coefficients
  * fitted to the relative error of 2^r on [-1/2, 1/2]) and 2^k is applied
  * with ldexpf, exact here.  The least result is 2^-126.  This is the exp
- * of the HIP scan kernels, operation for operation. */
-float ref_scan_exp2(float t) {
+ * of the HIP scan and CDF kernels, operation for operation. */
+float ref_exp2_neg(float t) {
     float s = fminf(fmaxf(t, -126.0f), 0.0f);
     float k = rintf(s);
     float r = s - k;
@@ -329,6 +330,8 @@ void ref_rc_decode_cdf_stream(const uint32_t* cdf, int32_t n_sym, const uint32_t
  * sum; total by warpReduceSumDouble (shuffle-down 16,8,4,2,1, lane 0's
  * value is used); exclusive lane prefix by warpScanSumDouble (Hillis-
  * Steele, offsets 1..16); then the lane-boundary monotonicity fix-up.
+ * The exponentials e_j = exp((l_j - max) / T) (the reference's exp_fast)
+ * are this project's 2^((l_j - max) / T * log2(e)) (ref_exp2_neg).
  * ===================================================================== */
 static double tree_sum32(const double* v_in) {
     double v[32];
@@ -377,7 +380,7 @@ void ref_cdf_build_mode(const float* logits, const float* bias, float inv_temper
         double s = 0.0;
         for (int i = 0; i < 8; ++i) {
             int c = l * 8 + i;
-            float e = ref_expf((vals[c] - mx) * inv_temperature);
+            float e = ref_exp2_neg(((vals[c] - mx) * inv_temperature) * 1.44269504088896340736f);
             vals[c] = e;
             s += (double)e;
         }
@@ -786,7 +789,7 @@ static inline float scan_row(const ref_layer* Ly, const ref_model* m, int dch, c
     const float dtu = dt * u;
     float y = 0.0f;
     for (int n = 0; n < ds; ++n) {
-        float dA = ref_scan_exp2(na[n] * dt);
+        float dA = ref_exp2_neg(na[n] * dt);
         h[n] = fmaf(dA, h[n], Bv[n] * dtu);
         y = fmaf(h[n], Cv[n], y);
     }

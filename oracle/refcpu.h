@@ -47,7 +47,7 @@ extern "C" {
 
 /* ---------------------------------------------------------------- math */
 float ref_expf(float x);
-float ref_scan_exp2(float t);     /* 2^t on the scan's domain t <= 0 (clamped to [-126, 0], NaN -> -126) */
+float ref_exp2_neg(float t);      /* 2^t for t <= 0 (scan decay, CDF; clamped to [-126, 0], NaN -> -126) */
 float ref_scan_na2(float a_log);  /* -exp(A_log) * log2(e), the scan's base-2 decay coefficient */
 float ref_logf(float x);
 float ref_repro_exp(float x);     /* activations.hpp:33-84 (device branch) */

@@ -61,7 +61,7 @@ def lib():
         u8p = np.ctypeslib.ndpointer(np.uint8, flags="C")
         sig = {
             "ref_expf": (C.c_float, [C.c_float]),
-            "ref_scan_exp2": (C.c_float, [C.c_float]),
+            "ref_exp2_neg": (C.c_float, [C.c_float]),
             "ref_scan_na2": (C.c_float, [C.c_float]),
             "ref_logf": (C.c_float, [C.c_float]),
             "ref_repro_exp": (C.c_float, [C.c_float]),
