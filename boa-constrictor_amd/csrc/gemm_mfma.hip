@@ -24,10 +24,12 @@ namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
+// Eight waves per SIMD (64 VGPRs): two 16-wave blocks share a CU.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int ACT>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void gemm_f32_kernel(
     const float* __restrict__ X, int ldx, const float* __restrict__ W, int ldw, float* C, int ldc,
-    const float* __restrict__ bias, const float* res, int ldr, int M, int N, int K, int act,
+    const float* __restrict__ bias, const float* res, int ldr, int M, int N, int K,
     int vec_store, int swizzle) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -62,6 +64,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
   for (int a = 0; a < TM; ++a)
 #pragma unroll
     for (int b = 0; b < TN; ++b) acc[a][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // The block's bias values (clamped at N - 1) in LDS before the K loop, so
+  // that the epilogue does not wait on global loads.
+  __shared__ float sbias[BN];
+  for (int c = tid; c < BN; c += NT) sbias[c] = bias ? bias[min(n_blk + c, N - 1)] : 0.0f;
 
   float4 xr[XL], wr[WL];
   auto load_tile = [&](int k0) {
@@ -135,9 +142,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_f32_kernel(
       float v[4] = {acc[a][b][0], acc[a][b][1], acc[a][b][2], acc[a][b][3]};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float t = v[e] + (bias ? bias[n + e < N ? n + e : N - 1] : 0.0f);
-        if (act == ACT_GELU) t = gelu(t);
-        else if (act == ACT_RELU) t = fmaxf(0.0f, t);
+        float t = v[e] + sbias[wn0 + b * 16 + 4 * g + e];
+        if (ACT == ACT_GELU) t = gelu(t);
+        else if (ACT == ACT_RELU) t = fmaxf(0.0f, t);
         v[e] = t;
       }
       if (vec_store) {
@@ -165,9 +172,18 @@ static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s, int swizzle = 1) 
   const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
   int vec = (a.N % 4 == 0) && (a.ldc % 4 == 0) && (!a.res || a.ldr % 4 == 0);
-  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM_, WN_, BK>), dim3((unsigned)tiles),
-                     dim3(64 * WM_ * WN_), 0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias, a.res,
-                     a.ldr, a.M, a.N, a.K, a.act, vec, swizzle);
+  // the activation is a template argument: the epilogue has no branch on it
+#define BOA_GEMM_GO(ACTv)                                                                     \
+  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM_, WN_, BK, ACTv>), dim3((unsigned)tiles),     \
+                     dim3(64 * WM_ * WN_), 0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias,   \
+                     a.res, a.ldr, a.M, a.N, a.K, vec, swizzle)
+  switch (a.act) {
+    case ACT_NONE: BOA_GEMM_GO(ACT_NONE); break;
+    case ACT_GELU: BOA_GEMM_GO(ACT_GELU); break;
+    case ACT_RELU: BOA_GEMM_GO(ACT_RELU); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BOA_GEMM_GO
   return hipGetLastError();
 }
 
