@@ -25,10 +25,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // Epilogue of one tile: lane owns C[m][n .. n+3], m = m_blk + wm0 + 16p + j,
-// n = n_blk + wn0 + 16q + 4g.
-template <int TM, int TN>
+// n = n_blk + wn0 + 16q + 4g.  `sbias` holds the block's bias values
+// (column c of the block at c, clamped at N - 1); the activation is a
+// template argument, so the epilogue has no branch on it.
+template <int TM, int TN, int ACT>
 __device__ __forceinline__ void b16_epilogue(const GemmB16Args& a, const floatx4 (&acc)[TM][TN],
-                                             int m_blk, int n_blk, int wm0, int wn0, int j, int g) {
+                                             int m_blk, int n_blk, int wm0, int wn0, int j, int g,
+                                             const float* sbias) {
+  const bool res4 = a.res && (a.ldr & 3) == 0;
 #pragma unroll
   for (int p = 0; p < TM; ++p) {
     const int m = m_blk + wm0 + 16 * p + j;
@@ -37,13 +41,21 @@ __device__ __forceinline__ void b16_epilogue(const GemmB16Args& a, const floatx4
     for (int q = 0; q < TN; ++q) {
       const int n = n_blk + wn0 + 16 * q + 4 * g;
       if (n >= a.N) continue;
+      float rv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (res4 && n + 4 <= a.N) {
+        const float4 t = *reinterpret_cast<const float4*>(a.res + (size_t)m * a.ldr + n);
+        rv[0] = t.x; rv[1] = t.y; rv[2] = t.z; rv[3] = t.w;
+      } else if (a.res) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rv[e] = n + e < a.N ? a.res[(size_t)m * a.ldr + n + e] : 0.0f;
+      }
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float t = acc[p][q][e] + (a.bias ? a.bias[min(n + e, a.N - 1)] : 0.0f);
-        if (a.act == ACT_GELU) t = gelu<MATH_HW>(t);
-        else if (a.act == ACT_RELU) t = fmaxf(0.0f, t);
-        if (a.res) t = t + (n + e < a.N ? a.res[(size_t)m * a.ldr + n + e] : 0.0f);
+        float t = acc[p][q][e] + sbias[n - n_blk + e];
+        if (ACT == ACT_GELU) t = gelu<MATH_HW>(t);
+        else if (ACT == ACT_RELU) t = fmaxf(0.0f, t);
+        if (a.res) t = t + rv[e];
         v[e] = t;
       }
       const size_t o = (size_t)m * a.ldc + n;
@@ -70,7 +82,7 @@ __device__ __forceinline__ void b16_epilogue(const GemmB16Args& a, const floatx4
   }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int NBUF = 2>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int NBUF, int ACT>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB16Args a,
                                                                            int swizzle) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
@@ -85,6 +97,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
   // other's main loop.
   __shared__ __attribute__((aligned(16))) uint16_t xs[NBUF][BM * S];
   __shared__ __attribute__((aligned(16))) uint16_t ws[NBUF][BN * S];
+  __shared__ float sbias[BN];  // the block's bias values, for the epilogue
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -99,6 +112,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
     if (w < per * 8) w = (w % 8) * per + w / 8;
   }
   const int m_blk = (w / nb) * BM, n_blk = (w % nb) * BN;
+  for (int c = tid; c < BN; c += NT) sbias[c] = a.bias ? a.bias[min(n_blk + c, a.N - 1)] : 0.0f;
 
   floatx4 acc[TM][TN];
 #pragma unroll
@@ -166,7 +180,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
 #undef BOA_B16_LOAD
 #undef BOA_B16_STORE
 
-  b16_epilogue<TM, TN>(a, acc, m_blk, n_blk, wm0, wn0, j, g);
+  b16_epilogue<TM, TN, ACT>(a, acc, m_blk, n_blk, wm0, wn0, j, g, sbias);
 }
 
 template <int BM, int BN, int WM_, int WN_, int BK, int NBUF = 2>
@@ -174,8 +188,16 @@ static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 
   if (a.K % BK || a.ldx % 8 || a.ldw % 8 || a.ldw < a.K) return hipErrorInvalidValue;
   const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, BK, NBUF>), dim3((unsigned)tiles),
-                     dim3(64 * WM_ * WN_), 0, s, a, swizzle);
+#define BOA_B16_GO(ACTv)                                                                  \
+  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, BK, NBUF, ACTv>), dim3((unsigned)tiles), \
+                     dim3(64 * WM_ * WN_), 0, s, a, swizzle)
+  switch (a.act) {
+    case ACT_NONE: BOA_B16_GO(ACT_NONE); break;
+    case ACT_GELU: BOA_B16_GO(ACT_GELU); break;
+    case ACT_RELU: BOA_B16_GO(ACT_RELU); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BOA_B16_GO
   return hipGetLastError();
 }
 
