@@ -21,14 +21,32 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // Wave tile 16 features x 16 lanes; lane (i, g) loads, per k-step s of 32,
 // W[s][n0+i][8g..8g+7] and X[s][m0+i][8g..8g+7]; accumulator v holds feature
 // n0 + 4g + v of lane m0 + i.
+// The tile's bias values and fp32 residual, loaded before the K loop so
+// that their latency hides behind it.
+struct B16Pre {
+  float b[4], r[4];
+};
+
+__device__ __forceinline__ void dec_b16_prefetch(const DecB16Args& a, int n0, int m, int g,
+                                                 B16Pre& p) {
+  if (m >= a.M || n0 >= a.N) return;
+  const int nb = n0 + 4 * g;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    p.b[e] = a.bias ? a.bias[min(nb + e, a.N - 1)] : 0.0f;
+    p.r[e] = (a.out_mode == DEC_OUT_F32 && a.res && nb + e < a.N) ? a.res[dblk(nb + e, m, a.ldr)]
+                                                                  : 0.0f;
+  }
+}
+
 __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floatx4 acc, int n0,
-                                                 int m, int g) {
+                                                 int m, int g, const B16Pre& pre) {
   if (m >= a.M || n0 >= a.N) return;
   const int nb = n0 + 4 * g;
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    float r = acc[e] + (a.bias ? a.bias[min(nb + e, a.N - 1)] : 0.0f);
+    float r = acc[e] + pre.b[e];
     if (a.act == ACT_GELU) r = gelu<MATH_HW>(r);
     else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
     v[e] = r;
@@ -51,7 +69,7 @@ __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floa
       const int n = nb + e;
       if (n >= a.N) break;
       float r = v[e];
-      if (a.res) r = r + a.res[dblk(n, m, a.ldr)];
+      if (a.res) r = r + pre.r[e];
       v[e] = r;
       C[dblk(n, m, a.ldc)] = r;
     }
@@ -107,6 +125,8 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_kernel(DecB16Args a) {
   const u32x4* xp = reinterpret_cast<const u32x4*>(a.X) + (size_t)min(m0 + i, a.M - 1) * 4 + g;
   const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // 16-byte units per k-step
   floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+  B16Pre pre;
+  dec_b16_prefetch(a, n0, m0 + i, g, pre);
   u32x4 af[R][UQ], bf[R][UQ];
 #define BOA_B16_DLOAD(BUF, S0)                            \
   _Pragma("unroll") for (int q = 0; q < UQ; ++q) {        \
@@ -127,7 +147,7 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_kernel(DecB16Args a) {
     __builtin_amdgcn_sched_barrier(0);
   }
 #undef BOA_B16_DLOAD
-  dec_b16_epilogue(a, acc, n0, m0 + i, g);
+  dec_b16_epilogue(a, acc, n0, m0 + i, g, pre);
 }
 
 hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
