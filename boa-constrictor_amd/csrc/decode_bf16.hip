@@ -150,11 +150,92 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_kernel(DecB16Args a) {
   dec_b16_epilogue(a, acc, n0, m0 + i, g, pre);
 }
 
+// Register-blocked form for many lanes: a wave runs TM x TN tiles (16 TM
+// lanes x 16 TN features), so each operand fragment it loads feeds TN (or
+// TM) MFMAs; the k-steps of every tile run in the order of
+// dec_b16_gemm_kernel (the same bits).  Loads run two k-steps ahead.
+template <int KS, int TM, int TN>
+__global__ __launch_bounds__(256) void dec_b16_gemm_blk_kernel(DecB16Args a) {
+  constexpr int R = (2 < KS ? 2 : KS - 1) + 1;  // ring size
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15, g = lane >> 4;
+  const int n_tiles = (a.N + 16 * TN - 1) / (16 * TN);
+  const int m_tiles = (a.M + 16 * TM - 1) / (16 * TM);
+  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wid >= n_tiles * m_tiles) return;  // whole waves exit; no barriers below
+  const int n0 = (wid % n_tiles) * 16 * TN;
+  const int m0 = (wid / n_tiles) * 16 * TM;
+  const u32x4* wp[TN];
+  const u32x4* xp[TM];
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+    wp[t] = reinterpret_cast<const u32x4*>(a.W) + (size_t)min(n0 + 16 * t + i, a.ldw - 1) * 4 + g;
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+    xp[t] = reinterpret_cast<const u32x4*>(a.X) + (size_t)min(m0 + 16 * t + i, a.M - 1) * 4 + g;
+  const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // 16-byte units per k-step
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = floatx4{0.f, 0.f, 0.f, 0.f};
+  u32x4 af[R][TN], bf[R][TM];
+#define BOA_B16_BLOAD(BUF, S0)                                                      \
+  _Pragma("unroll") for (int t = 0; t < TN; ++t) af[BUF][t] = wp[t][(size_t)(S0) * wq]; \
+  _Pragma("unroll") for (int t = 0; t < TM; ++t) bf[BUF][t] = xp[t][(size_t)(S0) * xq]; \
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < R - 1; ++p) { BOA_B16_BLOAD(p, p) }
+#pragma unroll
+  for (int st = 0; st < KS; ++st) {
+    if (st + R - 1 < KS) { BOA_B16_BLOAD((st + R - 1) % R, st + R - 1) }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, af[st % R][tn]), __builtin_bit_cast(bf16x8, bf[st % R][tm]),
+            acc[tm][tn], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#undef BOA_B16_BLOAD
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      B16Pre pre;
+      dec_b16_prefetch(a, n0 + 16 * tn, m0 + 16 * tm + i, g, pre);
+      dec_b16_epilogue(a, acc[tm][tn], n0 + 16 * tn, m0 + 16 * tm + i, g, pre);
+    }
+}
+
+namespace {
+template <int TM, int TN>
+hipError_t dec_b16_blk_launch(const DecB16Args& a, hipStream_t s) {
+  const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
+  const dim3 grid((tiles + 3) / 4), block(256);
+  switch (a.K) {
+    case 64: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<2, TM, TN>), grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<4, TM, TN>), grid, block, 0, s, a); break;
+    case 256: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<8, TM, TN>), grid, block, 0, s, a); break;
+    case 512: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<16, TM, TN>), grid, block, 0, s, a); break;
+    case 1024: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<32, TM, TN>), grid, block, 0, s, a); break;
+    case 2048: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<64, TM, TN>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
 hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (a.ldw < (a.N + 15) / 16 * 16 || a.ldx < a.M || (a.conv_di % 16) ||
       (a.out_mode != DEC_OUT_ROWMAJOR && a.ldc < a.M) || (a.res && a.ldr < a.M))
     return hipErrorInvalidValue;
+  // from 2048 lanes on, 2 x 2 tiles per wave halve the operand loads per
+  // MFMA (C3 decode 3.76 -> 4.40 MB/s on MI355X; 4 x 4, 2 x 1 and 1 x 2 were
+  // slower)
+  if (a.M >= 2048) return dec_b16_blk_launch<2, 2>(a, s);
   const int tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16);
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {

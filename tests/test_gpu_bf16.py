@@ -75,3 +75,30 @@ def test_bf16_round_trip_and_ratio(torch_dev, oracle, make_weights, d, L, ds, ge
     assert c.decompress(blob) == data
     ref = oracle.Model(w, d, L, ds, bf16=True).compress(data, chunk_size=chunk)
     assert abs(len(blob) / len(ref) - 1.0) < 5e-3, f"{len(blob)} vs oracle {len(ref)} bytes"
+
+
+@pytest.mark.parametrize("d,L,ds", [(64, 2, 16), (256, 1, 16)])
+def test_bf16_many_lanes_step_equals_chunk_and_round_trip(torch_dev, make_weights, d, L, ds):
+    """From 2048 lanes on the bf16 decode GEMMs run 2 x 2 tiles per wave:
+    step logits stay bit-identical to chunk logits, and a container of 2101
+    chunks (one decode batch) round-trips byte for byte."""
+    torch = torch_dev
+    w = make_weights(d, L, ds)
+    lanes, T = 2100, 5
+    rng = np.random.default_rng(7 + d)
+    tok = rng.integers(0, 256, size=(lanes, T), dtype=np.uint8)
+    c = _codec(d, L, ds, lanes=2200, w=w)
+    c.reset_state(lanes)
+    d_log = torch.zeros(lanes * T * 256, dtype=torch.float32, device="cuda")
+    c.forward_chunk(torch.from_numpy(tok).cuda(), lanes, T, d_log)
+    torch.cuda.synchronize()
+    got = d_log.cpu().numpy().reshape(lanes, T, 256)
+    c.reset_state(lanes)
+    d_s = torch.zeros(lanes * 256, dtype=torch.float32, device="cuda")
+    for t in range(T):
+        c.step_batch(torch.from_numpy(np.ascontiguousarray(tok[:, t])).cuda(), lanes, d_s, True)
+        st = d_s.cpu().numpy().reshape(lanes, 256)
+        assert np.array_equal(st.view(np.uint32), got[:, t].view(np.uint32)), f"step {t}"
+    data = synth.gen_c3(21)[:2100 * 40 + 7]
+    blob = c.compress(data, chunk_size=40)
+    assert c.decompress(blob) == data
