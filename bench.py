@@ -31,8 +31,8 @@ METRIC = ("compress & decompress input MB/s at d256×8L, 1000 chunks; "
           "compression ratio")
 PEAK_TFLOPS = {"fp32": 157.3, "bf16": 2500.0}  # MI355X dense matrix peaks
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E peak
-GEMM_KERNEL = {"fp32": "boa::gemm_f32_kernel<128, 256, 4, 4, 16>",
-               "bf16": "boa::gemm_bf16_kernel<256, 256, 4, 4, 64, 1|2>"}
+GEMM_KERNEL = {"fp32": "boa::gemm_f32_kernel<128, 256, 4, 4, 16, 0|1|2>",
+               "bf16": "boa::gemm_bf16_kernel<256, 256, 4, 4, 64, 1|2, 0|1|2>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_c2_traffic.json")
 
 
