@@ -209,7 +209,98 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_blk_kernel(DecB16Args a) {
     }
 }
 
+// Workgroup-tiled form for many lanes: a block of four waves owns 64 lanes
+// x 64 features.  Per group of KG 32-k steps it copies the lanes' and the
+// weight rows' k-blocks (each one contiguous 4 KB span of the 32-blocked
+// layouts) into LDS, double-buffered, and wave w runs the 2 x 2 tiles of
+// lanes 32 (w / 2) .. + 31 and features 32 (w % 2) .. + 31 from there, the
+// k-steps of every tile in the order of dec_b16_gemm_kernel (the same
+// bits).  Each operand byte fetched from L2 feeds eight times the MFMAs of
+// the wave-per-tile form.
+template <int KS, int KG>
+__global__ __launch_bounds__(256) void dec_b16_gemm_lds_kernel(DecB16Args a) {
+  static_assert(KS % KG == 0, "k-steps must divide into groups");
+  constexpr int NG = KS / KG;
+  __shared__ __align__(16) u32x4 xs[2][KG][256];  // [buffer][k-step][row * 4 + quarter]
+  __shared__ __align__(16) u32x4 ws[2][KG][256];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int n_blocks = (a.N + 63) / 64;
+  const int m0 = (blockIdx.x / n_blocks) * 64, n0 = (blockIdx.x % n_blocks) * 64;
+  // staging: thread t copies quarter t % 4 of row t / 4 of each k-block
+  const int sr = tid >> 2, sq = tid & 3;
+  const int ms = min(m0 + sr, a.M - 1), ns = min(n0 + sr, a.ldw - 1);
+  const u32x4* X4 = reinterpret_cast<const u32x4*>(a.X);
+  const u32x4* W4 = reinterpret_cast<const u32x4*>(a.W);
+  u32x4 xr[KG], wr[KG];
+#define BOA_B16_GLOAD(S0)                                                         \
+  _Pragma("unroll") for (int kg = 0; kg < KG; ++kg) {                             \
+    xr[kg] = X4[((size_t)((S0) + kg) * a.ldx + ms) * 4 + sq];                     \
+    wr[kg] = W4[((size_t)((S0) + kg) * a.ldw + ns) * 4 + sq];                     \
+  }
+#define BOA_B16_GSTORE(BUF)                                                       \
+  _Pragma("unroll") for (int kg = 0; kg < KG; ++kg) {                             \
+    xs[BUF][kg][tid] = xr[kg];                                                    \
+    ws[BUF][kg][tid] = wr[kg];                                                    \
+  }
+  const int lr = 32 * (wv >> 1), fr = 32 * (wv & 1);
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) acc[tm][tn] = floatx4{0.f, 0.f, 0.f, 0.f};
+  BOA_B16_GLOAD(0)
+  BOA_B16_GSTORE(0)
+  __syncthreads();
+  for (int gi = 0; gi < NG; ++gi) {
+    const int cur = gi & 1;
+    if (gi + 1 < NG) { BOA_B16_GLOAD((gi + 1) * KG) }
+#pragma unroll
+    for (int kg = 0; kg < KG; ++kg) {
+      u32x4 bf[2], af[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        bf[t] = xs[cur][kg][(lr + 16 * t + i) * 4 + g];
+        af[t] = ws[cur][kg][(fr + 16 * t + i) * 4 + g];
+      }
+#pragma unroll
+      for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, af[tn]), __builtin_bit_cast(bf16x8, bf[tm]), acc[tm][tn],
+              0, 0, 0);
+    }
+    if (gi + 1 < NG) { BOA_B16_GSTORE(cur ^ 1) }
+    __syncthreads();
+  }
+#undef BOA_B16_GLOAD
+#undef BOA_B16_GSTORE
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn) {
+      B16Pre pre;
+      dec_b16_prefetch(a, n0 + fr + 16 * tn, m0 + lr + 16 * tm + i, g, pre);
+      dec_b16_epilogue(a, acc[tm][tn], n0 + fr + 16 * tn, m0 + lr + 16 * tm + i, g, pre);
+    }
+}
+
 namespace {
+hipError_t dec_b16_lds_launch(const DecB16Args& a, hipStream_t s) {
+  const dim3 grid(((a.M + 63) / 64) * ((a.N + 63) / 64)), block(256);
+  switch (a.K) {
+    case 64: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<2, 2>), grid, block, 0, s, a); break;
+    case 128: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<4, 4>), grid, block, 0, s, a); break;
+    case 256: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<8, 4>), grid, block, 0, s, a); break;
+    case 512: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<16, 4>), grid, block, 0, s, a); break;
+    case 1024: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<32, 4>), grid, block, 0, s, a); break;
+    case 2048: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<64, 4>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int TM, int TN>
 hipError_t dec_b16_blk_launch(const DecB16Args& a, hipStream_t s) {
   const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
@@ -232,10 +323,12 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   if (a.ldw < (a.N + 15) / 16 * 16 || a.ldx < a.M || (a.conv_di % 16) ||
       (a.out_mode != DEC_OUT_ROWMAJOR && a.ldc < a.M) || (a.res && a.ldr < a.M))
     return hipErrorInvalidValue;
-  // from 2048 lanes on, 2 x 2 tiles per wave halve the operand loads per
-  // MFMA (C3 decode 3.76 -> 4.40 MB/s on MI355X; 4 x 4, 2 x 1 and 1 x 2 were
-  // slower)
-  if (a.M >= 2048) return dec_b16_blk_launch<2, 2>(a, s);
+  // From 2048 lanes on: 2 x 2 tiles per wave for K <= 256 (C3 decode 3.76 ->
+  // 4.40 MB/s on MI355X; 4 x 4, 2 x 1 and 1 x 2 were slower) and the
+  // LDS-tiled blocks for K >= 512 (4.40 -> 4.54 MB/s at C3, 0.95 -> 0.98 at
+  // C5; LDS tiles for in_proj and FF1 too were slower, the block's two
+  // waves per SIMD exposing their conv and epilogue latency)
+  if (a.M >= 2048) return a.K >= 512 ? dec_b16_lds_launch(a, s) : dec_b16_blk_launch<2, 2>(a, s);
   const int tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16);
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {
