@@ -45,6 +45,15 @@ __device__ __forceinline__ float4 ld_stream(const float4* p) {
 __device__ __forceinline__ void st_stream(float4* p, float4 v) {
   __builtin_nontemporal_store(stream_f4{v.x, v.y, v.z, v.w}, reinterpret_cast<stream_f4*>(p));
 }
+// State of the layers that fit in the last-level cache next to the weights
+// uses ordinary (cached) accesses; the rest is streamed.
+__device__ __forceinline__ float4 state_ld4(const float4* p, bool cached) {
+  return cached ? *p : ld_stream(p);
+}
+__device__ __forceinline__ void state_st4(float4* p, float4 v, bool cached) {
+  if (cached) *p = v;
+  else st_stream(p, v);
+}
 __device__ __forceinline__ size_t dblk(int k, int m, int ld) {
   return ((size_t)(k >> 4) * ld + m) * 16 + dperm(k & 15);
 }

@@ -109,6 +109,7 @@ struct DecGemmArgs {
   int conv_di;
   float* conv_state; int ld_state;
   const float* conv_w; const float* conv_b; float* conv_out;
+  int state_cached;  // conv state through the caches (1) or streamed (0)
 };
 hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s);
 // LayerNorm (mode 1: LN1, mode 2: LN2; weights lw, lb) of the K = d features
@@ -134,7 +135,7 @@ hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const flo
                           int ld, hipStream_t s);
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
                            const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
-                           int M, int ld, int ld_state, hipStream_t s);
+                           int M, int ld, int ld_state, bool state_cached, hipStream_t s);
 // ---- decode step, bf16 precision (decode_bf16.hip) ----------------------
 // Activations bf16 in the 32-blocked layout (feature k of lane m at
 // ((k/32) ld + m) 32 + k%32), the residual stream fp32 k-blocked.
@@ -150,6 +151,7 @@ struct DecB16Args {
   int conv_di;                  // DEC_OUT_B16 in_proj: the conv step on features < conv_di
   float* conv_state; int ld_state;
   const float* conv_w; const float* conv_b; uint16_t* conv_out;
+  int state_cached;             // conv state through the caches (1) or streamed (0)
 };
 hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s);
 hipError_t launch_dec_b16_weight(const float* w, int ldw_in, int n_src, uint16_t* out, int K,
@@ -162,7 +164,7 @@ hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w
 hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
                                const float* wdt_q, const uint16_t* zt, const uint16_t* cvt,
                                const uint16_t* rows, float* ssm, uint16_t* yt, int M, int ld,
-                               int ld_state, hipStream_t s);
+                               int ld_state, bool state_cached, hipStream_t s);
 
 // chunk layout: conv [lane][c][4], ssm [lane][c][n]; step layout: conv
 // [c][lane][4], ssm [c/16][n/4][lane][c%16][n%4] with lane stride ld_state.

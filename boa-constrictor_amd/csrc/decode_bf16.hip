@@ -86,10 +86,10 @@ __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floa
       const int n = nb + e;
       const float x0 = bf16r(v[e]);  // the compress pass reads xz in bf16
       float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
-      const float4 s0 = ld_stream(st);
+      const float4 s0 = state_ld4(st, a.state_cached);
       const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
       o[e] = f32_to_bf16(conv_step_value<MATH_HW>(a.conv_b[n], s0, x0, wv));
-      st_stream(st, make_float4(s0.y, s0.z, s0.w, x0));
+      state_st4(st, make_float4(s0.y, s0.z, s0.w, x0), a.state_cached);
     }
     *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) = make_ushort4(o[0], o[1], o[2], o[3]);
     return;
@@ -518,7 +518,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
                                                            const uint16_t* __restrict__ cvt,
                                                            const uint16_t* __restrict__ rows,
                                                            float* ssm, uint16_t* yt, int M, int ld,
-                                                           int ld_state, int r) {
+                                                           int ld_state, int r, int cached) {
   constexpr int NB = (RB + 2 * DS + 31) / 32;
   // the block's 16 lanes' x_proj rows (NB 32-blocked 32-feature blocks
   // each), loaded once and read by the 16 channel threads of each lane
@@ -542,7 +542,8 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 hv = ld_stream(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl);
+    const float4 hv =
+        state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl, cached);
     sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
     const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
     sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
@@ -572,19 +573,19 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   yt[cm] = f32_to_bf16(scan_token<DS, RB, MATH_HW>(sc, row, row + RB, r, u, z));
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
-    st_stream(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
-              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]));
+    state_st4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
+              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), cached);
 }
 
 hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
                                const float* wdt_q, const uint16_t* zt, const uint16_t* cvt,
                                const uint16_t* rows, float* ssm, uint16_t* yt, int M, int ld,
-                               int ld_state, hipStream_t s) {
+                               int ld_state, bool state_cached, hipStream_t s) {
   if (D.di % 16 || dec_rb(D.r) < D.r) return hipErrorInvalidValue;
   dim3 grid((M + 15) / 16, D.di / 16);
 #define BOA_B16_SCAN(DSv, RBv)                                                                  \
   hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, zt, \
-                     cvt, rows, ssm, yt, M, ld, ld_state, D.r)
+                     cvt, rows, ssm, yt, M, ld, ld_state, D.r, state_cached ? 1 : 0)
   const int rb = dec_rb(D.r);
   if (D.ds == 16) {
     if (rb == 8) BOA_B16_SCAN(16, 8);
