@@ -7,6 +7,24 @@
 
 namespace boa {
 
+// Workgroups are dispatched to the 8 XCDs, each with its own L2, round-robin
+// by block index.  The decode step's kernels keep every 64-lane group on one
+// XCD, so that one kernel's outputs for those lanes are read by the next
+// kernel from the same L2: block b, of per_group blocks per group, gets group
+// b % 8 + 8 ((b / 8) / per_group) and index (b / 8) % per_group in it.
+struct XcdSlot {
+  int grp, j;
+};
+__device__ __forceinline__ XcdSlot xcd_slot(int b, int per_group) {
+  const int s = b >> 3;
+  return XcdSlot{(b & 7) + 8 * (s / per_group), s % per_group};
+}
+// blocks covering `lanes` lanes in 64-lane groups of per_group blocks
+inline unsigned xcd_grid(int lanes, int per_group) {
+  return (unsigned)(((lanes + 511) / 512) * 8 * per_group);
+}
+
+
 enum { ACT_NONE = 0, ACT_GELU = 1, ACT_RELU = 2 };
 
 struct GemmArgs {

@@ -481,7 +481,9 @@ __global__ __launch_bounds__(256) void decode_step_kernel(
   __shared__ double s_cdf[8][260];
   __shared__ uint32_t s_target[8];
   const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
-  const int b = blockIdx.x * 8 + half;
+  const XcdSlot blk = xcd_slot(blockIdx.x, 8);  // 8 blocks of 8 lanes per 64-lane group
+  if (blk.grp * 64 >= lanes) return;           // the whole block, before the barrier
+  const int b = blk.grp * 64 + blk.j * 8 + half;
   const int bb = b < lanes ? b : lanes - 1;
   const int t = *t_counter;
   const bool active = b < lanes && t < lens[bb];
@@ -525,7 +527,7 @@ hipError_t launch_decode_step(const float* logits, const float* head_b2, float i
                               uint8_t* out, int64_t out_stride, RcDec* st, const uint32_t* payload,
                               const uint64_t* offsets_words, const int32_t* sizes_words, int lanes,
                               hipStream_t s) {
-  hipLaunchKernelGGL(decode_step_kernel, dim3((lanes + 7) / 8), dim3(256), 0, s, logits, head_b2,
+  hipLaunchKernelGGL(decode_step_kernel, dim3(xcd_grid(lanes, 8)), dim3(256), 0, s, logits, head_b2,
                      inv_temp, tok, lens, t_counter, out, out_stride, st, payload, offsets_words,
                      sizes_words, lanes);
   return hipGetLastError();

@@ -171,19 +171,25 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int i = lane & 15, g = lane >> 4;
   const int n_tiles = (a.N + 16 * TN - 1) / (16 * TN);
-  const int m_tiles = (a.M + 16 * TM - 1) / (16 * TM);
-  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (wid >= n_tiles * m_tiles) return;  // whole waves exit; no barriers below
-  const int n0 = (wid % n_tiles) * 16 * TN;
-  const int m0 = (wid / n_tiles) * 16 * TM;
   floatx4 acc[TM][TN];
-  if (TM == 1 && TN == 1) {  // one tile: its bias and residual load ahead of the K loop
+  if (TM == 1 && TN == 1) {
+    // one tile per wave; a block's 4 waves take the 4 16-lane tiles of one
+    // 64-lane group (xcd_slot) and one n tile.  Its bias and residual load
+    // ahead of the K loop.
+    const XcdSlot q = xcd_slot(blockIdx.x, n_tiles);
+    const int m0 = q.grp * 64 + 16 * (threadIdx.x >> 6), n0 = q.j * 16;
+    if (m0 >= a.M) return;  // whole waves exit; no barriers below
     EpiPre pre;
     dec_epi_prefetch(a, n0, m0 + i, g, pre);
     dec_mainloop<KS, TM, TN, UQ, PD>(a, n0, m0, i, g, acc);
     dec_epilogue(a, acc[0][0], n0, m0 + i, g, &pre);
     return;
   }
+  const int m_tiles = (a.M + 16 * TM - 1) / (16 * TM);
+  const int wid = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (wid >= n_tiles * m_tiles) return;  // whole waves exit; no barriers below
+  const int n0 = (wid % n_tiles) * 16 * TN;
+  const int m0 = (wid / n_tiles) * 16 * TM;
   dec_mainloop<KS, TM, TN, UQ, PD>(a, n0, m0, i, g, acc);
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
@@ -195,7 +201,7 @@ namespace {
 template <int TM, int TN, int UQ, int PD>
 hipError_t dec_launch(const DecGemmArgs& a, hipStream_t s) {
   const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
-  const dim3 grid((tiles + 3) / 4), block(256);
+  const dim3 grid(TM == 1 && TN == 1 ? xcd_grid(a.M, (a.N + 15) / 16) : (tiles + 3) / 4), block(256);
   switch (a.K) {
     case 64: hipLaunchKernelGGL((dec_gemm_kernel<16, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     case 128: hipLaunchKernelGGL((dec_gemm_kernel<32, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
@@ -285,8 +291,9 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
   __shared__ float stats[2 * 64];
   if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
   const int tid = threadIdx.x;
-  const int n_blocks = a.N / 64;
-  const int m0 = (blockIdx.x / n_blocks) * 64, n0 = (blockIdx.x % n_blocks) * 64;
+  const XcdSlot blk = xcd_slot(blockIdx.x, a.N / 64);
+  const int m0 = blk.grp * 64, n0 = blk.j * 64;
+  if (m0 >= a.M) return;  // the whole block, before any barrier
 
   // 1. stage weights, LayerNorm parameters and rows: float4 r = tid % 256 of
   // 16-k block q = 4 it + tid / 256 (row r / 4, quarter r % 4)
@@ -433,7 +440,7 @@ hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, 
       a.ldw < a.N || a.ldx < a.M || a.ldc < (a.row_major ? a.N : a.M) ||
       (a.res && a.ldr < a.M) || (a.conv_di % 16))
     return hipErrorInvalidValue;
-  const dim3 grid(((a.M + 63) / 64) * (a.N / 64)), block(1024);
+  const dim3 grid(xcd_grid(a.M, a.N / 64)), block(1024);
 #define BOA_LNG(NBv)                                                                          \
   if (emb)                                                                                    \
     hipLaunchKernelGGL((dec_ln_gemm_kernel<1, NBv, true>), grid, block, 0, s, a, emb, tok, xt,  \
@@ -685,15 +692,17 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
                                                        const float* __restrict__ cvt,
                                                        const float* __restrict__ rows,
                                                        float* ssm, float* yt, int M, int ld,
-                                                       int ld_state, int r, int cached) {
+                                                       int ld_state, int r, int cached, int cbn) {
   constexpr int NB = (RB + 2 * DS + 15) / 16;
   // the block's 16 lanes' x_proj rows (NB k-blocked 16-feature blocks each),
   // loaded once and read by the 16 channel threads of each lane
   __shared__ __align__(16) float4 srow[16 * NB * 4];
   const int cl = threadIdx.x & 15;
-  const int cb = blockIdx.y;
+  const XcdSlot blk = xcd_slot(blockIdx.x, 4 * cbn);  // cbn channel blocks x 4 16-lane blocks
+  const int cb = blk.j % cbn;
   const int c = cb * 16 + cl;
-  const int m0 = blockIdx.x * 16;
+  const int m0 = blk.grp * 64 + (blk.j / cbn) * 16;
+  if (m0 >= M) return;  // the whole block, before the barrier
   for (int q = threadIdx.x; q < 16 * NB * 4; q += 256) {
     const int lm = q / (NB * 4), kb = (q / 4) % NB, c4 = q % 4;
     const int mq = min(m0 + lm, M - 1);
@@ -748,10 +757,10 @@ hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, c
                            const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
                            int M, int ld, int ld_state, bool state_cached, hipStream_t s) {
   if (D.di % 16 || dec_rb(D.r) < D.r) return hipErrorInvalidValue;
-  dim3 grid((M + 15) / 16, D.di / 16);
+  const dim3 grid(xcd_grid(M, 4 * (D.di / 16)));
 #define BOA_DEC_SCAN(DSv, RBv)                                                                   \
   hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, zt, cvt, \
-                     rows, ssm, yt, M, ld, ld_state, D.r, state_cached ? 1 : 0)
+                     rows, ssm, yt, M, ld, ld_state, D.r, state_cached ? 1 : 0, D.di / 16)
   const int rb = dec_rb(D.r);
   if (D.ds == 16) {
     if (rb == 8) BOA_DEC_SCAN(16, 8);
