@@ -659,6 +659,26 @@ namespace {
 hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t chunk,
                         const uint32_t* d_payload) {
   hipStream_t s = c->stream;
+  const Dims& D = c->D;
+  if (!c->bf16 && dec_persist_fits(D.d, D.ds, D.r, D.L)) {
+    // small model: every step in one persistent kernel (decode_persist.hip)
+    PersistArgs p{};
+    for (int l = 0; l < D.L; ++l) {
+      const LayerW& W = c->layers[l];
+      const boa_ctx::DecW& DW = c->dlayers[l];
+      p.layer[l] = PersistLayer{W.ln1_w, W.ln1_b, DW.w_in, W.b_in, W.conv_w, W.conv_b, DW.w_x,
+                                DW.na, DW.w_dt, W.b_dt, W.dd, DW.w_out, W.b_out, W.ln2_w,
+                                W.ln2_b, DW.w1, W.b1, DW.w2, W.b2, dec_conv_of(c, l),
+                                dec_ssm_of(c, l)};
+    }
+    p.L = D.L; p.r = D.r; p.lanes = lanes; p.maxlen = maxlen; p.ld_state = c->ld_dec;
+    p.emb = c->emb; p.hw1 = c->dhw1; p.hb1 = c->hb1; p.hw2 = c->dhw2; p.hb2 = c->hb2;
+    p.inv_t = c->inv_temp; p.tok = c->tok; p.lens = c->lens; p.t_counter = c->t_counter;
+    p.out = out; p.out_stride = chunk; p.states = c->dec; p.payload = d_payload;
+    p.offsets = c->offsets; p.sizes = c->sizes;
+    return timed(c, BOA_K_DECODE, 1024.0 * lanes * (maxlen - 1),
+                 [&] { return launch_dec_persist(p, D.d, D.ds, s); });
+  }
   auto one_step = [&](hipStream_t gs) -> hipError_t {
     hipError_t e = step_range(c, 0, lanes, gs, c->t_counter, c->tok, false, c->dlogits);
     if (e) return e;

@@ -154,6 +154,35 @@ hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const flo
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
                            const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
                            int M, int ld, int ld_state, bool state_cached, hipStream_t s);
+// ---- persistent decode for small models (decode_persist.hip) -----------
+// One block of 1024 threads per 16 lanes runs steps 1 .. maxlen-1 of a batch
+// (model, CDF, search, coder) with the step kernels' operations and state
+// layouts.  d_model 64, d_state 16, at most PERSIST_MAX_LAYERS layers (their
+// per-channel parameters are staged in LDS).
+constexpr int PERSIST_MAX_LAYERS = 2;
+struct PersistLayer {
+  const float *ln1_w, *ln1_b, *w_in, *b_in, *conv_w, *conv_b, *w_x, *na_q, *wdt_q, *b_dt, *dd,
+      *w_out, *b_out, *ln2_w, *ln2_b, *w1, *b1, *w2, *b2;  // decode (k-blocked) weights
+  float *conv, *ssm;                                         // step-layout state
+};
+struct PersistArgs {
+  PersistLayer layer[PERSIST_MAX_LAYERS];
+  int L, r, lanes, maxlen, ld_state;
+  const float *emb, *hw1, *hb1, *hw2, *hb2;
+  float inv_t;
+  uint8_t* tok;
+  const int32_t* lens;
+  int* t_counter;
+  uint8_t* out;
+  int64_t out_stride;
+  RcDec* states;
+  const uint32_t* payload;
+  const uint64_t* offsets;
+  const int32_t* sizes;
+};
+bool dec_persist_fits(int d, int ds, int r, int L);
+hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, hipStream_t s);
+
 // ---- decode step, bf16 precision (decode_bf16.hip) ----------------------
 // Activations bf16 in the 32-blocked layout (feature k of lane m at
 // ((k/32) ld + m) 32 + k%32), the residual stream fp32 k-blocked.
