@@ -685,14 +685,14 @@ hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const flo
 //   h[c][n] of lane m at ((((c/16) DS/4 + n/4) ld_state + m) 16 + c%16) 4 + n%4
 //   na[c][n]          at (((c/16) DS/4 + n/4) 16 + c%16) 4 + n%4
 //   wdt[c][j]         at (((c/16) RB/4 + j/4) 16 + c%16) 4 + j%4
-template <int DS, int RB>
+template <int DS, int RB, bool CACHED>
 __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* __restrict__ na_q,
                                                        const float* __restrict__ wdt_q,
                                                        const float* __restrict__ zt,
                                                        const float* __restrict__ cvt,
                                                        const float* __restrict__ rows,
                                                        float* ssm, float* yt, int M, int ld,
-                                                       int ld_state, int r, int cached, int cbn) {
+                                                       int ld_state, int r, int cbn) {
   constexpr int NB = (RB + 2 * DS + 15) / 16;
   // the block's 16 lanes' x_proj rows (NB k-blocked 16-feature blocks each),
   // loaded once and read by the 16 channel threads of each lane
@@ -719,7 +719,7 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4) {
     const float4 hv =
-        state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl, cached);
+        state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl, CACHED);
     sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
     const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
     sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
@@ -750,7 +750,7 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
     state_st4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
-              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), cached);
+              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), CACHED);
 }
 
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
@@ -758,9 +758,13 @@ hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, c
                            int M, int ld, int ld_state, bool state_cached, hipStream_t s) {
   if (D.di % 16 || dec_rb(D.r) < D.r) return hipErrorInvalidValue;
   const dim3 grid(xcd_grid(M, 4 * (D.di / 16)));
-#define BOA_DEC_SCAN(DSv, RBv)                                                                   \
-  hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, zt, cvt, \
-                     rows, ssm, yt, M, ld, ld_state, D.r, state_cached ? 1 : 0, D.di / 16)
+#define BOA_DEC_SCAN(DSv, RBv)                                                                  \
+  if (state_cached)                                                                             \
+    hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv, true>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, \
+                       zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r, D.di / 16);                 \
+  else                                                                                          \
+    hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv, false>), grid, dim3(256), 0, s, Lw, na_q, wdt_q,\
+                       zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r, D.di / 16)
   const int rb = dec_rb(D.r);
   if (D.ds == 16) {
     if (rb == 8) BOA_DEC_SCAN(16, 8);

@@ -511,14 +511,14 @@ hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w
 // ------------------------------------------------------------------- scan
 // As the fp32 step scan (16 channels x 16 lanes per block, quad-layout state
 // and parameters), with bf16 32-blocked u, z, rows and y.
-template <int DS, int RB>
+template <int DS, int RB, bool CACHED>
 __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const float* __restrict__ na_q,
                                                            const float* __restrict__ wdt_q,
                                                            const uint16_t* __restrict__ zt,
                                                            const uint16_t* __restrict__ cvt,
                                                            const uint16_t* __restrict__ rows,
                                                            float* ssm, uint16_t* yt, int M, int ld,
-                                                           int ld_state, int r, int cached) {
+                                                           int ld_state, int r) {
   constexpr int NB = (RB + 2 * DS + 31) / 32;
   // the block's 16 lanes' x_proj rows (NB 32-blocked 32-feature blocks
   // each), loaded once and read by the 16 channel threads of each lane
@@ -543,7 +543,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4) {
     const float4 hv =
-        state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl, cached);
+        state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl, CACHED);
     sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
     const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
     sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
     state_st4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
-              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), cached);
+              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), CACHED);
 }
 
 hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
@@ -584,8 +584,12 @@ hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_
   if (D.di % 16 || dec_rb(D.r) < D.r) return hipErrorInvalidValue;
   dim3 grid((M + 15) / 16, D.di / 16);
 #define BOA_B16_SCAN(DSv, RBv)                                                                  \
-  hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, zt, \
-                     cvt, rows, ssm, yt, M, ld, ld_state, D.r, state_cached ? 1 : 0)
+  if (state_cached)                                                                             \
+    hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv, true>), grid, dim3(256), 0, s, Lw, na_q,    \
+                       wdt_q, zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r);                     \
+  else                                                                                          \
+    hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv, false>), grid, dim3(256), 0, s, Lw, na_q,   \
+                       wdt_q, zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r)
   const int rb = dec_rb(D.r);
   if (D.ds == 16) {
     if (rb == 8) BOA_B16_SCAN(16, 8);
