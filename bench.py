@@ -121,7 +121,8 @@ def decode_step_profile(codec, lanes: int, ds: int, d: int, bf16: bool, steps: i
         "roofline_scan": {
             "bound": "hbm",
             "kernel": f"boa::{'dec_b16_scan_kernel' if bf16 else 'dec_scan_kernel'}"
-                      f"<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>",
+                      f"<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}, true|false>"
+                      " (state cached | streamed, by layer)",
             "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
             "frac": round(gbs / PEAK_HBM_GBS, 4),
             "avg_launch_us": round(sc["ms"] * 1e3 / max(sc["launches"], 1), 2),
