@@ -106,6 +106,8 @@ def test_container_temperature(torch_dev, oracle, w_c1):
     (513, 512, 4, 0),        # last chunk of one byte
     (7 * 300, 300, 3, 0),    # three batches of lanes
     (10 * 256, 256, 4, 4),   # --max-chunks truncation
+    (37 * 333 - 100, 333, 37, 0),  # three 16-lane decode blocks, the last one partial
+    (45 * 200 + 5, 200, 20, 0),    # batches of 20 lanes, a last batch of 6, a 5-byte chunk
 ])
 def test_container_edges(torch_dev, oracle, w_c1, n, chunk, lanes, max_chunks):
     data = synth.gen_c1()[:n]
