@@ -6,6 +6,13 @@
 // (6 L + 3 kernels per step, each a few microseconds of launch and drain at
 // this size) by block barriers.
 //
+// It covers, for one batch, what the reference's decompress loop runs per
+// step as a graph replay (portability_solved_cpp/boa.cpp:672-774):
+// BoaPredictorGPU::step_batch (boa_gpu.hpp:1034-1053; blocks :835-843,
+// Mamba step :227-247, feed-forward :739-764, head :1049-1052) and the fused
+// decode step of range_coder_kernels.cu:491-629 (CDF, symbol search, coder
+// advance).
+//
 // Every operation is the one of the step kernels (decode.hip, coder.hip),
 // with the same operand arrangement and k order in every MFMA chain, the
 // same LayerNorm reduction orders and the same epilogue order (bias,
