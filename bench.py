@@ -12,7 +12,14 @@ HBM, then decompress that payload back into HBM and check the round trip.
 throughput, the compression ratio, the roofline of the dominant kernel and
 the CPU baseline are reported in the same JSON line.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Timing: at most one warmup step (its compress half profiled per kernel with
+HIP events), then up to K timed steps without events, as many as fit the
+run's wall budget (--budget-s, default 470 s; the line reports the steps
+actually timed), then a decode-step kernel profile, one host-buffer round
+trip (PCIe-inclusive, reported beside the device-resident `value`) and the
+CPU baseline.  Progress goes to stderr at least every 15 s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--budget-s S]
 """
 from __future__ import annotations
 
@@ -94,10 +101,10 @@ def cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, sample_len, thre
                 blob=blob)
 
 
-def decode_step_profile(codec, lanes: int, ds: int, d: int, bf16: bool, steps: int = 32) -> dict:
+def decode_step_profile(codec, lanes: int, steps: int = 32) -> dict:
     """Per-class kernel times of `steps` decode steps over `lanes` lanes,
     launched directly (not graph-replayed) with HIP events around every
-    kernel; the scan's algorithmic bytes give its HBM roofline."""
+    kernel on the launch stream."""
     import torch
     tok = torch.randint(0, 256, (lanes,), dtype=torch.uint8, device="cuda")
     logits = torch.empty(lanes, 256, device="cuda")
@@ -112,31 +119,46 @@ def decode_step_profile(codec, lanes: int, ds: int, d: int, bf16: bool, steps: i
     torch.cuda.synchronize()
     p = codec.profile_read()
     codec.profile(False)
-    sc = p["scan"]
-    gbs = sc["work"] / (sc["ms"] * 1e-3) / 1e9 if sc["ms"] > 0 else 0.0
-    di = 2 * d
-    return {
-        "lanes": lanes, "steps": steps, "launch": "direct (HIP events per kernel)",
-        "kernel_us_per_step": {k: round(v["ms"] * 1e3 / steps, 2) for k, v in p.items() if v["ms"] > 0},
-        "roofline_scan": {
-            "bound": "hbm",
-            "kernel": f"boa::{'dec_b16_scan_kernel' if bf16 else 'dec_scan_kernel'}"
-                      f"<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}, true|false>"
-                      " (state cached | streamed, by layer)",
-            "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-            "frac": round(gbs / PEAK_HBM_GBS, 4),
-            "avg_launch_us": round(sc["ms"] * 1e3 / max(sc["launches"], 1), 2),
-            "bytes_per_launch": round(sc["work"] / max(sc["launches"], 1)),
-            "bytes_per_lane_layer": f"8*di*ds + {2 if bf16 else 4}*(3*di + R), di = {di}, ds = {ds}",
-        },
-    }
+    return {k: dict(us_per_step=v["ms"] * 1e3 / steps, launches_per_step=v["launches"] / steps,
+                    work_per_step=v["work"] / steps) for k, v in p.items() if v["launches"]}
+
+
+def cpu_info() -> dict:
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return {"nproc": os.cpu_count(), "affinity": affinity, "model": model,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def roofline_entry(kernel, bound, achieved, peak, unit, avg_launch, per_launch, per_launch_key,
+                   traffic=None, **extra):
+    d = {"bound": bound, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak,
+         "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+         "avg_launch_us": round(avg_launch, 2), per_launch_key: round(per_launch)}
+    d.update(extra)
+    return d
 
 
 def main() -> int:
+    t_start = time.perf_counter()
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1)
-    ap.add_argument("--warmup", type=int, default=0)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--budget-s", type=float, default=470.0,
+                    help="wall-clock budget of the whole run; timed steps beyond it are skipped "
+                         "(the line reports the steps actually timed)")
     ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                     help="BASELINE config (c2 is the metric's config)")
     ap.add_argument("--chunks", type=int, default=0)
@@ -145,15 +167,14 @@ def main() -> int:
     ap.add_argument("--tile", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--cpu-sample-chunks", type=int, default=0)
+    ap.add_argument("--cpu-sample-chunks", type=int, default=64)
     ap.add_argument("--cpu-sample-len", type=int, default=4096)
     ap.add_argument("--no-decompress", action="store_true")
+    ap.add_argument("--no-host-path", action="store_true",
+                    help="skip the host-buffer (PCIe-inclusive) round trip")
     ap.add_argument("--warm-start", type=int, default=0, metavar="B",
                     help="warm-start interleave over B lanes (boa.cpp --warm-start with "
                          "--gpu-batch B); not the metric config")
-    ap.add_argument("--host-path", action="store_true",
-                    help="also time the host-buffer path (bytes in host memory -> BOA2 container "
-                         "in host memory, PCIe transfers included)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
     args = ap.parse_args()
@@ -166,12 +187,16 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
+    def log(msg):
+        print(f"[bench {time.perf_counter() - t_start:7.1f}s] {msg}", file=sys.stderr, flush=True)
+
     import numpy as np
     import torch
     import boa_hip
     import synth
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    log("torch and the codec library loaded")
     cfg = synth.CONFIGS[args.config]
     d, L, ds, prec = cfg["d_model"], cfg["n_layers"], cfg["d_state"], cfg["precision"]
     tmp = tempfile.mkdtemp(prefix="boa_bench_")
@@ -190,7 +215,7 @@ def main() -> int:
         workload += f"-warm{args.warm_start}"
     n = len(data)
     n_chunks = math.ceil(n / chunk)
-    print(f"[bench] {workload}: {n} bytes, {n_chunks} chunks of {chunk} B", file=sys.stderr, flush=True)
+    log(f"{workload}: {n} bytes, {n_chunks} chunks of {chunk} B")
 
     stream = torch.cuda.current_stream()
     codec = boa_hip.Codec(d, L, ds, max_lanes=n_chunks, tile=args.tile, precision=prec)
@@ -201,13 +226,28 @@ def main() -> int:
     d_pay = torch.empty(cap, dtype=torch.int32, device="cuda")
     d_out = torch.empty(n, dtype=torch.uint8, device="cuda")
 
-    # load every kernel once (module load, first-touch of buffers)
+    last_report = [time.perf_counter()]
+
+    def progress(phase, done, total):
+        now = time.perf_counter()
+        if now - last_report[0] >= 15.0:
+            last_report[0] = now
+            log(f"  {'compress' if phase == 0 else 'decompress'}: {done / 1e6:.1f} of "
+                f"{total / 1e6:.1f} MB")
+
+    codec.set_progress(progress)
+
+    # load every kernel once (module load, first touch of the buffers)
     prime = min(n, n_chunks * 64)
     codec.compress_device(d_data, prime, 64, d_pay, cap)
     torch.cuda.synchronize()
     codec.set_warm_start(args.warm_start)
+    last = n - (n_chunks - 1) * chunk
 
     def step(profile: bool):
+        """One pass of the path: compress the HBM-resident input, decompress
+        it back, check the round trip.  Returns (compress s, decompress s,
+        stream lengths, round trip ok, per-class profile of the compress)."""
         torch.cuda.synchronize()
         codec.profile(profile)
         if profile:
@@ -223,7 +263,6 @@ def main() -> int:
         if not args.no_decompress:
             offs = np.zeros(len(lens), np.uint64)
             offs[1:] = np.cumsum(lens[:-1] // 4)
-            last = n - (n_chunks - 1) * chunk
             d_out.zero_()
             torch.cuda.synchronize()
             t2 = time.perf_counter()
@@ -233,98 +272,160 @@ def main() -> int:
             ok = bool(torch.equal(d_out, d_data))
         return t1 - t0, t_dec, lens, ok, prof
 
-    for w in range(args.warmup):
-        print(f"[bench] warmup step {w}", file=sys.stderr, flush=True)
-        step(False)
+    # Warmup: at most one full step, with per-kernel HIP-event profiling of
+    # its compress half (the timed steps run without events).
+    prof = None
+    warm_done = 0
+    step_s = None
+    if args.warmup > 0:
+        log("warmup step (compress kernels profiled with HIP events)")
+        tc, td, lens, ok, prof = step(profile=True)
+        warm_done = 1
+        step_s = tc + (0 if args.no_decompress else td)
+        log(f"warmup: compress {tc:.2f} s, decompress {td:.2f} s, round trip {ok}")
+        if ok is False:
+            print("bench.py: warmup round trip failed", file=sys.stderr)
+            return 1
+
+    # Timed steps, within the run's wall budget: reserve the host-path round
+    # trip, the decode-step profile, the CPU baseline and a margin.
+    def reserve():
+        r = 45.0 + (0 if args.no_cpu else 45.0)
+        if not args.no_host_path and step_s:
+            r += step_s * 1.1
+        if prof is None and step_s:
+            r += step_s * 0.5
+        return r
+
     t_c = t_d = 0.0
     ok_all = True
-    prof = None
+    K = 0
     lens = None
-    for k in range(args.steps):
-        tc, td, lens, ok, p = step(profile=True)
-        print(f"[bench] step {k}: compress {tc:.3f} s, decompress {td:.3f} s, round trip {ok}",
-              file=sys.stderr, flush=True)
+    while K < args.steps:
+        left = args.budget_s - (time.perf_counter() - t_start) - reserve()
+        if K > 0 and step_s and left < step_s * 1.05:
+            break
+        tc, td, lens, ok, _ = step(profile=False)
+        K += 1
+        step_s = tc + (0 if args.no_decompress else td)
+        log(f"timed step {K}: compress {tc:.3f} s, decompress {td:.3f} s, round trip {ok}")
         t_c += tc
         t_d += td
         ok_all = ok_all and (ok is not False)
-        prof = p
-    K = args.steps
+    if K < args.steps:
+        log(f"timed {K} of {args.steps} requested steps (wall budget {args.budget_s:.0f} s)")
     comp_mb_s = n * K / t_c / 1e6
     dec_mb_s = n * K / t_d / 1e6 if not args.no_decompress else None
     ratio = n / container_bytes(lens, n_chunks)
 
-    # per-class kernel times come from HIP events recorded around every
-    # launch on the stream the kernels run on (boa_profile_*)
+    if prof is None:  # no warmup step: profile one compress pass now
+        log("compress pass with kernel profiling")
+        codec.profile(True)
+        codec.profile_reset()
+        codec.compress_device(d_data, n, chunk, d_pay, cap)
+        torch.cuda.synchronize()
+        prof = codec.profile_read()
+        codec.profile(False)
+
+    # per-class kernel times of the compress (HIP events on the launch stream)
+    kernel_ms = {k: round(v["ms"], 3) for k, v in prof.items() if v["launches"]}
     g = prof["gemm"]
-    gemm_tflops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
-    kernel_ms = {k: round(v["ms"], 3) for k, v in prof.items()}
-    roofline = {
-        "bound": "mfma",
-        "kernel": GEMM_KERNEL[prec],
-        "achieved": round(gemm_tflops, 2),
-        "peak": PEAK_TFLOPS[prec],
-        "unit": "TFLOP/s",
-        "frac": round(gemm_tflops / PEAK_TFLOPS[prec], 4),
-        "traffic": gemm_traffic_bytes() if workload == "c2" else None,
-        "launches": g["launches"],
-        "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4),
-        "flop_per_launch": round(g["work"] / max(g["launches"], 1)),
-    }
+    gemm_tf = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
+    peak_mm = PEAK_TFLOPS[prec]
+    gemm_launch_us = g["ms"] * 1e3 / max(g["launches"], 1)
+    roof_gemm = roofline_entry(GEMM_KERNEL[prec], "mfma", gemm_tf, peak_mm, "TFLOP/s",
+                               gemm_launch_us, g["work"] / max(g["launches"], 1), "flop_per_launch",
+                               traffic=gemm_traffic_bytes() if workload == "c2" else None,
+                               launches=g["launches"], class_ms_per_compress=round(g["ms"], 1))
     sc = prof["scan"]
     scan_gbs = sc["work"] / (sc["ms"] * 1e-3) / 1e9 if sc["ms"] > 0 else 0.0
-    roofline_scan = {
-        "bound": "hbm",
-        "kernel": f"boa::scan_chunk_kernel<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>",
-        "achieved": round(scan_gbs, 1),
-        "peak": PEAK_HBM_GBS,
-        "unit": "GB/s",
-        "frac": round(scan_gbs / PEAK_HBM_GBS, 4),
-        "launches": sc["launches"],
-        "avg_launch_ms": round(sc["ms"] / max(sc["launches"], 1), 4),
-        "bytes_per_launch": round(sc["work"] / max(sc["launches"], 1)),
-    }
-
+    roof_scan = roofline_entry(
+        f"boa::scan_chunk_kernel<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>", "hbm",
+        scan_gbs, PEAK_HBM_GBS, "GB/s", sc["ms"] * 1e3 / max(sc["launches"], 1),
+        sc["work"] / max(sc["launches"], 1), "bytes_per_launch", launches=sc["launches"],
+        class_ms_per_compress=round(sc["ms"], 1))
     cd_ = prof["cdf"]
     cdf_gbs = cd_["work"] / (cd_["ms"] * 1e-3) / 1e9 if cd_["ms"] > 0 else 0.0
-    roofline_coder = {
-        "bound": "hbm",
-        "kernel": "boa::cdf_targets_kernel",
-        "achieved": round(cdf_gbs, 1),
-        "peak": PEAK_HBM_GBS,
-        "unit": "GB/s",
-        "frac": round(cdf_gbs / PEAK_HBM_GBS, 4),
-        "launches": cd_["launches"],
-        "avg_launch_ms": round(cd_["ms"] / max(cd_["launches"], 1), 4),
-        "bytes_per_launch": round(cd_["work"] / max(cd_["launches"], 1)),
-    }
+    roof_coder = roofline_entry("boa::cdf_targets_kernel", "hbm", cdf_gbs, PEAK_HBM_GBS, "GB/s",
+                                cd_["ms"] * 1e3 / max(cd_["launches"], 1),
+                                cd_["work"] / max(cd_["launches"], 1), "bytes_per_launch",
+                                launches=cd_["launches"])
 
-    # The decode step's kernels, timed with HIP events on a few directly
-    # launched steps (boa_step_batch) after the timed region; the decode
-    # scan is the step's HBM-bound kernel.
-    dec_step = None
+    # The decode step's kernels, timed with HIP events on directly launched
+    # steps (boa_step_batch) after the timed region.
+    dec = None
+    roof_dec_gemm = roof_dec_scan = None
     if not args.no_decompress:
-        dec_step = decode_step_profile(codec, n_chunks, ds, d, prec == "bf16")
+        log("decode-step kernel profile (32 directly launched steps)")
+        lanes = n_chunks
+        dec = decode_step_profile(codec, lanes)
+        cached, fused, persistent = codec.decode_plan(lanes)
+        if "dec_gemm" in dec:
+            dg = dec["dec_gemm"]
+            tf = dg["work_per_step"] / (dg["us_per_step"] * 1e-6) / 1e12
+            roof_dec_gemm = roofline_entry(
+                "boa::dec_ln_gemm_kernel / dec_gemm_kernel / dec_b16_gemm* (decode-step GEMMs)",
+                "mfma", tf, peak_mm, "TFLOP/s", dg["us_per_step"] / dg["launches_per_step"],
+                dg["work_per_step"] / dg["launches_per_step"], "flop_per_launch",
+                launches_per_step=dg["launches_per_step"], us_per_step=round(dg["us_per_step"], 1))
+        if "dec_scan" in dec:
+            ds_ = dec["dec_scan"]
+            gbs = ds_["work_per_step"] / (ds_["us_per_step"] * 1e-6) / 1e9
+            roof_dec_scan = roofline_entry(
+                f"boa::{'dec_b16_scan_kernel' if prec == 'bf16' else 'dec_scan_kernel'}", "hbm",
+                gbs, PEAK_HBM_GBS, "GB/s", ds_["us_per_step"] / ds_["launches_per_step"],
+                ds_["work_per_step"] / ds_["launches_per_step"], "bytes_per_launch",
+                launches_per_step=ds_["launches_per_step"], us_per_step=round(ds_["us_per_step"], 1),
+                bytes_per_lane_layer=f"8*di*ds + {2 if prec == 'bf16' else 4}*(3*di + R)")
+        dec = {"lanes": lanes, "steps": 32, "launch": "direct (HIP events per kernel)",
+               "cached_layers": cached, "fused_layernorm": fused, "persistent": persistent,
+               "kernel_us_per_step": {k: round(v["us_per_step"], 2) for k, v in dec.items()}}
+
+    # The dominant kernel class of a step: its share of the measured round
+    # trip (compress classes from the profiled pass, decode classes from the
+    # per-step profile times the steps of the decompress).
+    # (cold mode: one batch of n_chunks lanes runs chunk - 1 steps)
+    steps_per_dec = chunk - 1
+    shares = {"compress GEMM": (g["ms"] * 1e-3, roof_gemm),
+              "compress scan": (sc["ms"] * 1e-3, roof_scan)}
+    if roof_dec_gemm:
+        shares["decode GEMMs"] = (dec["kernel_us_per_step"]["dec_gemm"] * 1e-6 * steps_per_dec,
+                                  roof_dec_gemm)
+    if roof_dec_scan:
+        shares["decode scan"] = (dec["kernel_us_per_step"]["dec_scan"] * 1e-6 * steps_per_dec,
+                                 roof_dec_scan)
+    dom = max(shares, key=lambda k: shares[k][0])
+    roofline = dict(shares[dom][1])
+    roofline["class"] = dom
+    roofline["class_s_per_step"] = round(shares[dom][0], 2)
 
     host = None
-    if args.host_path:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        blob = codec.compress(data, chunk_size=chunk)
-        t1 = time.perf_counter()
-        back = codec.decompress(blob) if not args.no_decompress else data
-        t2 = time.perf_counter()
-        host = {"compress_mb_s": round(n / (t1 - t0) / 1e6, 4),
-                "decompress_mb_s": round(n / (t2 - t1) / 1e6, 4) if not args.no_decompress else None,
-                "container_bytes": len(blob), "roundtrip_ok": back == data,
-                "container_matches_device_path": len(blob) == container_bytes(lens, n_chunks)}
-        ok_all = ok_all and host["roundtrip_ok"]
+    if not args.no_host_path:
+        left = args.budget_s - (time.perf_counter() - t_start) - (0 if args.no_cpu else 45.0)
+        if step_s and left > step_s * 1.1:
+            log("host-buffer round trip (PCIe-inclusive)")
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            blob = codec.compress(data, chunk_size=chunk)
+            t1 = time.perf_counter()
+            back = codec.decompress(blob) if not args.no_decompress else data
+            t2 = time.perf_counter()
+            host = {"compress_mb_s": round(n / (t1 - t0) / 1e6, 4),
+                    "decompress_mb_s": round(n / (t2 - t1) / 1e6, 4) if not args.no_decompress else None,
+                    "container_bytes": len(blob), "roundtrip_ok": back == data,
+                    "container_matches_device_path": len(blob) == container_bytes(lens, n_chunks),
+                    "span": "input bytes in host memory -> BOA2 container in host memory "
+                            "(H2D, D2H and the container write included)"}
+            ok_all = ok_all and host["roundtrip_ok"]
+        else:
+            log("host-buffer round trip skipped (wall budget)")
 
     cpu = None
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        sample_chunks = args.cpu_sample_chunks or 4 * threads
-        print(f"[bench] cpu baseline: {sample_chunks} chunks x {args.cpu_sample_len} B on {threads} threads",
-              file=sys.stderr, flush=True)
+        info = cpu_info()
+        threads = args.cpu_threads or int(info["omp_num_threads"] or 0) or info["affinity"]
+        sample_chunks = min(args.cpu_sample_chunks, n_chunks)
+        log(f"cpu baseline: {sample_chunks} chunks x {args.cpu_sample_len} B on {threads} threads")
         cb = cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, args.cpu_sample_len,
                           threads, d, L, ds, bf16=prec == "bf16")
         cpu = {"value": round(cb["compress_mb_s"], 5), "unit": "MB/s", "cores": threads,
@@ -332,7 +433,10 @@ def main() -> int:
                "sample": f"first {args.cpu_sample_len} B of each of the first {sample_chunks} chunks "
                          f"({cb['bytes']} B), oracle/refcpu compress (OpenMP over chunks)",
                "decompress_value": round(cb["decompress_mb_s"], 5),
-               "compress_s": round(cb["compress_s"], 2), "decompress_s": round(cb["decompress_s"], 2)}
+               "compress_s": round(cb["compress_s"], 2), "decompress_s": round(cb["decompress_s"], 2),
+               "host": info,
+               "threads_rule": "OMP_NUM_THREADS of the GPU box (its CPU share for one GPU), "
+                               "else every core in the process's affinity mask"}
 
     out = {
         "metric": METRIC,
@@ -340,7 +444,9 @@ def main() -> int:
         "unit": "MB/s",
         "n_gpus": 1,
         "steps": K,
-        "warmup": args.warmup,
+        "steps_requested": args.steps,
+        "warmup": warm_done,
+        "warmup_requested": args.warmup,
         "ms_per_step": round((t_c + (0 if args.no_decompress else t_d)) / K * 1e3, 1),
         "higher_is_better": True,
         "scaling": "weak",
@@ -354,20 +460,25 @@ def main() -> int:
                    "input": f"synth.gen_{args.config}"},
         "compress_mb_s": round(comp_mb_s, 4),
         "decompress_mb_s": round(dec_mb_s, 4) if dec_mb_s else None,
+        "value_span": "device-resident: input in HBM -> compacted payload in HBM (and back)",
         "compression_ratio": round(ratio, 5),
         "roundtrip_ok": ok_all,
         "compress_kernel_ms": kernel_ms,
         "roofline": roofline,
-        "roofline_scan": roofline_scan,
-        "roofline_coder": roofline_coder,
-        "decode_step": dec_step,
+        "roofline_compress_gemm": roof_gemm,
+        "roofline_scan": roof_scan,
+        "roofline_coder": roof_coder,
+        "roofline_decode_gemm": roof_dec_gemm,
+        "roofline_decode_scan": roof_dec_scan,
+        "decode_step": dec,
+        "host_path": host,
         "cpu_baseline": cpu,
+        "wall_s": round(time.perf_counter() - t_start, 1),
     }
-    if host:
-        out["host_path"] = host
     if cpu:
         out["speedup_vs_cpu_compress"] = round(comp_mb_s / cpu["value"], 1)
     print(json.dumps(out), flush=True)
+    codec.set_progress(None)
     codec.close()
     return 0 if ok_all else 1
 

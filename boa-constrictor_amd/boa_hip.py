@@ -19,12 +19,20 @@ LIB_PATH = os.path.join(HERE, "libboa_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "boa_hip.h")
 
 BOA_OK = 0
-K_GEMM, K_SCAN, K_CONV, K_LN, K_CDF, K_CODER, K_DECODE, K_GEMM_SMALL = range(8)
-K_NAMES = ["gemm", "scan", "conv", "ln", "cdf", "coder", "decode", "gemm_small"]
+(K_GEMM, K_SCAN, K_CONV, K_LN, K_CDF, K_CODER, K_DECODE, K_GEMM_SMALL, K_DEC_GEMM,
+ K_DEC_SCAN) = range(10)
+K_NAMES = ["gemm", "scan", "conv", "ln", "cdf", "coder", "decode", "gemm_small", "dec_gemm",
+           "dec_scan"]
+BOA_E_ARG, BOA_E_HIP, BOA_E_IO, BOA_E_FORMAT, BOA_E_STATE, BOA_E_NOMEM = -1, -2, -3, -4, -5, -6
+
+# void (*)(void* user, int32_t phase, int64_t done_bytes, int64_t total_bytes)
+PROGRESS_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int32, C.c_int64, C.c_int64)
 
 
 class BoaError(RuntimeError):
-    pass
+    def __init__(self, msg, rc=None):
+        super().__init__(msg)
+        self.rc = rc
 
 
 class Config(C.Structure):
@@ -66,6 +74,11 @@ def lib():
             "boa_use_own_stream": (C.c_int, [P]),
             "boa_set_temperature": (C.c_int, [P, f32]),
             "boa_set_warm_start": (C.c_int, [P, i32]),
+            "boa_set_progress": (C.c_int, [P, PROGRESS_FN, P]),
+            "boa_decode_plan": (C.c_int, [P, i32, C.POINTER(i32), C.POINTER(i32), C.POINTER(i32)]),
+            "boa_set_state_cache_budget": (C.c_int, [P, i64]),
+            "boa_last_timings": (C.c_int, [P, C.POINTER(C.c_double), C.POINTER(C.c_double),
+                                           C.POINTER(C.c_double)]),
             "boa_load_weights": (C.c_int, [P, C.c_char_p]),
             "boa_load_weights_mem": (C.c_int, [P, P, C.c_size_t]),
             "boa_weight_file_bytes": (i64, [i32, i32, i32, i32]),
@@ -123,7 +136,7 @@ class Codec:
 
     def _check(self, rc, what):
         if rc != BOA_OK:
-            raise BoaError(f"{what} failed ({rc}): {lib().boa_last_error(self.h).decode()}")
+            raise BoaError(f"{what} failed ({rc}): {lib().boa_last_error(self.h).decode()}", rc)
 
     def close(self):
         if getattr(self, "h", None):
@@ -193,6 +206,33 @@ class Codec:
                                                 lens.ctypes.data, fb.ctypes.data, len(fb),
                                                 chunk_len, last_len, _ptr(d_out)),
                     "decompress_device")
+
+    def set_progress(self, fn):
+        """fn(phase, done_bytes, total_bytes) during compress (phase 0) and
+        decompress (phase 1); None turns the reports off."""
+        if fn is None:
+            self._progress = None
+            self._check(lib().boa_set_progress(self.h, PROGRESS_FN(), None), "set_progress")
+            return
+        self._progress = PROGRESS_FN(lambda _u, ph, done, total: fn(ph, done, total))
+        self._check(lib().boa_set_progress(self.h, self._progress, None), "set_progress")
+
+    def decode_plan(self, lanes):
+        """(cached_layers, fused_ln, persistent) of the decode step at `lanes` lanes."""
+        a, b, p = C.c_int32(), C.c_int32(), C.c_int32()
+        self._check(lib().boa_decode_plan(self.h, lanes, C.byref(a), C.byref(b), C.byref(p)),
+                    "decode_plan")
+        return a.value, bool(b.value), bool(p.value)
+
+    def last_timings(self):
+        """(h2d_s, compute_s, d2h_s) of the last compress()/decompress() call."""
+        a, b, c = C.c_double(), C.c_double(), C.c_double()
+        self._check(lib().boa_last_timings(self.h, C.byref(a), C.byref(b), C.byref(c)),
+                    "last_timings")
+        return a.value, b.value, c.value
+
+    def set_state_cache_budget(self, nbytes):
+        self._check(lib().boa_set_state_cache_budget(self.h, int(nbytes)), "set_state_cache_budget")
 
     def set_warm_start(self, interleave_batch):
         """--warm-start (boa.cpp:310-319): 0 turns it off."""

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -29,6 +30,10 @@ namespace {
 constexpr int VOCAB = 256;
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+double now_s() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
 
 struct ProfRec {
   int cls;
@@ -103,10 +108,42 @@ struct boa_ctx {
   uint8_t* tok = nullptr;
   int* t_counter = nullptr;     // decode step counter (device)
 
-  // decompress: every step is replayed from a HIP graph on dec_stream
+  // decompress: every step is replayed from a HIP graph on dec_stream; the
+  // executable graph is kept while the step's launch arguments stay the same
   hipStream_t dec_stream = nullptr;
   hipEvent_t dec_fork = nullptr, dec_join = nullptr;
+  hipGraphExec_t dec_exec = nullptr;
+  struct GraphKey {
+    int lanes = -1;
+    const uint8_t* out = nullptr;
+    int64_t stride = 0;
+    const uint32_t* payload = nullptr;
+    float inv_temp = 0.0f;
+    hipStream_t stream = nullptr;
+  } dec_key;
   int32_t* h_sizes = nullptr;  // pinned
+
+  // first bytes of the chunks (compress) or of a batch's lanes (decompress)
+  uint8_t* first_buf = nullptr;
+  int64_t first_cap = 0;
+  // warm-start reorder scratch: the staged payload, stream offsets and sizes
+  uint32_t* reorder_words = nullptr;
+  int64_t reorder_words_cap = 0;
+  uint64_t* reorder_off = nullptr;
+  int32_t* reorder_sz = nullptr;
+  int64_t reorder_n_cap = 0;
+
+  // progress reports (boa.cpp's print_progress)
+  boa_progress_fn progress = nullptr;
+  void* progress_user = nullptr;
+  hipEvent_t prog_ev[2] = {nullptr, nullptr};
+  int64_t prog_base = 0, prog_total = 0;  // bytes done before this batch, bytes of the call
+
+  // wall-clock phases of the last buffer call: H2D, device work, D2H (s)
+  double t_h2d = 0, t_compute = 0, t_d2h = 0;
+
+  // decode state kept in the caches (bytes; < 0 = the default budget)
+  int64_t state_cache_budget = -1;
 
   // profiling
   bool prof_on = false;
@@ -398,7 +435,7 @@ hipError_t dgemm(boa_ctx* c, const float* Xt, const float* W, float* C, int ldc,
   a.Xt = Xt; a.ldx = c->ld_dec; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ldc;
   a.bias = bias;
   a.res = res; a.ldr = c->ld_dec; a.M = M; a.N = N; a.K = K; a.act = act; a.row_major = row_major;
-  return timed(c, BOA_K_GEMM_SMALL, 2.0 * M * N * K, [&] { return dec_gemm(a, c->stream); });
+  return timed(c, BOA_K_DEC_GEMM, 2.0 * M * N * K, [&] { return dec_gemm(a, c->stream); });
 }
 
 // Move the recurrent state into the layout the next call needs.
@@ -433,10 +470,66 @@ hipError_t ensure_state_layout(boa_ctx* c, int want_step) {
 // past the caches.  At C2 (1000 lanes, 40 KB of state per lane and layer)
 // this caches 4 of 8 layers: decode 1.72 -> 1.78 MB/s on MI355X, against
 // 1.75 with 5 and 1.65 with all 8.
+constexpr int64_t kStateCacheBudget = (int64_t)160 << 20;
+
 int dec_cached_layers(const boa_ctx* c, int lanes) {
   const double per_layer = (double)lanes * c->D.di * (c->D.ds + 4) * sizeof(float);
-  const double budget = 160.0 * (1 << 20);
+  const double budget =
+      (double)(c->state_cache_budget >= 0 ? c->state_cache_budget : kStateCacheBudget);
   return per_layer <= 0 ? c->D.L : std::min(c->D.L, (int)(budget / per_layer));
+}
+
+// LayerNorm fused into in_proj and FF1 up to 2048 lanes; above that the
+// separate kernels spread the work better (MI355X sweep)
+bool dec_fuse_ln(const boa_ctx* c, int lanes) {
+  const Dims& D = c->D;
+  return lanes <= 2048 && dec_ln_gemm_fits(D.d, 2 * D.di) && dec_ln_gemm_fits(D.d, 4 * D.d);
+}
+
+// Grow-only device buffer: reallocated only when a call needs more.
+template <class T>
+hipError_t ensure_buf(T** p, int64_t* cap, int64_t need) {
+  if (need <= *cap) return hipSuccess;
+  dfree(*p);
+  *p = nullptr;
+  *cap = 0;
+  hipError_t e = dalloc(p, (size_t)need);
+  if (e == hipSuccess) *cap = need;
+  return e;
+}
+
+// Drop the cached decode graph (its kernels hold weight and buffer pointers
+// and template choices that a weight load or a cache-budget change alters).
+void drop_dec_graph(boa_ctx* c) {
+  if (!c->dec_exec) return;
+  if (c->dec_stream) (void)hipStreamSynchronize(c->dec_stream);
+  (void)hipGraphExecDestroy(c->dec_exec);
+  c->dec_exec = nullptr;
+  c->dec_key = boa_ctx::GraphKey{};
+}
+
+// Report progress to the caller's callback once the work before the last
+// marker has finished on the device: `done` bytes of `total` are reported
+// when the marker recorded at the previous call has completed, so one
+// slice of work stays queued while the host waits.
+hipError_t progress_mark(boa_ctx* c, int phase, int64_t done_prev, int64_t total, int64_t* pend,
+                         int* slot) {
+  if (!c->progress) return hipSuccess;
+  for (int k = 0; k < 2; ++k)
+    if (!c->prog_ev[k]) {
+      hipError_t e = hipEventCreateWithFlags(&c->prog_ev[k], hipEventDisableTiming);
+      if (e) return e;
+    }
+  hipError_t e = hipEventRecord(c->prog_ev[*slot], c->stream);
+  if (e) return e;
+  if (*pend >= 0) {
+    e = hipEventSynchronize(c->prog_ev[*slot ^ 1]);
+    if (e) return e;
+    c->progress(c->progress_user, phase, *pend, total);
+  }
+  *pend = done_prev;
+  *slot ^= 1;
+  return hipSuccess;
 }
 
 hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
@@ -453,10 +546,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
   hipStream_t saved = c->stream;
   c->stream = s;  // dgemm and timed() launch on c->stream
   hipError_t e = hipSuccess;
-  // LayerNorm fused into in_proj and FF1 up to 2048 lanes; above that the
-  // separate kernels spread the work better (MI355X sweep)
-  const bool fuse_ln =
-      lanes <= 2048 && dec_ln_gemm_fits(D.d, 2 * D.di) && dec_ln_gemm_fits(D.d, 4 * D.d);
+  const bool fuse_ln = dec_fuse_ln(c, lanes);
   const int n_cached = dec_cached_layers(c, lanes);
   for (int l = 0; l < D.L && !e; ++l) {
     const LayerW& W = c->layers[l];
@@ -472,7 +562,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     a.conv_b = W.conv_b; a.conv_out = cvt;
     if (fuse_ln) {  // LN1 in front of in_proj, in one kernel
       a.Xt = xt;
-      e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * a.N * a.K, [&] {
+      e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * a.N * a.K, [&] {
         return launch_dec_ln_gemm(1, a, l == 0 ? c->emb : nullptr, tok, xt, W.ln1_w, W.ln1_b,
                                   l == 0 ? t_counter : nullptr, s);
       });
@@ -482,11 +572,11 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
                               D.d, ld, l == 0 ? t_counter : nullptr, s);
       });
       if (!e)
-        e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
+        e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
     }
     if (!e) e = dgemm(c, cvt, DW.w_x, rows, ld, nullptr, nullptr, lanes, c->n_xdec, D.di, ACT_NONE);
     if (!e)
-      e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
+      e = timed(c, BOA_K_DEC_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
         return launch_dec_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, cached, s);
       });
     if (!e) e = dgemm(c, yt, DW.w_out, ot, ld, W.b_out, nullptr, lanes, D.d, D.di, ACT_NONE);
@@ -494,7 +584,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
       DecGemmArgs f{};
       f.Xt = ot; f.ldx = ld; f.W = DW.w1; f.ldw = 4 * D.d; f.C = hidt; f.ldc = ld;
       f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU;
-      e = timed(c, BOA_K_GEMM_SMALL, 2.0 * lanes * f.N * f.K, [&] {
+      e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * f.N * f.K, [&] {
         return launch_dec_ln_gemm(2, f, nullptr, nullptr, nullptr, W.ln2_w, W.ln2_b, nullptr, s);
       });
     } else if (!e) {
@@ -532,7 +622,7 @@ hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* 
     return a;
   };
   auto run = [&](const DecB16Args& a) {
-    return timed(c, BOA_K_GEMM_SMALL, 2.0 * a.M * a.N * a.K, [&] { return dec_b16_gemm(a, s); });
+    return timed(c, BOA_K_DEC_GEMM, 2.0 * a.M * a.N * a.K, [&] { return dec_b16_gemm(a, s); });
   };
   hipError_t e = hipSuccess;
   const int n_cached = dec_cached_layers(c, lanes);
@@ -555,7 +645,7 @@ hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* 
     }
     if (!e) e = run(g(cvt, B.w_x, c->n_xdec, D.di, rows, DEC_OUT_B16, nullptr, ACT_NONE));
     if (!e)
-      e = timed(c, BOA_K_SCAN, 8.0 * lanes * D.di * D.ds + 2.0 * lanes * (3.0 * D.di + D.R), [&] {
+      e = timed(c, BOA_K_DEC_SCAN, 8.0 * lanes * D.di * D.ds + 2.0 * lanes * (3.0 * D.di + D.R), [&] {
         return launch_dec_b16_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, cached,
                                   s);
       });
@@ -691,9 +781,16 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
     c->stream = saved;
     return e;
   };
+  // progress: every kProgSteps steps, once the steps before have run
+  constexpr int kProgSteps = 2048;
+  int64_t pend = -1;
+  int slot = 0;
+  const int64_t total = c->prog_total, base = c->prog_base;
   if (c->prof_on || maxlen <= 2) {
     for (int t = 1; t < maxlen; ++t) {
       hipError_t e = one_step(s);
+      if (!e && c->progress && t % kProgSteps == 0)
+        e = progress_mark(c, 1, base + (int64_t)lanes * (t + 1), total, &pend, &slot);
       if (e) return e;
     }
     return hipSuccess;
@@ -705,25 +802,48 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
   if (!e) e = hipEventRecord(c->dec_fork, s);
   if (!e) e = hipStreamWaitEvent(c->dec_stream, c->dec_fork, 0);
   if (e) return e;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  e = hipStreamBeginCapture(c->dec_stream, hipStreamCaptureModeThreadLocal);
-  if (!e) {
-    hipError_t le = one_step(c->dec_stream);
-    e = hipStreamEndCapture(c->dec_stream, &graph);
-    if (!e) e = le;
+  // the step's launch arguments; the executable graph is reused while they
+  // stay the same (every pointer the step reads or writes is either one of
+  // these or a buffer of the context)
+  boa_ctx::GraphKey key;
+  key.lanes = lanes; key.out = out; key.stride = chunk; key.payload = d_payload;
+  key.inv_temp = c->inv_temp; key.stream = c->dec_stream;
+  const boa_ctx::GraphKey& k0 = c->dec_key;
+  const bool same = c->dec_exec && k0.lanes == key.lanes && k0.out == key.out &&
+                    k0.stride == key.stride && k0.payload == key.payload &&
+                    k0.inv_temp == key.inv_temp && k0.stream == key.stream;
+  if (!same) {
+    if (c->dec_exec) {
+      e = hipStreamSynchronize(c->dec_stream);  // its last replay has finished
+      (void)hipGraphExecDestroy(c->dec_exec);
+      c->dec_exec = nullptr;
+      if (e) return e;
+    }
+    hipGraph_t graph = nullptr;
+    e = hipStreamBeginCapture(c->dec_stream, hipStreamCaptureModeThreadLocal);
+    if (!e) {
+      hipError_t le = one_step(c->dec_stream);
+      e = hipStreamEndCapture(c->dec_stream, &graph);
+      if (!e) e = le;
+    }
+    if (!e) e = hipGraphInstantiate(&c->dec_exec, graph, nullptr, nullptr, 0);
+    if (graph) (void)hipGraphDestroy(graph);
+    if (e) {
+      c->dec_exec = nullptr;
+      return e;
+    }
+    c->dec_key = key;
   }
-  if (!e) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  if (graph) (void)hipGraphDestroy(graph);
-  for (int t = 1; t < maxlen && !e; ++t) e = hipGraphLaunch(exec, c->dec_stream);
+  hipStream_t saved = c->stream;
+  c->stream = c->dec_stream;  // progress markers go on the replay stream
+  for (int t = 1; t < maxlen && !e; ++t) {
+    e = hipGraphLaunch(c->dec_exec, c->dec_stream);
+    if (!e && c->progress && t % kProgSteps == 0)
+      e = progress_mark(c, 1, base + (int64_t)lanes * (t + 1), total, &pend, &slot);
+  }
+  c->stream = saved;
   hipError_t e2 = hipEventRecord(c->dec_join, c->dec_stream);
   if (!e2) e2 = hipStreamWaitEvent(s, c->dec_join, 0);
-  // the executable graph is released only after its last replay finished
-  if (exec) {
-    hipError_t e3 = hipStreamSynchronize(c->dec_stream);
-    if (!e2) e2 = e3;
-    (void)hipGraphExecDestroy(exec);
-  }
   return e ? e : e2;
 }
 
@@ -797,6 +917,10 @@ void boa_destroy(boa_ctx* c) {
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
   dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
   if (c->h_sizes) (void)hipHostFree(c->h_sizes);
+  drop_dec_graph(c);
+  dfree(c->first_buf); dfree(c->reorder_words); dfree(c->reorder_off); dfree(c->reorder_sz);
+  for (hipEvent_t e : c->prog_ev)
+    if (e) (void)hipEventDestroy(e);
   if (c->dec_stream) (void)hipStreamDestroy(c->dec_stream);
   if (c->dec_fork) (void)hipEventDestroy(c->dec_fork);
   if (c->dec_join) (void)hipEventDestroy(c->dec_join);
@@ -822,6 +946,31 @@ int boa_set_temperature(boa_ctx* c, float t) {
   if (!c || !(t > 0.0f)) return BOA_E_ARG;
   c->cfg.temperature = t;
   c->inv_temp = 1.0f / t;
+  return BOA_OK;
+}
+
+int boa_set_progress(boa_ctx* c, boa_progress_fn fn, void* user) {
+  if (!c) return BOA_E_ARG;
+  c->progress = fn;
+  c->progress_user = user;
+  return BOA_OK;
+}
+
+int boa_set_state_cache_budget(boa_ctx* c, int64_t bytes) {
+  if (!c) return BOA_E_ARG;
+  drop_dec_graph(c);
+  c->state_cache_budget = bytes < 0 ? -1 : bytes;
+  return BOA_OK;
+}
+
+int boa_decode_plan(const boa_ctx* c, int32_t lanes, int32_t* cached_layers, int32_t* fused_ln,
+                    int32_t* persistent) {
+  if (!c || lanes < 1 || lanes > c->cfg.max_lanes) return BOA_E_ARG;
+  const Dims& D = c->D;
+  const bool pers = !c->bf16 && dec_persist_fits(D.d, D.ds, D.r, D.L);
+  if (cached_layers) *cached_layers = pers ? D.L : dec_cached_layers(c, lanes);
+  if (fused_ln) *fused_ln = (!pers && !c->bf16 && dec_fuse_ln(c, lanes)) ? 1 : 0;
+  if (persistent) *persistent = pers ? 1 : 0;
   return BOA_OK;
 }
 
@@ -915,6 +1064,7 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
   const size_t hb2 = raw(VOCAB);
   if (rd.bad || rd.pos != n) return fail(c, BOA_E_FORMAT, "weight file truncated");
 
+  drop_dec_graph(c);
   dfree(c->wbuf);
   c->wbuf = nullptr;
   c->loaded = false;
@@ -1179,15 +1329,16 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
   if ((rc = ensure_rows(c, (int64_t)B * T))) return rc;
   if ((rc = ensure_words(c, pitch))) return rc;
   hipStream_t s = c->stream;
-  uint8_t* d_first = nullptr;
-  if (dalloc(&d_first, (size_t)nc)) return fail(c, BOA_E_NOMEM, "allocation failed");
+  if (ensure_buf(&c->first_buf, &c->first_cap, nc))
+    return fail(c, BOA_E_NOMEM, "device allocation of the first-byte buffer failed");
   hipLaunchKernelGGL(gather_first_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s,
-                     d_data, chunk, n, (int)nc, d_first);
+                     d_data, chunk, n, (int)nc, c->first_buf);
   hipError_t e = hipGetLastError();
-  if (!e) e = hipMemcpyAsync(h_first, d_first, (size_t)nc, hipMemcpyDeviceToHost, s);
+  if (!e) e = hipMemcpyAsync(h_first, c->first_buf, (size_t)nc, hipMemcpyDeviceToHost, s);
   if (!e) e = hipStreamSynchronize(s);
-  dfree(d_first);
   if (e) return hip_fail(c, e, "first bytes");
+  const int64_t processed = std::min<int64_t>(n, nc * chunk);
+  int64_t done = 0;  // input bytes of finished batch iterations
   // warm-start: where each chunk's stream landed in the iteration-ordered payload
   std::vector<uint64_t> stage_off(warm ? (size_t)nc : 0);
   int64_t out_words = 0;
@@ -1202,6 +1353,8 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
       if (i == 0 && (rc = boa_reset_state(c, G))) return rc;
       e = launch_rc_enc_init(c->enc, lanes, s);
       if (e) return hip_fail(c, e, "rc init");
+      int64_t pend = -1;
+      int slot = 0;
       for (int64_t t0 = 0; t0 < chunk; t0 += T) {
         const int Tt = (int)std::min<int64_t>(T, chunk - t0);
         e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
@@ -1215,6 +1368,9 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
             return launch_rc_encode_tile(c->lowprob, tok, Tt, (int)t0, lanes, c->enc, c->words,
                                          pitch, s);
           });
+        if (!e && c->progress)
+          e = progress_mark(c, 0, std::min(processed, done + (int64_t)lanes * (t0 + Tt)), processed,
+                            &pend, &slot);
         if (e) return hip_fail(c, e, "compress tile");
       }
       e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
@@ -1236,8 +1392,10 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
         h_stream_bytes[ci] = 4ull * (uint64_t)c->h_sizes[b];
         if (warm) stage_off[(size_t)ci] = (uint64_t)at;
         at += c->h_sizes[b];
+        done += std::min<int64_t>(chunk, n - ci * chunk);
       }
       out_words += batch_words;
+      if (c->progress) c->progress(c->progress_user, 0, done, processed);
     }
   }
   if (warm && S > 1 && out_words > 0) {
@@ -1250,14 +1408,18 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
       sizes[(size_t)ci] = (int32_t)(h_stream_bytes[ci] / 4);
       at += sizes[(size_t)ci];
     }
-    uint32_t* tmp = nullptr;
-    uint64_t* d_off = nullptr;
-    int32_t* d_sz = nullptr;
-    if (dalloc(&tmp, (size_t)out_words) || dalloc(&d_off, 2 * (size_t)nc) ||
-        dalloc(&d_sz, (size_t)nc)) {
-      dfree(tmp); dfree(d_off);
-      return fail(c, BOA_E_NOMEM, "allocation failed");
+    if (ensure_buf(&c->reorder_words, &c->reorder_words_cap, out_words))
+      return fail(c, BOA_E_NOMEM, "device allocation of the reorder buffer failed");
+    if (nc > c->reorder_n_cap) {
+      dfree(c->reorder_off); dfree(c->reorder_sz);
+      c->reorder_off = nullptr; c->reorder_sz = nullptr; c->reorder_n_cap = 0;
+      if (dalloc(&c->reorder_off, 2 * (size_t)nc) || dalloc(&c->reorder_sz, (size_t)nc))
+        return fail(c, BOA_E_NOMEM, "device allocation of the reorder buffer failed");
+      c->reorder_n_cap = nc;
     }
+    uint32_t* tmp = c->reorder_words;
+    uint64_t* d_off = c->reorder_off;
+    int32_t* d_sz = c->reorder_sz;
     e = hipMemcpyAsync(d_off, stage_off.data(), 8 * (size_t)nc, hipMemcpyHostToDevice, s);
     if (!e) e = hipMemcpyAsync(d_off + nc, dst_off.data(), 8 * (size_t)nc, hipMemcpyHostToDevice, s);
     if (!e) e = hipMemcpyAsync(d_sz, sizes.data(), 4 * (size_t)nc, hipMemcpyHostToDevice, s);
@@ -1267,7 +1429,6 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
       });
     if (!e) e = hipMemcpyAsync(d_payload, tmp, 4 * (size_t)out_words, hipMemcpyDeviceToDevice, s);
     if (!e) e = hipStreamSynchronize(s);
-    dfree(tmp); dfree(d_off); dfree(d_sz);
     if (e) return hip_fail(c, e, "warm-start reorder");
   }
   if (h_payload_words) *h_payload_words = out_words;
@@ -1292,9 +1453,12 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
   std::vector<uint64_t> offs(B);
   std::vector<int32_t> nw(B), lens(B);
   std::vector<uint8_t> first(B);
-  uint8_t* d_first = nullptr;
-  if (dalloc(&d_first, (size_t)B)) return fail(c, BOA_E_NOMEM, "allocation failed");
+  if (ensure_buf(&c->first_buf, &c->first_cap, B))
+    return fail(c, BOA_E_NOMEM, "device allocation of the first-byte buffer failed");
+  uint8_t* d_first = c->first_buf;
   const int64_t pitch_bytes = pitch_words_for(chunk) * 4;
+  c->prog_total = (nc - 1) * chunk + last_len;
+  c->prog_base = 0;
   for (int64_t u0 = 0; u0 < units; u0 += B) {
     const int G = (int)std::min<int64_t>(B, units - u0);
     for (int64_t i = 0; i < S; ++i) {
@@ -1303,10 +1467,8 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       int32_t maxlen = 0;
       for (int b = 0; b < lanes; ++b) {
         const int64_t ci = warm ? (u0 + b) * S + i : u0 + b;
-        if ((int64_t)h_stream_bytes[ci] > pitch_bytes) {
-          dfree(d_first);
+        if ((int64_t)h_stream_bytes[ci] > pitch_bytes)
           return fail(c, BOA_E_FORMAT, "stream too large for the chunk length");
-        }
         offs[b] = h_offsets_words[ci];
         nw[b] = (int32_t)(h_stream_bytes[ci] / 4);
         lens[b] = (int32_t)(ci == nc - 1 ? last_len : chunk);
@@ -1317,9 +1479,9 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       if (!e) e = hipMemcpyAsync(c->sizes, nw.data(), 4 * lanes, hipMemcpyHostToDevice, s);
       if (!e) e = hipMemcpyAsync(c->lens, lens.data(), 4 * lanes, hipMemcpyHostToDevice, s);
       if (!e) e = hipMemcpyAsync(d_first, first.data(), lanes, hipMemcpyHostToDevice, s);
-      if (e) { dfree(d_first); return hip_fail(c, e, "decode upload"); }
+      if (e) return hip_fail(c, e, "decode upload");
       // warm-start resets the state only before a unit's first chunk (boa.cpp:690-693)
-      if (i == 0 && (rc = boa_reset_state(c, G))) { dfree(d_first); return rc; }
+      if (i == 0 && (rc = boa_reset_state(c, G))) return rc;
       const int64_t c0 = warm ? u0 * S + i : u0;
       const int64_t stride = warm ? S * chunk : chunk;
       uint8_t* out = d_out + c0 * chunk;
@@ -1328,21 +1490,22 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       e = hipGetLastError();
       if (!e) e = launch_rc_dec_init(c->dec, d_payload, c->offsets, c->sizes, lanes, s);
       if (!e) e = ensure_state_layout(c, 1);
-      if (e) { dfree(d_first); return hip_fail(c, e, "decode init"); }
+      if (e) return hip_fail(c, e, "decode init");
       e = decode_steps(c, lanes, maxlen, out, stride, d_payload);
-      if (e) { dfree(d_first); return hip_fail(c, e, "decode step"); }
+      if (e) return hip_fail(c, e, "decode step");
       // The compressor's state consumed every byte of the chunk; the units
       // that go on feed the last decoded byte before their next chunk.
       const int next = warm && i + 1 < S ? iter_lanes(warm, nc, S, u0, G, i + 1) : 0;
       if (next > 0) {
         e = step_forward(c, c->tok, next, false, c->dlogits);
-        if (e) { dfree(d_first); return hip_fail(c, e, "warm-start carry step"); }
+        if (e) return hip_fail(c, e, "warm-start carry step");
       }
       e = hipStreamSynchronize(s);
-      if (e) { dfree(d_first); return hip_fail(c, e, "decode sync"); }
+      if (e) return hip_fail(c, e, "decode sync");
+      for (int b = 0; b < lanes; ++b) c->prog_base += lens[b];
+      if (c->progress) c->progress(c->progress_user, 1, c->prog_base, c->prog_total);
     }
   }
-  dfree(d_first);
   return BOA_OK;
 }
 
@@ -1360,20 +1523,27 @@ int boa_compress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, int64_t chun
     dfree(d_in);
     return fail(c, BOA_E_NOMEM, "allocation failed");
   }
+  const double t0 = now_s();
   if (n) {
     hipError_t e = hipMemcpyAsync(d_in, h_in, (size_t)n, hipMemcpyHostToDevice, c->stream);
+    if (!e) e = hipStreamSynchronize(c->stream);
     if (e) { dfree(d_in); dfree(d_pay); return hip_fail(c, e, "upload"); }
   }
+  const double t1 = now_s();
   std::vector<uint64_t> lens((size_t)std::max<int64_t>(nc, 1));
   std::vector<uint8_t> first((size_t)std::max<int64_t>(nc, 1));
   int64_t words = 0;
   rc = boa_compress_device(c, d_in, n, chunk, max_chunks, d_pay, cap, lens.data(), first.data(), &words);
   if (rc) { dfree(d_in); dfree(d_pay); return rc; }
+  const double t2 = now_s();
   std::vector<uint8_t> payload((size_t)words * 4);
   if (words) {
     hipError_t e = hipMemcpy(payload.data(), d_pay, (size_t)words * 4, hipMemcpyDeviceToHost);
     if (e) { dfree(d_in); dfree(d_pay); return hip_fail(c, e, "download"); }
   }
+  c->t_h2d = t1 - t0;
+  c->t_compute = t2 - t1;
+  c->t_d2h = now_s() - t2;
   dfree(d_in);
   dfree(d_pay);
   Boa2Header h;
@@ -1435,17 +1605,23 @@ int boa_decompress_buffer(boa_ctx* c, const uint8_t* h_in, int64_t n, uint8_t** 
     dfree(d_pay);
     return fail(c, BOA_E_NOMEM, "allocation failed");
   }
+  const double t0 = now_s();
   hipError_t e = hipMemcpy(d_pay, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
   if (e) { dfree(d_pay); dfree(d_out); return hip_fail(c, e, "upload"); }
+  const double t1 = now_s();
   const int32_t saved_warm = c->warm_batch;
   c->warm_batch = warm ? (int32_t)P.interleave_batch : 0;
   rc = boa_decompress_device(c, d_pay, offs.data(), lens.data(), P.first.data(), (int32_t)nc,
                              P.hdr.chunk_len, nc ? P.hdr.last_chunk_len : 0, d_out);
   c->warm_batch = saved_warm;
   if (rc) { dfree(d_pay); dfree(d_out); return rc; }
+  const double t2 = now_s();
   uint8_t* o = (uint8_t*)malloc((size_t)std::max<int64_t>(total, 1));
   if (!o) { dfree(d_pay); dfree(d_out); return fail(c, BOA_E_NOMEM, "host allocation failed"); }
   if (total) e = hipMemcpy(o, d_out, (size_t)total, hipMemcpyDeviceToHost);
+  c->t_h2d = t1 - t0;
+  c->t_compute = t2 - t1;
+  c->t_d2h = now_s() - t2;
   dfree(d_pay);
   dfree(d_out);
   if (e) { free(o); return hip_fail(c, e, "download"); }
@@ -1484,6 +1660,14 @@ int boa_decompress_file(boa_ctx* c, const char* in_path, const char* out_path) {
 void boa_free(void* p) { free(p); }
 
 uint32_t boa_crc32(const uint8_t* data, int64_t n) { return boa2_crc32(data, (size_t)n); }
+
+int boa_last_timings(const boa_ctx* c, double* h2d_s, double* compute_s, double* d2h_s) {
+  if (!c) return BOA_E_ARG;
+  if (h2d_s) *h2d_s = c->t_h2d;
+  if (compute_s) *compute_s = c->t_compute;
+  if (d2h_s) *d2h_s = c->t_d2h;
+  return BOA_OK;
+}
 
 int boa_profile_enable(boa_ctx* c, int32_t on) {
   if (!c) return BOA_E_ARG;

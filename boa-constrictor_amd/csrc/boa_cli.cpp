@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <chrono>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -30,29 +31,58 @@ static int usage() {
   return 1;
 }
 
-static int auto_batch(boa_config cfg, int64_t chunk, bool compress) {
+// --gpu-batch 0: size the lane batch from free device memory, the steps of
+// auto_size_params (boa.cpp:109-156): start at 64 (compress) or 1024
+// (decompress) lanes, halve while the estimate exceeds 90 % of free memory,
+// and if one lane still does not fit halve the chunk size down to 256 bytes;
+// otherwise double while the next size fits, up to 8192 lanes.
+static int auto_batch(boa_config cfg, int64_t& chunk, bool compress) {
   size_t free_b = 0, total_b = 0;
   if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return compress ? 64 : 1024;
   const int64_t target = (int64_t)(free_b * 0.9);
   int b = compress ? 64 : 1024;
-  cfg.max_lanes = b;
-  int64_t mem = boa_estimate_memory(&cfg, chunk, compress);
+  auto est = [&](int lanes) {
+    cfg.max_lanes = lanes;
+    return boa_estimate_memory(&cfg, chunk, compress);
+  };
+  int64_t mem = est(b);
   if (mem > target) {
     while (b > 1 && mem > target) {
       b /= 2;
-      cfg.max_lanes = b;
-      mem = boa_estimate_memory(&cfg, chunk, compress);
+      mem = est(b);
+    }
+    while (chunk > 256 && mem > target) {
+      chunk /= 2;
+      mem = est(b);
     }
   } else {
-    for (;;) {
-      cfg.max_lanes = b * 2;
-      int64_t m2 = boa_estimate_memory(&cfg, chunk, compress);
-      if (m2 < target && b * 2 <= 8192) b *= 2;
-      else break;
-    }
+    while (b * 2 <= 8192 && est(b * 2) < target) b *= 2;
   }
-  printf("Auto-sizing: Selected Batch=%d, Chunk=%lld\n", b, (long long)chunk);
+  mem = est(b);
+  printf("Auto-sizing: Selected Batch=%d, Chunk=%lld (%lld MB VRAM est, %lld MB free)\n", b,
+         (long long)chunk, (long long)(mem >> 20), (long long)(free_b >> 20));
   return b;
+}
+
+// Progress bar in the form of print_progress (boa.cpp:30-50): percent of the
+// input done and MB/s (2^20 B/s) so far.
+struct Progress {
+  std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+  const char* prefix = "";
+};
+
+static void on_progress(void* user, int32_t, int64_t done, int64_t total) {
+  const Progress* p = (const Progress*)user;
+  const double sec =
+      std::chrono::duration<double>(std::chrono::steady_clock::now() - p->t0).count();
+  const double frac = total > 0 ? (double)done / (double)total : 1.0;
+  const int width = 40, pos = (int)(width * frac);
+  char bar[64];
+  for (int i = 0; i < width; ++i) bar[i] = i < pos ? '=' : (i == pos ? '>' : ' ');
+  bar[width] = 0;
+  printf("\r%s [%s] %d%% %.2f MB/s", p->prefix, bar, (int)(frac * 100),
+         sec > 0 ? (double)done / (1024.0 * 1024.0) / sec : 0.0);
+  fflush(stdout);
 }
 
 int main(int argc, char** argv) {
@@ -103,7 +133,9 @@ int main(int argc, char** argv) {
   if (chunk <= 0) chunk = 4096;
   const bool compress = mode == "compress";
   if (!compress && mode != "decompress") { fprintf(stderr, "Unknown mode: %s\n", mode.c_str()); return 1; }
-  cfg.max_lanes = gpu_batch > 0 ? gpu_batch : auto_batch(cfg, chunk, compress);
+  int64_t chunk64 = chunk;
+  cfg.max_lanes = gpu_batch > 0 ? gpu_batch : auto_batch(cfg, chunk64, compress);
+  chunk = chunk64;
   boa_ctx* ctx = nullptr;
   int rc = boa_create(&cfg, &ctx);
   if (rc) { fprintf(stderr, "boa_create failed (%d)\n", rc); return 1; }
@@ -113,16 +145,34 @@ int main(int argc, char** argv) {
     boa_set_warm_start(ctx, cfg.max_lanes);
     printf("Using warm-start interleaved compression. Batch=%d\n", cfg.max_lanes);
   }
+  Progress prog;
+  prog.prefix = compress ? "Compressing" : "Decompressing";
+  boa_set_progress(ctx, on_progress, &prog);
+  if (show_timings) boa_profile_enable(ctx, 1);
   auto t0 = std::chrono::steady_clock::now();
+  prog.t0 = t0;
   rc = compress ? boa_compress_file(ctx, in.c_str(), out.c_str(), chunk, max_chunks)
                 : boa_decompress_file(ctx, in.c_str(), out.c_str());
   double sec = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-  if (rc) { fprintf(stderr, "%s failed: %s\n", mode.c_str(), boa_last_error(ctx)); boa_destroy(ctx); return 1; }
+  if (rc) { fprintf(stderr, "\n%s failed: %s\n", mode.c_str(), boa_last_error(ctx)); boa_destroy(ctx); return 1; }
   FILE* f = fopen(compress ? in.c_str() : out.c_str(), "rb");
   long long nbytes = 0;
   if (f) { fseek(f, 0, SEEK_END); nbytes = ftell(f); fclose(f); }
-  printf("Done. Time: %.3fs, Avg Throughput: %.3f MB/s\n", sec, nbytes / 1e6 / (sec > 0 ? sec : 1));
-  if (show_timings) printf("Timing (s): total=%.3f (file I/O and PCIe included)\n", sec);
+  printf("\nDone. Time: %.3fs, Avg Throughput: %.3f MB/s\n", sec,
+         nbytes / (1024.0 * 1024.0) / (sec > 0 ? sec : 1));
+  if (show_timings) {
+    // H2D / Compute / D2H as boa.cpp:504-507; Forward and Encode are the
+    // summed kernel times of the model and of the CDF + coder kernels
+    double h2d = 0, comp = 0, d2h = 0, fwd = 0, enc = 0;
+    boa_last_timings(ctx, &h2d, &comp, &d2h);
+    const int fwd_k[] = {BOA_K_GEMM, BOA_K_SCAN, BOA_K_CONV, BOA_K_LN, BOA_K_GEMM_SMALL,
+                         BOA_K_DEC_GEMM, BOA_K_DEC_SCAN};
+    const int enc_k[] = {BOA_K_CDF, BOA_K_CODER, BOA_K_DECODE};
+    for (int k : fwd_k) { double ms = 0; boa_profile_read(ctx, k, &ms, nullptr, nullptr); fwd += ms * 1e-3; }
+    for (int k : enc_k) { double ms = 0; boa_profile_read(ctx, k, &ms, nullptr, nullptr); enc += ms * 1e-3; }
+    printf("Timing (s): H2D=%.3f Compute=%.3f D2H=%.3f Forward=%.3f Encode=%.3f\n", h2d, comp, d2h,
+           fwd, enc);
+  }
   boa_destroy(ctx);
   return 0;
 }

@@ -39,7 +39,6 @@ hipError_t gemm_f32(const GemmArgs& a, hipStream_t s);
 // Tile configuration gemm_f32 picks: 0 = 128x256 (bulk GEMMs of a compress
 // tile), 1 = 128x64 (narrow compress GEMMs), 2 = 32x32 (decode-step sizes).
 int gemm_f32_config(const GemmArgs& a);
-hipError_t gemm_f32_sweep(int cfg, const GemmArgs& a, hipStream_t s);
 
 // Encoder / decoder coder state (layout of RCState / RCDecState,
 // portability_solved_cpp/gemm_gpu.hpp:115-121, 212-217, padded to 8 bytes).
@@ -93,7 +92,6 @@ struct GemmB16Args {
   int M, N, K, act;
 };
 hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s);
-hipError_t gemm_bf16_sweep(int cfg, const GemmB16Args& a, hipStream_t s);
 hipError_t launch_b16_weight_nk(const float* w, int ldw_in, int N, int K, int n_pad, uint16_t* out,
                                 hipStream_t s);
 
@@ -138,7 +136,7 @@ bool dec_ln_gemm_fits(int d, int N);
 hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, const uint8_t* tok,
                               float* xt, const float* lw, const float* lb, int* t_counter,
                               hipStream_t s);
-// explicit wave-tile configuration (tile sweeps)
+// decode GEMM with an explicit wave-tile configuration (4, 9, 10 or 13; all give the same bits)
 hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s);
 hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* out, int K, int ldn,
                                  int permute, int zs, int ze, hipStream_t s);

@@ -167,8 +167,22 @@ inline bool boa2_parse(const uint8_t* d, size_t n, Boa2Parsed& P, std::string& w
       why = "BOA2 payload out of range";
       return false;
     }
-  if (nc && (P.hdr.chunk_len == 0 || P.hdr.last_chunk_len > P.hdr.chunk_len)) {
+  // Header consistency beyond what the reference's reader checks: the
+  // lengths a compressor can write (chunks of at most 2^30 bytes, a last
+  // chunk of 1 .. chunk_len bytes, total = (n - 1) chunk_len + last), and a
+  // warm-start interleave batch in [1, n_chunks].
+  if (nc && (P.hdr.chunk_len == 0 || P.hdr.chunk_len > (1u << 30) || P.hdr.last_chunk_len == 0 ||
+             P.hdr.last_chunk_len > P.hdr.chunk_len)) {
     why = "Bad BOA2 chunk lengths";
+    return false;
+  }
+  const uint64_t total = nc ? (uint64_t)(nc - 1) * P.hdr.chunk_len + P.hdr.last_chunk_len : 0;
+  if (P.hdr.total_size != total) {
+    why = "BOA2 total size does not match the chunk lengths";
+    return false;
+  }
+  if ((P.hdr.flags & 1u) && nc && (fp_len < 4 || P.interleave_batch == 0 || P.interleave_batch > nc)) {
+    why = "Bad BOA2 warm-start interleave batch";
     return false;
   }
   return true;

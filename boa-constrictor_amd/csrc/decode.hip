@@ -226,23 +226,10 @@ hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (hipError_t e = dec_check(a)) return e;
   switch (cfg) {
-    case 0: return dec_launch<1, 1, 2, 2>(a, s);
-    case 1: return dec_launch<1, 1, 2, 4>(a, s);
-    case 2: return dec_launch<1, 1, 2, 6>(a, s);
-    case 3: return dec_launch<1, 1, 2, 8>(a, s);
     case 4: return dec_launch<1, 1, 1, 8>(a, s);
-    case 5: return dec_launch<1, 1, 1, 16>(a, s);
-    case 6: return dec_launch<1, 1, 4, 4>(a, s);
-    case 7: return dec_launch<2, 1, 2, 4>(a, s);
-    case 8: return dec_launch<1, 2, 2, 4>(a, s);
     case 9: return dec_launch<2, 2, 1, 6>(a, s);
     case 10: return dec_launch<1, 1, 1, 2>(a, s);
-    case 11: return dec_launch<1, 4, 1, 4>(a, s);
-    case 12: return dec_launch<1, 4, 2, 2>(a, s);
     case 13: return dec_launch<4, 1, 1, 4>(a, s);
-    case 14: return dec_launch<2, 1, 1, 8>(a, s);
-    case 15: return dec_launch<1, 2, 1, 8>(a, s);
-    case 16: return dec_launch<1, 2, 2, 2>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -215,29 +215,6 @@ hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s) {
   return launch_b16<128, 64, 4, 2, 64>(a, s);
 }
 
-// Explicit configurations for tile sweeps (same numerics for every entry).
-hipError_t gemm_bf16_sweep(int cfg, const GemmB16Args& a, hipStream_t s) {
-  switch (cfg) {
-    case 0: return launch_b16<128, 256, 4, 4, 64>(a, s);
-    case 1: return launch_b16<128, 64, 4, 2, 64>(a, s);
-    case 2: return launch_b16<256, 256, 4, 4, 64>(a, s);
-    case 3: return launch_b16<128, 128, 2, 2, 64>(a, s);
-    case 4: return launch_b16<128, 256, 4, 4, 32>(a, s);
-    case 5: return launch_b16<256, 128, 4, 4, 64>(a, s);
-    case 6: return launch_b16<256, 256, 2, 4, 64>(a, s);
-    case 7: return launch_b16<256, 256, 4, 2, 64>(a, s);
-    case 8: return launch_b16<256, 256, 4, 4, 32>(a, s);
-    case 9: return launch_b16<256, 256, 4, 4, 64, 1>(a, s);
-    case 10: return launch_b16<128, 256, 4, 4, 64, 1>(a, s);
-    case 11: return launch_b16<256, 256, 4, 4, 32, 1>(a, s);
-    case 12: return launch_b16<128, 128, 2, 2, 64, 1>(a, s);
-    case 13: return launch_b16<128, 128, 2, 2, 32, 2>(a, s);
-    case 14: return launch_b16<128, 256, 2, 4, 64, 1>(a, s);
-    case 15: return launch_b16<256, 128, 4, 2, 64, 1>(a, s);
-    default: return hipErrorInvalidValue;
-  }
-}
-
 // Weight relayout for the bf16 compress GEMM: W [K][ldw_in] fp32 (the fp32
 // compress layout) -> [n_pad][K] bf16, rows n >= N zero.
 __global__ void b16_weight_nk_kernel(const float* __restrict__ w, int ldw_in, int N, int K,

@@ -208,28 +208,4 @@ hipError_t gemm_f32(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-// Explicit configurations for tile sweeps (same numerics for every entry);
-// cfg >= 100 runs cfg - 100 without the XCD swizzle.
-hipError_t gemm_f32_sweep(int cfg, const GemmArgs& a, hipStream_t s) {
-  const int sw = cfg >= 100 ? 0 : 1;
-  switch (cfg % 100) {
-    case 0: return launch_cfg<128, 128, 2, 2, 16>(a, s, sw);
-    case 2: return launch_cfg<256, 128, 4, 2, 16>(a, s, sw);
-    case 3: return launch_cfg<128, 256, 2, 4, 16>(a, s, sw);
-    case 4: return launch_cfg<64, 64, 2, 2, 16>(a, s, sw);
-    case 7: return launch_cfg<32, 32, 2, 2, 32>(a, s, sw);
-    case 14: return launch_cfg<32, 32, 2, 2, 16>(a, s, sw);
-    case 15: return launch_cfg<64, 128, 2, 2, 16>(a, s, sw);
-    case 16: return launch_cfg<128, 128, 4, 4, 16>(a, s, sw);
-    case 17: return launch_cfg<128, 64, 4, 2, 16>(a, s, sw);
-    case 18: return launch_cfg<64, 64, 4, 4, 16>(a, s, sw);
-    case 19: return launch_cfg<256, 256, 4, 4, 16>(a, s, sw);
-    case 20: return launch_cfg<128, 256, 4, 4, 16>(a, s, sw);
-    case 21: return launch_cfg<32, 64, 2, 4, 16>(a, s, sw);
-    case 22: return launch_cfg<16, 64, 1, 4, 16>(a, s, sw);
-    case 23: return launch_cfg<32, 32, 2, 2, 8>(a, s, sw);
-    default: return hipErrorInvalidValue;
-  }
-}
-
 }  // namespace boa

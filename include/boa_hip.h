@@ -76,6 +76,28 @@ int boa_set_temperature(boa_ctx* ctx, float temperature);
  * zero state. */
 int boa_set_warm_start(boa_ctx* ctx, int32_t interleave_batch);
 
+/* Progress reports, the callback form of print_progress (boa.cpp:30-50,
+ * called per batch at :410 and :688).  fn(user, phase, done, total) is
+ * called on the calling thread during boa_compress_* (phase 0) and
+ * boa_decompress_* (phase 1) with input bytes done and the call's total:
+ * per compress tile and batch, and every 2048 decode steps and per batch,
+ * each report once the device has finished that work.  NULL turns the
+ * reports off (the default); without a callback no synchronisation is
+ * added. */
+typedef void (*boa_progress_fn)(void* user, int32_t phase, int64_t done_bytes, int64_t total_bytes);
+int boa_set_progress(boa_ctx* ctx, boa_progress_fn fn, void* user);
+
+/* Decode-step plan (no reference counterpart; a diagnostic of this build's
+ * schedule for `lanes` lanes): how many layers keep their recurrent state in
+ * the caches (the rest stream it past them), whether LayerNorm runs fused
+ * into in_proj and FF1, and whether one persistent kernel runs the whole
+ * batch.  boa_set_state_cache_budget sets the bytes of decode state kept in
+ * the caches (< 0 restores the default, 160 MiB), which changes only the
+ * cache policy of the state accesses, never the results. */
+int boa_decode_plan(const boa_ctx* ctx, int32_t lanes, int32_t* cached_layers, int32_t* fused_ln,
+                    int32_t* persistent);
+int boa_set_state_cache_budget(boa_ctx* ctx, int64_t bytes);
+
 /* Weights in the convert_boa_weights.py layout: "BOA\0" fp32, "BOA\1" fp16 or
  * headerless fp32.  Replaces BoaPredictorGPU::load_weights
  * (boa_gpu.hpp:990-1029); unlike the reference the file size is validated
@@ -161,6 +183,11 @@ int boa_compress_buffer(boa_ctx* ctx, const uint8_t* h_in, int64_t n, int64_t ch
 /* Decompress a BOA2 container; replaces decompress_v2 (boa.cpp:584-817). */
 int boa_decompress_buffer(boa_ctx* ctx, const uint8_t* h_in, int64_t n, uint8_t** h_out,
                           int64_t* out_len);
+/* Wall-clock phases of the last boa_compress_buffer / boa_decompress_buffer
+ * (and so of the file calls): host-to-device copy, device work, device-to-
+ * host copy, in seconds -- the H2D / Compute / D2H of boa.cpp's
+ * --show-timings line (boa.cpp:504-507). */
+int boa_last_timings(const boa_ctx* ctx, double* h2d_s, double* compute_s, double* d2h_s);
 int boa_compress_file(boa_ctx* ctx, const char* in_path, const char* out_path, int64_t chunk_size,
                       int32_t max_chunks);
 int boa_decompress_file(boa_ctx* ctx, const char* in_path, const char* out_path);
@@ -178,8 +205,10 @@ uint32_t boa_crc32(const uint8_t* data, int64_t n);
 #define BOA_K_CDF 4
 #define BOA_K_CODER 5
 #define BOA_K_DECODE 6
-#define BOA_K_GEMM_SMALL 7 /* GEMMs on the smaller tiles (x_proj, decode) */
-#define BOA_K_COUNT 8
+#define BOA_K_GEMM_SMALL 7 /* compress GEMMs on the smaller tile (x_proj) */
+#define BOA_K_DEC_GEMM 8   /* decode-step GEMMs (LayerNorm-fused ones included) */
+#define BOA_K_DEC_SCAN 9   /* decode-step scan */
+#define BOA_K_COUNT 10
 /* When enabled, every kernel launch is bracketed by HIP events recorded on
  * the launch stream; boa_profile_read synchronises and returns, for a
  * kernel class, the summed kernel time (ms), the launch count and the
