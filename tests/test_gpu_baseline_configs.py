@@ -17,8 +17,9 @@ of a chunk subset are within 0.5 % of the oracle's bf16 restatement; logits
 of a lane subset are within 2e-2 of the logit scale of the fp32 oracle (the
 reference CPU path's precision) and of the bf16 oracle.  Each case also
 checks which decode schedule ran (boa_decode_plan): C2 keeps 4 of 8
-layers' state in the caches and streams the rest, C3-C5 stream every
-layer, C4 runs the unfused-LayerNorm step above 2048 lanes.
+layers' state in the caches and streams the rest, C4 keeps one (its 160 MiB
+of state per layer fills the budget exactly) and runs the unfused-LayerNorm
+step above 2048 lanes, C3 and C5 stream every layer.
 """
 import numpy as np
 import pytest
@@ -87,7 +88,7 @@ def test_fp32_configs_container_equals_oracle(torch_dev, oracle, make_weights, n
     if name == "c2":
         assert 0 < cached < 8 and fused, "C2: first layers cached, the rest streamed, LN fused"
     else:
-        assert cached == 0 and not fused, "C4: every layer streamed, separate LayerNorm kernels"
+        assert cached <= 1 and not fused, "C4: (all but) every layer streamed, separate LayerNorms"
     blob = c.compress(data, chunk_size=chunk)
     want = oracle.Model(w, 256, 8).compress(data, chunk_size=chunk)
     assert blob == want, f"{name}: container differs ({len(blob)} vs {len(want)} bytes)"
