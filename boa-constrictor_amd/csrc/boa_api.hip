@@ -574,11 +574,18 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
       if (!e)
         e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
     }
-    if (!e) e = dgemm(c, cvt, DW.w_x, rows, ld, nullptr, nullptr, lanes, c->n_xdec, D.di, ACT_NONE);
-    if (!e)
+    if (!e && dec_xscan_fits(D)) {  // x_proj inside the scan kernel
       e = timed(c, BOA_K_DEC_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
-        return launch_dec_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, cached, s);
+        return launch_dec_xscan(D, W, DW.na, DW.w_dt, DW.w_x, (int)round_up(c->n_xdec, 16), zt, cvt,
+                                ssm, yt, lanes, ld, ld, cached, s);
       });
+    } else if (!e) {
+      e = dgemm(c, cvt, DW.w_x, rows, ld, nullptr, nullptr, lanes, c->n_xdec, D.di, ACT_NONE);
+      if (!e)
+        e = timed(c, BOA_K_DEC_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
+          return launch_dec_scan(D, W, DW.na, DW.w_dt, zt, cvt, rows, ssm, yt, lanes, ld, ld, cached, s);
+        });
+    }
     if (!e) e = dgemm(c, yt, DW.w_out, ot, ld, W.b_out, nullptr, lanes, D.d, D.di, ACT_NONE);
     if (!e && fuse_ln) {  // LN2 in front of FF1, in one kernel
       DecGemmArgs f{};

@@ -149,6 +149,13 @@ hipError_t launch_dec_ln1(const float* emb, const uint8_t* tok, float* xt, float
                           hipStream_t s);
 hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const float* b, int M, int d,
                           int ld, hipStream_t s);
+// x_proj fused with the decode scan (dec_xscan_kernel); same results as
+// dec_gemm (x_proj) + launch_dec_scan
+bool dec_xscan_fits(const Dims& D);
+hipError_t launch_dec_xscan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
+                            const float* w_x, int ldw_x, const float* zt, const float* cvt,
+                            float* ssm, float* yt, int M, int ld, int ld_state, bool state_cached,
+                            hipStream_t s);
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
                            const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
                            int M, int ld, int ld_state, bool state_cached, hipStream_t s);

@@ -740,6 +740,138 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
               make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), CACHED);
 }
 
+// ------------------------------------------------ x_proj fused with the scan
+// dec_xscan_kernel runs x_proj and the scan of one layer in one launch.  A
+// block of 1024 threads owns 16 lanes x 128 channels:
+//   1. every thread issues the loads of its first channel's SSM state;
+//   2. waves 0 .. NB-1 each run one 16-feature block of the lanes' x_proj
+//      row (dt_in, B, C; K = di) as dec_gemm_kernel's wave does -- the same
+//      K-ordered fma chain, then + 0 as the bias-free epilogue -- and store
+//      it to LDS in natural feature order (position 4g + v of a lane's
+//      float4 is feature 4v + g of its block);
+//   3. after the block's only barrier, each thread runs the scan of its lane
+//      for two channels (c and c + 64) in turn, reading dt_in, B and C from
+//      LDS (the 16 channel threads of a lane read the same words).
+// x_proj is recomputed by the di / 128 blocks of a 16-lane tile (4 at
+// d_model 256) instead of being stored and reloaded, which removes a launch
+// and the rows' round trip per layer; the bits are those of dec_gemm +
+// dec_scan_kernel.  d_state 16 and d_model <= 256 only (larger shapes keep
+// the two kernels: their state, decay and dt_proj registers do not fit
+// 1024 threads).
+template <int DS, int RB, int DI, bool CACHED>
+__global__ __launch_bounds__(1024) void dec_xscan_kernel(LayerW Lw, const float* __restrict__ na_q,
+                                                         const float* __restrict__ wdt_q,
+                                                         const float* __restrict__ w_x, int ldw_x,
+                                                         const float* __restrict__ zt,
+                                                         const float* __restrict__ cvt,
+                                                         float* ssm, float* yt, int M, int ld,
+                                                         int ld_state, int r) {
+  constexpr int NB = (RB + 2 * DS + 15) / 16;  // 16-feature blocks of the x_proj row
+  constexpr int CB = DI / 128;                 // 128-channel blocks per 16-lane tile
+  constexpr int RS = NB * 16 + 4;              // LDS row stride (floats, 16-byte aligned)
+  static_assert(NB <= 16 && DI % 128 == 0, "one wave per x_proj feature block");
+  __shared__ __align__(16) float rown[16 * RS];
+  const int tid = threadIdx.x;
+  const XcdSlot blk = xcd_slot(blockIdx.x, 4 * CB);  // 4 16-lane tiles x CB channel blocks
+  const int cb = blk.j % CB;
+  const int m0 = blk.grp * 64 + (blk.j / CB) * 16;
+  if (m0 >= M) return;  // the whole block, before the barrier
+  const int cl = tid & 15, lm = (tid >> 4) & 15, q = tid >> 8;
+  const int m = m0 + lm;
+  const int mc = min(m, M - 1);  // lanes past M load a valid row and store nothing
+  float4* h4 = reinterpret_cast<float4*>(ssm);
+  // 1. the first channel's state (16-channel block 8 cb + q)
+  float h0[DS];
+  {
+    const int c16 = 8 * cb + q;
+#pragma unroll
+    for (int n4 = 0; n4 < DS / 4; ++n4) {
+      const float4 hv = state_ld4(h4 + ((size_t)(c16 * (DS / 4) + n4) * ld_state + mc) * 16 + cl, CACHED);
+      h0[4 * n4] = hv.x; h0[4 * n4 + 1] = hv.y; h0[4 * n4 + 2] = hv.z; h0[4 * n4 + 3] = hv.w;
+    }
+  }
+  // 2. x_proj: wave w < NB computes feature block w for lanes m0 .. m0 + 15
+  const int wv = tid >> 6;
+  if (wv < NB) {
+    const int lane = tid & 63, i = lane & 15, g = lane >> 4;
+    DecGemmArgs a{};
+    a.Xt = cvt; a.ldx = ld; a.W = w_x; a.ldw = ldw_x; a.M = M; a.N = NB * 16; a.K = DI;
+    floatx4 acc[1][1];
+    dec_mainloop<DI / 4, 1, 1, 1, 4>(a, 16 * wv, m0, i, g, acc);
+#pragma unroll
+    for (int v = 0; v < 4; ++v)  // the bias-free epilogue of dec_gemm_kernel: acc + 0
+      rown[i * RS + 16 * wv + 4 * v + g] = acc[0][0][v] + 0.0f;
+  }
+  __syncthreads();
+  if (m >= M) return;  // after the block's only barrier
+  const float* row = rown + lm * RS;
+  const float4* na4 = reinterpret_cast<const float4*>(na_q);
+  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
+  // 3. channels c and c + 64 of the lane, one after the other
+#pragma unroll 1
+  for (int p = 0; p < 2; ++p) {
+    const int c16 = 8 * cb + q + 4 * p;
+    const int c = 16 * c16 + cl;
+    ScanCtx<DS, RB> sc;
+    if (p == 0) {
+#pragma unroll
+      for (int n = 0; n < DS; ++n) sc.h[n] = h0[n];
+    } else {
+#pragma unroll
+      for (int n4 = 0; n4 < DS / 4; ++n4) {
+        const float4 hv = state_ld4(h4 + ((size_t)(c16 * (DS / 4) + n4) * ld_state + m) * 16 + cl, CACHED);
+        sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
+      }
+    }
+#pragma unroll
+    for (int n4 = 0; n4 < DS / 4; ++n4) {
+      const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + cl];
+      sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
+    }
+#pragma unroll
+    for (int j4 = 0; j4 < RB / 4; ++j4) {
+      const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + cl];
+      sc.wdt[4 * j4] = wv4.x; sc.wdt[4 * j4 + 1] = wv4.y; sc.wdt[4 * j4 + 2] = wv4.z; sc.wdt[4 * j4 + 3] = wv4.w;
+    }
+    sc.bdt = Lw.b_dt[c];
+    sc.dd = Lw.dd[c];
+    const size_t cm = dblk(c, m, ld);
+    const float u = cvt[cm];
+    const float z = zt[cm];
+    yt[cm] = scan_token<DS, RB, MATH_BR>(sc, row, row + RB, r, u, z);
+#pragma unroll
+    for (int n4 = 0; n4 < DS / 4; ++n4)
+      state_st4(h4 + ((size_t)(c16 * (DS / 4) + n4) * ld_state + m) * 16 + cl,
+                make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), CACHED);
+  }
+}
+
+bool dec_xscan_fits(const Dims& D) {
+  const int rb = dec_rb(D.r);
+  return D.ds == 16 && ((D.di == 128 && rb == 8) || (D.di == 256 && rb == 8) ||
+                        (D.di == 512 && rb == 16));
+}
+
+hipError_t launch_dec_xscan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
+                            const float* w_x, int ldw_x, const float* zt, const float* cvt,
+                            float* ssm, float* yt, int M, int ld, int ld_state, bool state_cached,
+                            hipStream_t s) {
+  if (!dec_xscan_fits(D) || ldw_x < dec_rb(D.r) + 2 * D.ds || ld < M) return hipErrorInvalidValue;
+  const dim3 grid(xcd_grid(M, 4 * (D.di / 128))), block(1024);
+#define BOA_XSCAN(RBv, DIv)                                                                       \
+  if (state_cached)                                                                               \
+    hipLaunchKernelGGL((dec_xscan_kernel<16, RBv, DIv, true>), grid, block, 0, s, Lw, na_q, wdt_q,  \
+                       w_x, ldw_x, zt, cvt, ssm, yt, M, ld, ld_state, D.r);                        \
+  else                                                                                            \
+    hipLaunchKernelGGL((dec_xscan_kernel<16, RBv, DIv, false>), grid, block, 0, s, Lw, na_q, wdt_q, \
+                       w_x, ldw_x, zt, cvt, ssm, yt, M, ld, ld_state, D.r)
+  if (D.di == 128) BOA_XSCAN(8, 128);
+  else if (D.di == 256) BOA_XSCAN(8, 256);
+  else BOA_XSCAN(16, 512);
+#undef BOA_XSCAN
+  return hipGetLastError();
+}
+
 hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, const float* wdt_q,
                            const float* zt, const float* cvt, const float* rows, float* ssm, float* yt,
                            int M, int ld, int ld_state, bool state_cached, hipStream_t s) {
