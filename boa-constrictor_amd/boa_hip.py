@@ -86,6 +86,7 @@ def lib():
             "boa_reset_state": (C.c_int, [P, i32]),
             "boa_forward_chunk": (C.c_int, [P, P, i32, i32, P]),
             "boa_step_batch": (C.c_int, [P, P, i32, P, i32]),
+            "boa_forward_chunk_noalloc": (C.c_int, [P, P, i32, i32, P]),
             "boa_cdf_from_logits": (C.c_int, [P, P, P, i32, P]),
             "boa_cdf_from_probs": (C.c_int, [P, P, i32, i32, P]),
             "boa_rc_encode_cdf": (C.c_int, [P, P, P, i32, i32, P, i64, P]),
@@ -161,6 +162,12 @@ class Codec:
     def forward_chunk(self, d_tokens, lanes, T, d_logits):
         self._check(lib().boa_forward_chunk(self.h, _ptr(d_tokens), lanes, T, _ptr(d_logits)),
                     "forward_chunk")
+
+    def forward_chunk_noalloc(self, d_tokens, lanes, T, d_logits):
+        """boa_forward_chunk with its activations in the library's fixed
+        per-GPU scratch array (no device allocation during the call)."""
+        self._check(lib().boa_forward_chunk_noalloc(self.h, _ptr(d_tokens), lanes, T,
+                                                    _ptr(d_logits)), "forward_chunk_noalloc")
 
     def step_batch(self, d_tokens, lanes, d_logits, add_bias=True):
         self._check(lib().boa_step_batch(self.h, _ptr(d_tokens), lanes, _ptr(d_logits),

@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -40,6 +41,17 @@ struct ProfRec {
   hipEvent_t a, b;
   double work;
 };
+
+// Scratch of the allocation-free entry point (boa_forward_chunk_noalloc):
+// one fixed array per GPU, held until the process ends.  Host code never
+// uses the array's name as an address: boa_create looks up each device's
+// own address once (hipGetSymbolAddress, with that device current) and the
+// entry point passes that pointer on.  Calls on one GPU share the array.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int kScratchDevices = 64;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
 
 }  // namespace
 
@@ -138,6 +150,9 @@ struct boa_ctx {
   void* progress_user = nullptr;
   hipEvent_t prog_ev[2] = {nullptr, nullptr};
   int64_t prog_base = 0, prog_total = 0;  // bytes done before this batch, bytes of the call
+
+  // this device's scratch array (boa_forward_chunk_noalloc), or null
+  unsigned char* scratch = nullptr;
 
   // wall-clock phases of the last buffer call: H2D, device work, D2H (s)
   double t_h2d = 0, t_compute = 0, t_d2h = 0;
@@ -877,6 +892,22 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
       (cfg->precision != 0 && cfg->precision != 1) || cfg->tile < 0)
     return BOA_E_ARG;
   boa_ctx* c = new boa_ctx();
+  {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { delete c; return BOA_E_HIP; }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (dev >= 0 && dev < kScratchDevices) {
+      if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+          delete c;
+          return BOA_E_HIP;
+        }
+        g_scratch_ptr[dev] = p;
+      }
+      c->scratch = (unsigned char*)g_scratch_ptr[dev];
+    }
+  }
   c->cfg = *cfg;
   if (!(c->cfg.temperature > 0.0f)) c->cfg.temperature = 1.0f;
   c->inv_temp = 1.0f / c->cfg.temperature;
@@ -1247,6 +1278,56 @@ int boa_forward_chunk(boa_ctx* c, const uint8_t* d_tokens, int32_t lanes, int32_
   if ((rc = ensure_rows(c, (int64_t)lanes * T))) return rc;
   TokenSrc tok{d_tokens, T, (int64_t)lanes * T, T};
   HIP_TRY(c, forward_tile(c, tok, lanes, T, 0, d_logits));
+  return BOA_OK;
+}
+
+// Rows (lanes x T) that the scratch array holds: the seven activation
+// buffers of a forward (x, xn [d]; xz [2 di]; conv, y [di]; delta [R];
+// hidden [4 d] floats per row), each slice aligned to 256 bytes.
+static int64_t noalloc_max_rows(const Dims& D) {
+  const int64_t per_row = 4 * (int64_t)(14 * D.d + D.R);
+  return ((int64_t)kScratchBytes - 7 * 256) / per_row;
+}
+
+int boa_forward_chunk_noalloc(boa_ctx* c, const uint8_t* d_tokens, int32_t lanes, int32_t T,
+                              float* d_logits) {
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (!d_tokens || !d_logits || lanes < 1 || lanes > c->cfg.max_lanes || T < 1)
+    return fail(c, BOA_E_ARG, "boa_forward_chunk_noalloc: bad arguments");
+  if (!c->scratch) return fail(c, BOA_E_STATE, "boa_forward_chunk_noalloc: no scratch on this device");
+  const Dims& D = c->D;
+  const int64_t rows = (int64_t)lanes * T, max_rows = noalloc_max_rows(D);
+  if (rows > max_rows) {
+    char msg[200];
+    snprintf(msg, sizeof msg,
+             "boa_forward_chunk_noalloc: lanes x T = %lld rows exceeds the %lld rows its %zu-byte "
+             "scratch holds at d_model %d",
+             (long long)rows, (long long)max_rows, kScratchBytes, D.d);
+    return fail(c, BOA_E_ARG, msg);
+  }
+  // carve the scratch into the activation buffers of this call
+  unsigned char* at = c->scratch;
+  auto take = [&](int64_t floats) {
+    float* p = (float*)at;
+    at += round_up(floats * 4, 256);
+    return p;
+  };
+  float *x = take(rows * D.d), *xn = take(rows * D.d), *xz = take(rows * 2 * D.di),
+        *cv = take(rows * D.di), *delta = take(rows * D.R), *y = take(rows * D.di),
+        *hid = take(rows * 4 * D.d);
+  // the context's own buffers step aside for the call; profiling (which
+  // creates events) is off during it
+  float* saved[7] = {c->x, c->xn, c->xz, c->cv, c->delta, c->y, c->hid};
+  const bool prof = c->prof_on;
+  c->x = x; c->xn = xn; c->xz = xz; c->cv = cv; c->delta = delta; c->y = y; c->hid = hid;
+  c->prof_on = false;
+  TokenSrc tok{d_tokens, T, rows, T};
+  hipError_t e = forward_tile(c, tok, lanes, T, 0, d_logits);
+  c->x = saved[0]; c->xn = saved[1]; c->xz = saved[2]; c->cv = saved[3]; c->delta = saved[4];
+  c->y = saved[5]; c->hid = saved[6];
+  c->prof_on = prof;
+  if (e) return hip_fail(c, e, "boa_forward_chunk_noalloc");
   return BOA_OK;
 }
 

@@ -120,6 +120,21 @@ int boa_reset_state(boa_ctx* ctx, int32_t lanes);
  * Replaces BoaPredictorGPU::forward_chunk (boa_gpu.hpp:1081-1102). */
 int boa_forward_chunk(boa_ctx* ctx, const uint8_t* d_tokens, int32_t lanes, int32_t T,
                       float* d_logits);
+/* Allocation-free variant of boa_forward_chunk (no counterpart in the
+ * reference).  For callers that cannot allocate device memory during the
+ * call: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Same inputs, outputs, state and results as
+ * boa_forward_chunk, but the activations live in a fixed 64 MiB scratch
+ * array per GPU (held until the process ends) instead of buffers the
+ * context grows on demand; the call makes no hipMalloc, hipFree or other
+ * allocating call.  Limit: lanes x T <= (64 MiB - 1792) / (4 (14 d_model +
+ * ceil(d_model/16) + 2 d_state)) rows (4619 at d_model 256, d_state 16);
+ * larger requests fail with BOA_E_ARG.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (two host threads, or
+ * two streams) race, so serialise them.  HIP-event profiling is off during
+ * the call. */
+int boa_forward_chunk_noalloc(boa_ctx* ctx, const uint8_t* d_tokens, int32_t lanes, int32_t T,
+                              float* d_logits);
 /* One decode step for every lane: d_tokens [lanes] -> d_logits [lanes][256];
  * add_bias = 0 leaves head.2's bias out as the decoder's call does.
  * Replaces BoaPredictorGPU::step_batch (boa_gpu.hpp:1034-1053). */
