@@ -887,9 +887,13 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
   if (!cfg || !out) return BOA_E_ARG;
   *out = nullptr;
   const int d = cfg->d_model;
-  if ((d != 64 && d != 128 && d != 256 && d != 512) || cfg->n_layers < 1 ||
-      (cfg->d_state != 16 && cfg->d_state != 32) || cfg->max_lanes < 1 || cfg->max_lanes > 65535 ||
-      (cfg->precision != 0 && cfg->precision != 1) || cfg->tile < 0)
+  // d_model: the shapes the kernels are built for (80: the reference's
+  // ..._mambav1_80_1_20.pt checkpoint); bf16 needs K in multiples of 64
+  const bool d_ok = d == 64 || d == 80 || d == 128 || d == 256 || d == 512;
+  if (!d_ok || cfg->n_layers < 1 || (cfg->d_state != 16 && cfg->d_state != 32) ||
+      cfg->max_lanes < 1 || cfg->max_lanes > 65535 ||
+      (cfg->precision != 0 && cfg->precision != 1) || (cfg->precision == 1 && d % 64) ||
+      cfg->tile < 0)
     return BOA_E_ARG;
   boa_ctx* c = new boa_ctx();
   {

@@ -204,12 +204,15 @@ hipError_t dec_launch(const DecGemmArgs& a, hipStream_t s) {
   const dim3 grid(TM == 1 && TN == 1 ? xcd_grid(a.M, (a.N + 15) / 16) : (tiles + 3) / 4), block(256);
   switch (a.K) {
     case 64: hipLaunchKernelGGL((dec_gemm_kernel<16, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 80: hipLaunchKernelGGL((dec_gemm_kernel<20, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 160: hipLaunchKernelGGL((dec_gemm_kernel<40, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 320: hipLaunchKernelGGL((dec_gemm_kernel<80, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     case 128: hipLaunchKernelGGL((dec_gemm_kernel<32, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     case 256: hipLaunchKernelGGL((dec_gemm_kernel<64, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     case 512: hipLaunchKernelGGL((dec_gemm_kernel<128, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     case 1024: hipLaunchKernelGGL((dec_gemm_kernel<256, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     case 2048: hipLaunchKernelGGL((dec_gemm_kernel<512, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    default: return hipErrorInvalidValue;  // decode needs d_model a power of two >= 64
+    default: return hipErrorInvalidValue;  // K = d, 2d or 4d of a supported d_model
   }
   return hipGetLastError();
 }
@@ -640,10 +643,11 @@ hipError_t dec_ln_launch(const float* emb, const uint8_t* tok, float* xt, const 
                        xt, src, xnt, w, b, M, ld, t_counter);
   switch (d) {
     case 64: BOA_DEC_LN(4) break;
+    case 80: BOA_DEC_LN(5) break;
     case 128: BOA_DEC_LN(8) break;
     case 256: BOA_DEC_LN(16) break;
     case 512: BOA_DEC_LN(32) break;
-    default: return hipErrorInvalidValue;  // decode needs d_model in {64, 128, 256, 512}
+    default: return hipErrorInvalidValue;  // decode needs d_model in {64, 80, 128, 256, 512}
   }
 #undef BOA_DEC_LN
   return hipGetLastError();

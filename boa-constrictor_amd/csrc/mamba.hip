@@ -43,7 +43,8 @@ __device__ __forceinline__ void st4(uint16_t* p, const float* v) {
 
 // LN1: 8 rows per 256-thread block; half-wave h sums row h as the
 // reference's warp-per-row reduction does: lane l accumulates elements l,
-// l+32, ... in order, then the shuffle-down tree 16, 8, 4, 2, 1, lane 0's
+// l+32, ... (those below D) in order, then the shuffle-down tree 16, 8, 4,
+// 2, 1, lane 0's
 // totals broadcast.  Layer 0 gathers the embedding rows of the tile's
 // tokens and also stores them as x.
 template <typename TO, int D>
@@ -83,10 +84,13 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
   float* row = tile + h * S;
   float sum = 0.0f, sq = 0.0f;
 #pragma unroll
-  for (int e = 0; e < D / 32; ++e) {
-    const float v = row[l + 32 * e];
-    sum = sum + v;
-    sq = sq + v * v;
+  for (int e = 0; e < (D + 31) / 32; ++e) {
+    const int idx = l + 32 * e;
+    if (D % 32 == 0 || idx < D) {
+      const float v = row[idx];
+      sum = sum + v;
+      sq = sq + v * v;
+    }
   }
 #pragma unroll
   for (int off = 16; off > 0; off >>= 1) {
@@ -99,9 +103,9 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
   const float var = sq / (float)D - mean * mean;
   const float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
 #pragma unroll
-  for (int e = 0; e < D / 32; ++e) {
+  for (int e = 0; e < (D + 31) / 32; ++e) {
     const int idx = l + 32 * e;
-    row[idx] = ((row[idx] - mean) * inv_std) * w[idx] + b[idx];
+    if (D % 32 == 0 || idx < D) row[idx] = ((row[idx] - mean) * inv_std) * w[idx] + b[idx];
   }
   __syncthreads();
 #pragma unroll
@@ -124,6 +128,7 @@ hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, v
                        (float*)xn, w, b, rows);
   switch (d) {
     case 64: BOA_LN1(64) break;
+    case 80: BOA_LN1(80) break;
     case 128: BOA_LN1(128) break;
     case 256: BOA_LN1(256) break;
     case 512: BOA_LN1(512) break;
@@ -207,6 +212,7 @@ hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, 
   }
   switch (d) {
     case 64: BOA_LN2(64) break;
+    case 80: BOA_LN2(80) break;
     case 128: BOA_LN2(128) break;
     case 256: BOA_LN2(256) break;
     case 512: BOA_LN2(512) break;

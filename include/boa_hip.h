@@ -42,7 +42,7 @@ typedef struct boa_ctx boa_ctx;
  * --temperature CLI state of boa.cpp:838-897.  d_conv = 4 and expand = 2 are
  * fixed as in the reference; dt_rank = ceil(d_model / 16). */
 typedef struct {
-    int32_t d_model;     /* 64, 128, 256 or 512 */
+    int32_t d_model;     /* 64, 80, 128, 256 or 512 (bf16: not 80) */
     int32_t n_layers;
     int32_t d_state;     /* 16 or 32 (the reference supports 16 only) */
     int32_t max_lanes;   /* chunks processed in parallel (--gpu-batch) */

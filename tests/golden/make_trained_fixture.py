@@ -32,6 +32,11 @@ import synth  # noqa: E402
 CKPT = ("/root/reference/experiments/cms_experiment/"
         "cms_experiment_final_model_fp32_mambav1_64_2_20ep.pt")
 WEIGHTS = "trained_mambav1_64_2_fp16.bin"
+# the reference's d_model-80 checkpoint (one layer; dt_rank 5): a shape
+# whose d_model is not a power of two
+CKPT80 = ("/root/reference/experiments/cms_experiment/"
+          "cms_experiment_final_model_fp32_mambav1_80_1_20.pt")
+WEIGHTS80 = "trained_mambav1_80_1_fp16.bin"
 
 
 def inputs():
@@ -65,6 +70,23 @@ def main():
         manifest["containers"][name] = dict(n=len(data), chunk=chunk, bytes=len(blob),
                                             ratio=round(len(data) / len(blob), 4),
                                             sha256=hashlib.sha256(blob).hexdigest())
+    # d_model 80: its weights and one container of the config-1 input
+    w80 = os.path.join(HERE, WEIGHTS80)
+    info80 = convert_weights.convert(CKPT80, w80, fp16=True)
+    assert (info80["d_model"], info80["n_layers"]) == (80, 1), info80
+    with open(w80, "rb") as f:
+        wb80 = f.read()
+    m80 = refcpu.Model(w80, 80, 1)
+    data80, chunk80 = synth.gen_c1()[:8 * 1024], 1024
+    blob80 = m80.compress(data80, chunk_size=chunk80)
+    assert m80.decompress(blob80) == data80
+    with open(os.path.join(HERE, "trained80_c1_8x1024.boa"), "wb") as f:
+        f.write(blob80)
+    manifest["d_model_80"] = {
+        "checkpoint": os.path.basename(CKPT80),
+        "weights": dict(file=WEIGHTS80, bytes=len(wb80), sha256=hashlib.sha256(wb80).hexdigest()),
+        "container": dict(file="trained80_c1_8x1024.boa", n=len(data80), chunk=chunk80,
+                          bytes=len(blob80), sha256=hashlib.sha256(blob80).hexdigest())}
     with open(os.path.join(HERE, "trained_manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1)
     print(json.dumps(manifest, indent=1))

@@ -34,7 +34,7 @@ def _codec(d, L, ds=16, lanes=64, tile=0, w=None, temperature=1.0):
     return c
 
 
-@pytest.mark.parametrize("d,L,ds", [(128, 1, 16), (256, 2, 16), (512, 1, 32)])
+@pytest.mark.parametrize("d,L,ds", [(80, 2, 16), (128, 1, 16), (256, 2, 16), (512, 1, 32)])
 def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
     """Chunk-mode logits equal the oracle's; step-mode logits equal chunk mode."""
     torch = torch_dev
@@ -81,6 +81,13 @@ def test_container_c2_shape(torch_dev, oracle, make_weights):
 def test_container_c5_shape_d_state_32(torch_dev, oracle, make_weights):
     data = synth.gen_c5(2048)[:5 * 512 + 77]
     _same_container(oracle, make_weights(512, 1, 32), 512, 1, 32, data, 512, lanes=6)
+
+
+def test_container_d_model_80(torch_dev, oracle, make_weights):
+    """d_model 80 (dt_rank 5), the shape of the reference's
+    ..._mambav1_80_1_20.pt, with two layers and ragged chunks."""
+    data = synth.gen_c1()[:7 * 600 + 41]
+    _same_container(oracle, make_weights(80, 2), 80, 2, 16, data, 600, lanes=5)
 
 
 def test_container_markov_source(torch_dev, oracle, w_c1):

@@ -58,6 +58,29 @@ def test_trained_model_containers(oracle, name):
     c.close()
 
 
+def test_trained_d_model_80(oracle):
+    """The reference's d_model-80 checkpoint (..._mambav1_80_1_20.pt, one
+    layer, dt_rank 5): a d_model that is not a power of two."""
+    import synth
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a visible MI355X"
+    spec = MANIFEST["d_model_80"]
+    w80 = os.path.join(GOLD, spec["weights"]["file"])
+    raw = open(w80, "rb").read()
+    assert hashlib.sha256(raw).hexdigest() == spec["weights"]["sha256"]
+    cs = spec["container"]
+    data = synth.gen_c1()[:cs["n"]]
+    gold = open(os.path.join(GOLD, cs["file"]), "rb").read()
+    c = boa_hip.Codec(80, 1, 16, 8)
+    c.set_stream(torch.cuda.current_stream().cuda_stream)
+    c.load_weights(w80)
+    blob = c.compress(data, chunk_size=cs["chunk"])
+    assert blob == gold
+    assert blob == oracle.Model(w80, 80, 1).compress(data, chunk_size=cs["chunk"])
+    assert c.decompress(blob) == data
+    c.close()
+
+
 def test_cli_auto_batch(oracle, w_c1, tmp_path):
     """--gpu-batch 0 sizes the batch from free memory (auto_size_params,
     boa.cpp:109-156) and still writes the oracle's container."""
