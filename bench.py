@@ -359,7 +359,7 @@ def main() -> int:
         log("decode-step kernel profile (32 directly launched steps)")
         lanes = n_chunks
         dec = decode_step_profile(codec, lanes)
-        cached, fused, persistent = codec.decode_plan(lanes)
+        plan = codec.decode_plan(lanes)
         if "dec_gemm" in dec:
             dg = dec["dec_gemm"]
             tf = dg["work_per_step"] / (dg["us_per_step"] * 1e-6) / 1e12
@@ -378,7 +378,7 @@ def main() -> int:
                 launches_per_step=ds_["launches_per_step"], us_per_step=round(ds_["us_per_step"], 1),
                 bytes_per_lane_layer=f"8*di*ds + {2 if prec == 'bf16' else 4}*(3*di + R)")
         dec = {"lanes": lanes, "steps": 32, "launch": "direct (HIP events per kernel)",
-               "cached_layers": cached, "fused_layernorm": fused, "persistent": persistent,
+               "plan": plan,
                "kernel_us_per_step": {k: round(v["us_per_step"], 2) for k, v in dec.items()}}
 
     # The dominant kernel class of a step: its share of the measured round

@@ -423,7 +423,7 @@ hipError_t head_forward(boa_ctx* c, int rows, bool add_bias, float* logits) {
 
 hipError_t ensure_state_layout(boa_ctx* c, int want_step);
 
-hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0, float* logits) {
+hipError_t blocks_forward(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0) {
   const int rows = lanes * T;
   hipError_t es = ensure_state_layout(c, 0);
   if (es) return es;
@@ -432,7 +432,30 @@ hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t
                            : block_forward(c, l, rows, lanes, T, tok, t0);
     if (e) return e;
   }
-  return head_forward(c, rows, true, logits);
+  return hipSuccess;
+}
+
+hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0, float* logits) {
+  hipError_t e = blocks_forward(c, tok, lanes, T, t0);
+  return e ? e : head_forward(c, lanes * T, true, logits);
+}
+
+// A compress tile up to the coder's input (fp32): the blocks, head.1, then
+// head.2 fused with the CDF, which writes each row's (low, prob) of the next
+// byte to c->lowprob without storing the logits.
+hipError_t forward_tile_cdf(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0) {
+  const Dims& D = c->D;
+  const int rows = lanes * T;
+  hipError_t e = blocks_forward(c, tok, lanes, T, t0);
+  if (!e)
+    e = gemm(c, c->x, D.d, c->hw1, D.ld_h1, c->xn, D.d, c->hb1, nullptr, 0, rows, D.d, D.d,
+             ACT_RELU);
+  if (e) return e;
+  GemmArgs a{c->xn, D.d, c->hw2, D.ld_h2, nullptr, 0, c->hb2, nullptr, 0, rows, VOCAB, D.d,
+             ACT_NONE};
+  CdfEpi ce{tok.base, tok.stride, tok.total, tok.len, T, t0, c->inv_temp, c->lowprob};
+  return timed(c, BOA_K_HEAD_CDF, 2.0 * rows * VOCAB * D.d,
+               [&] { return gemm_f32_head_cdf(a, ce, c->stream); });
 }
 
 float* dec_conv_of(boa_ctx* c, int l) {
@@ -501,6 +524,20 @@ bool dec_fuse_ln(const boa_ctx* c, int lanes) {
   return lanes <= 2048 && dec_ln_gemm_fits(D.d, 2 * D.di) && dec_ln_gemm_fits(D.d, 4 * D.d);
 }
 
+// x_proj fused into the scan kernel up to 2048 lanes (its x_proj is
+// recomputed by the 4 channel blocks of a lane tile); above that the
+// separate x_proj GEMM is faster (MI355X, C2 probe at 1000 lanes: decode
+// 1.806 -> 1.852 MB/s fused; C4 probe at 4096 lanes: 2.673 -> 2.527 fused).
+bool dec_fuse_xproj(const boa_ctx* c, int lanes) {
+  return lanes <= 2048 && dec_xscan_fits(c->D);
+}
+
+// head.2 fused with the coder step from 2048 lanes on: its 16-lane blocks
+// (one per 16 lanes) fill the CUs only there (MI355X: C2 probe at 1000 lanes
+// 1.865 MB/s apart against 1.852 fused; C4 probe at 4096 lanes 2.514
+// apart against 2.527 fused).
+bool dec_fuse_head(int lanes) { return lanes >= 2048; }
+
 // Grow-only device buffer: reallocated only when a call needs more.
 template <class T>
 hipError_t ensure_buf(T** p, int64_t* cap, int64_t need) {
@@ -550,8 +587,10 @@ hipError_t progress_mark(boa_ctx* c, int phase, int64_t done_prev, int64_t total
 hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
                           const uint8_t* tok, bool add_bias, float* logits);
 
+// with_head2 = false stops after head.1 (its output in the k-blocked dot
+// buffer): the decode loop runs head.2 fused with the coder step.
 hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_counter,
-                      const uint8_t* tok, bool add_bias, float* logits) {
+                      const uint8_t* tok, bool add_bias, float* logits, bool with_head2 = true) {
   if (c->bf16) return step_range_b16(c, lane0, lanes, s, t_counter, tok, add_bias, logits);
   const Dims& D = c->D;
   const int ld = c->ld_dec;
@@ -589,7 +628,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
       if (!e)
         e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
     }
-    if (!e && dec_xscan_fits(D)) {  // x_proj inside the scan kernel
+    if (!e && dec_fuse_xproj(c, lanes)) {  // x_proj inside the scan kernel
       e = timed(c, BOA_K_DEC_SCAN, 8.0 * lanes * D.di * D.ds + 4.0 * lanes * (3.0 * D.di + D.R), [&] {
         return launch_dec_xscan(D, W, DW.na, DW.w_dt, DW.w_x, (int)round_up(c->n_xdec, 16), zt, cvt,
                                 ssm, yt, lanes, ld, ld, cached, s);
@@ -617,7 +656,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     if (!e) e = dgemm(c, hidt, DW.w2, xt, ld, W.b2, xt, lanes, D.d, 4 * D.d, ACT_NONE);
   }
   if (!e) e = dgemm(c, xt, c->dhw1, ot, ld, c->hb1, nullptr, lanes, D.d, D.d, ACT_RELU);
-  if (!e)
+  if (!e && with_head2)
     e = dgemm(c, ot, c->dhw2, logits, VOCAB, add_bias ? c->hb2 : nullptr, nullptr, lanes, VOCAB,
               D.d, ACT_NONE, 1);
   c->stream = saved;
@@ -791,15 +830,30 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
     return timed(c, BOA_K_DECODE, 1024.0 * lanes * (maxlen - 1),
                  [&] { return launch_dec_persist(p, D.d, D.ds, s); });
   }
+  // fp32 from 2048 lanes on: head.2 runs fused with the coder step
+  // (dec_head_step_kernel), so the logits stay on chip; below that, and in
+  // bf16, head.2 and the coder step are separate launches
+  const bool fuse_head = !c->bf16 && dec_fuse_head(lanes);
   auto one_step = [&](hipStream_t gs) -> hipError_t {
-    hipError_t e = step_range(c, 0, lanes, gs, c->t_counter, c->tok, false, c->dlogits);
+    hipError_t e =
+        step_range(c, 0, lanes, gs, c->t_counter, c->tok, false, c->dlogits, !fuse_head);
     if (e) return e;
     hipStream_t saved = c->stream;
     c->stream = gs;
-    e = timed(c, BOA_K_DECODE, 1024.0 * lanes, [&] {
-      return launch_decode_step(c->dlogits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter, out,
-                                chunk, c->dec, d_payload, c->offsets, c->sizes, lanes, gs);
-    });
+    if (fuse_head) {
+      DecGemmArgs h{};
+      h.Xt = c->dot; h.ldx = c->ld_dec; h.W = c->dhw2; h.ldw = VOCAB; h.M = lanes; h.N = VOCAB;
+      h.K = D.d; h.act = ACT_NONE; h.row_major = 1;
+      e = timed(c, BOA_K_DECODE, 2.0 * lanes * VOCAB * D.d, [&] {
+        return launch_dec_head_step(h, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter, out,
+                                    chunk, c->dec, d_payload, c->offsets, c->sizes, gs);
+      });
+    } else {
+      e = timed(c, BOA_K_DECODE, 1024.0 * lanes, [&] {
+        return launch_decode_step(c->dlogits, c->hb2, c->inv_temp, c->tok, c->lens, c->t_counter,
+                                  out, chunk, c->dec, d_payload, c->offsets, c->sizes, lanes, gs);
+      });
+    }
     c->stream = saved;
     return e;
   };
@@ -1005,14 +1059,17 @@ int boa_set_state_cache_budget(boa_ctx* c, int64_t bytes) {
   return BOA_OK;
 }
 
-int boa_decode_plan(const boa_ctx* c, int32_t lanes, int32_t* cached_layers, int32_t* fused_ln,
-                    int32_t* persistent) {
+int boa_decode_plan(const boa_ctx* c, int32_t lanes, int32_t* cached_layers, int32_t* flags) {
   if (!c || lanes < 1 || lanes > c->cfg.max_lanes) return BOA_E_ARG;
   const Dims& D = c->D;
   const bool pers = !c->bf16 && dec_persist_fits(D.d, D.ds, D.r, D.L);
+  const bool chain32 = !pers && !c->bf16;
   if (cached_layers) *cached_layers = pers ? D.L : dec_cached_layers(c, lanes);
-  if (fused_ln) *fused_ln = (!pers && !c->bf16 && dec_fuse_ln(c, lanes)) ? 1 : 0;
-  if (persistent) *persistent = pers ? 1 : 0;
+  if (flags)
+    *flags = (chain32 && dec_fuse_ln(c, lanes) ? BOA_PLAN_FUSED_LN : 0) |
+             (pers ? BOA_PLAN_PERSISTENT : 0) |
+             (chain32 && dec_fuse_xproj(c, lanes) ? BOA_PLAN_FUSED_XPROJ : 0) |
+             (chain32 && dec_fuse_head(lanes) ? BOA_PLAN_FUSED_HEAD : 0);
   return BOA_OK;
 }
 
@@ -1449,12 +1506,16 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
       int slot = 0;
       for (int64_t t0 = 0; t0 < chunk; t0 += T) {
         const int Tt = (int)std::min<int64_t>(T, chunk - t0);
-        e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
-        if (!e)
-          e = timed(c, BOA_K_CDF, 1032.0 * lanes * Tt, [&] {
-            return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
-                                             c->lowprob, s);
-          });
+        if (c->bf16) {  // bf16: head.2 stores the logits, the CDF kernel reads them
+          e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
+          if (!e)
+            e = timed(c, BOA_K_CDF, 1032.0 * lanes * Tt, [&] {
+              return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
+                                               c->lowprob, s);
+            });
+        } else {
+          e = forward_tile_cdf(c, tok, lanes, Tt, (int)t0);
+        }
         if (!e)
           e = timed(c, BOA_K_CODER, 8.0 * lanes * Tt, [&] {
             return launch_rc_encode_tile(c->lowprob, tok, Tt, (int)t0, lanes, c->enc, c->words,

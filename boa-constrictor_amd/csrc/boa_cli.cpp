@@ -162,11 +162,12 @@ int main(int argc, char** argv) {
          nbytes / (1024.0 * 1024.0) / (sec > 0 ? sec : 1));
   if (show_timings) {
     // H2D / Compute / D2H as boa.cpp:504-507; Forward and Encode are the
-    // summed kernel times of the model and of the CDF + coder kernels
+    // summed kernel times of the model (head.2 + CDF included where they run
+    // fused) and of the CDF and coder kernels
     double h2d = 0, comp = 0, d2h = 0, fwd = 0, enc = 0;
     boa_last_timings(ctx, &h2d, &comp, &d2h);
     const int fwd_k[] = {BOA_K_GEMM, BOA_K_SCAN, BOA_K_CONV, BOA_K_LN, BOA_K_GEMM_SMALL,
-                         BOA_K_DEC_GEMM, BOA_K_DEC_SCAN};
+                         BOA_K_DEC_GEMM, BOA_K_DEC_SCAN, BOA_K_HEAD_CDF};
     const int enc_k[] = {BOA_K_CDF, BOA_K_CODER, BOA_K_DECODE};
     for (int k : fwd_k) { double ms = 0; boa_profile_read(ctx, k, &ms, nullptr, nullptr); fwd += ms * 1e-3; }
     for (int k : enc_k) { double ms = 0; boa_profile_read(ctx, k, &ms, nullptr, nullptr); enc += ms * 1e-3; }

@@ -36,6 +36,16 @@ struct GemmArgs {
   int M, N, K, act;
 };
 hipError_t gemm_f32(const GemmArgs& a, hipStream_t s);
+// the CDF epilogue's inputs: the tile's tokens, the row -> (lane, position)
+// map (row = lane * T + t, position t0 + t) and the temperature
+struct CdfEpi {
+  const uint8_t* tok_base;  // see TokenSrc
+  int64_t tok_stride, tok_total, tok_len;
+  int T, t0;
+  float inv_t;
+  uint2* lowprob;           // [M] (low, prob) of the next byte per row
+};
+hipError_t gemm_f32_head_cdf(const GemmArgs& a, const CdfEpi& cdf, hipStream_t s);
 // Tile configuration gemm_f32 picks: 0 = 128x256 (bulk GEMMs of a compress
 // tile), 1 = 128x64 (narrow compress GEMMs), 2 = 32x32 (decode-step sizes).
 int gemm_f32_config(const GemmArgs& a);
@@ -239,6 +249,13 @@ hipError_t launch_gather_streams(const uint32_t* src, const uint64_t* src_off,
                                  uint32_t* dst, hipStream_t s);
 hipError_t launch_rc_dec_init(RcDec* st, const uint32_t* payload, const uint64_t* offsets_words,
                               const int32_t* sizes_words, int lanes, hipStream_t s);
+// head.2 (a: Xt = head.1 output, W = head.2 decode weights, N = 256, no
+// bias, row-major) fused with launch_decode_step; same results as the two
+hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, float inv_temp,
+                                uint8_t* tok, const int32_t* lens, const int* t_counter,
+                                uint8_t* out, int64_t out_stride, RcDec* st,
+                                const uint32_t* payload, const uint64_t* offsets_words,
+                                const int32_t* sizes_words, hipStream_t s);
 hipError_t launch_decode_step(const float* logits, const float* head_b2, float inv_temp,
                               uint8_t* tok, const int32_t* lens, const int* t_counter,
                               uint8_t* out, int64_t out_stride, RcDec* st, const uint32_t* payload,

@@ -308,24 +308,9 @@ __global__ __launch_bounds__(256) void decode_step_kernel(
   }
   __syncthreads();
   if (!active) return;  // no barrier follows
-  const uint32_t target = s_target[half];
-  const double* sc = s_cdf[half];
-  int sym = 0;
-  uint32_t low_s = 0, high_s = 0;
-  const int shift = (threadIdx.x & 32);
-  for (int round = 0; round < 8; ++round) {
-    const int k = round * 32 + l;
-    const uint32_t lo = q_low(sc, k), hi = q_high(sc, k);
-    const bool match = target >= lo && target < hi;
-    const uint32_t mask = (uint32_t)(__ballot(match) >> shift);
-    if (mask != 0u) {
-      const int winner = __ffs(mask) - 1;
-      sym = __shfl(k, winner, 32);
-      low_s = __shfl(lo, winner, 32);
-      high_s = __shfl(hi, winner, 32);
-      break;
-    }
-  }
+  int sym;
+  uint32_t low_s, high_s;
+  cdf_search_halfwave(s_cdf[half], s_target[half], l, sym, low_s, high_s);
   if (l == 0) {
     const uint32_t* in = payload + offsets_words[b];
     dec_advance(st, low_s, high_s, in, sizes_words[b]);

@@ -193,4 +193,29 @@ __device__ __forceinline__ uint32_t q_high(const double* s_cdf, int k) {
   return k == 255 ? TOTAL : (uint32_t)(s_cdf[k + 1] * CDF_SCALE) + (uint32_t)(k + 1);
 }
 
+// The decoder's symbol search on a half-wave (range_coder_kernels.cu:594-610):
+// the first symbol k whose integer interval [low_k, high_k) holds the
+// coder target, in 8 rounds of 32 candidates, ballot + first set bit; the
+// result is broadcast to the half-wave.
+__device__ __forceinline__ void cdf_search_halfwave(const double* s_cdf, uint32_t target, int l,
+                                                    int& sym, uint32_t& low_s, uint32_t& high_s) {
+  sym = 0;
+  low_s = 0;
+  high_s = 0;
+  const int shift = (threadIdx.x & 32);
+  for (int round = 0; round < 8; ++round) {
+    const int k = round * 32 + l;
+    const uint32_t lo = q_low(s_cdf, k), hi = q_high(s_cdf, k);
+    const bool match = target >= lo && target < hi;
+    const uint32_t mask = (uint32_t)(__ballot(match) >> shift);
+    if (mask != 0u) {
+      const int winner = __ffs(mask) - 1;
+      sym = __shfl(k, winner, 32);
+      low_s = __shfl(lo, winner, 32);
+      high_s = __shfl(hi, winner, 32);
+      return;
+    }
+  }
+}
+
 }  // namespace boa

@@ -21,6 +21,7 @@
 // chain, so decode logits are bit-identical to the compress logits.
 #include "block_device.h"
 #include "boa_kernels.h"
+#include "coder_device.h"
 
 namespace boa {
 
@@ -246,6 +247,92 @@ hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
   if (a.K <= 256 && a.N >= 1024) cfg = 10;
   else if (a.M >= 2048 && a.N >= 256) cfg = a.K >= 512 ? 9 : 13;
   return dec_gemm_cfg(a, cfg, s);
+}
+
+// ----------------------------------------- head.2 fused with the decode step
+// dec_head_step_kernel: head.2 (the 256 logits of a lane, no bias, K = d),
+// the CDF (head.2's bias added, temperature), the symbol search and the
+// coder advance in one launch, so the logits never leave the CU
+// (boa_gpu.hpp:1049-1052 followed by range_coder_kernels.cu:504-627).  A
+// block of 1024 threads owns 16 lanes: wave w computes logits 16w .. 16w+15
+// of the 16 lanes as dec_gemm_kernel's wave does (the same K-ordered fma
+// chain, + 0 as its bias-free epilogue) into LDS; then half-wave h of waves
+// 0-7 runs decode_step_kernel's work for lane h.  Same bits as
+// dec_gemm (head.2) + decode_step_kernel.
+template <int KS>
+__global__ __launch_bounds__(1024) void dec_head_step_kernel(
+    DecGemmArgs a, const float* __restrict__ head_b2, float inv_t, uint8_t* tok,
+    const int32_t* __restrict__ lens, const int* __restrict__ t_counter, uint8_t* out,
+    int64_t out_stride, RcDec* states, const uint32_t* __restrict__ payload,
+    const uint64_t* __restrict__ offsets_words, const int32_t* __restrict__ sizes_words) {
+  constexpr int LS = 256 + 4;  // LDS logits row stride
+  __shared__ __align__(16) float lg[16 * LS];
+  __shared__ double s_cdf[16][260];
+  __shared__ uint32_t s_target[16];
+  const int tid = threadIdx.x;
+  const XcdSlot blk = xcd_slot(blockIdx.x, 4);  // 4 16-lane tiles per 64-lane group
+  const int m0 = blk.grp * 64 + blk.j * 16;
+  if (m0 >= a.M) return;  // the whole block, before any barrier
+  const int wv = tid >> 6, lane = tid & 63, i = lane & 15, g = lane >> 4;
+  {
+    floatx4 acc[1][1];
+    dec_mainloop<KS, 1, 1, 1, 8>(a, 16 * wv, m0, i, g, acc);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) lg[i * LS + 16 * wv + 4 * g + v] = acc[0][0][v] + 0.0f;
+  }
+  __syncthreads();
+  const int h = tid >> 5, l = tid & 31;  // half-waves 0-15 (waves 0-7) own lanes m0 + h
+  const int b = m0 + h;
+  const bool mine = h < 16;
+  const int t = *t_counter;
+  const bool active = mine && b < a.M && t < lens[b < a.M ? b : a.M - 1];
+  RcDec st;
+  if (mine) {
+    double r[8];
+    cdf_halfwave_regs(lg + h * LS, head_b2, inv_t, l, r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_cdf[h][8 * l + e] = r[e];
+    if (l == 31) s_cdf[h][256] = 1.0;
+    if (active && l == 0) {
+      st = states[b];
+      s_target[h] = dec_target(st);
+    }
+  }
+  __syncthreads();
+  if (!active) return;  // no barrier follows
+  int sym;
+  uint32_t low_s, high_s;
+  cdf_search_halfwave(s_cdf[h], s_target[h], l, sym, low_s, high_s);
+  if (l == 0) {
+    dec_advance(st, low_s, high_s, payload + offsets_words[b], sizes_words[b]);
+    states[b] = st;
+    out[(size_t)b * out_stride + t] = (uint8_t)sym;
+    tok[b] = (uint8_t)sym;
+  }
+}
+
+hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, float inv_temp,
+                                uint8_t* tok, const int32_t* lens, const int* t_counter,
+                                uint8_t* out, int64_t out_stride, RcDec* st,
+                                const uint32_t* payload, const uint64_t* offsets_words,
+                                const int32_t* sizes_words, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.N != 256 || a.ldw < 256 || a.ldx < a.M || a.row_major != 1 || a.bias)
+    return hipErrorInvalidValue;
+  const dim3 grid(xcd_grid(a.M, 4)), block(1024);
+#define BOA_HEADSTEP(KSv)                                                                     \
+  hipLaunchKernelGGL((dec_head_step_kernel<KSv>), grid, block, 0, s, a, head_b2, inv_temp, tok, \
+                     lens, t_counter, out, out_stride, st, payload, offsets_words, sizes_words)
+  switch (a.K) {
+    case 64: BOA_HEADSTEP(16); break;
+    case 80: BOA_HEADSTEP(20); break;
+    case 128: BOA_HEADSTEP(32); break;
+    case 256: BOA_HEADSTEP(64); break;
+    case 512: BOA_HEADSTEP(128); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef BOA_HEADSTEP
+  return hipGetLastError();
 }
 
 // ------------------------------------------------ LayerNorm + GEMM (K = d)

@@ -19,10 +19,16 @@
 // float4 per lane.  LDS: activations [BM][BK+4] (16-byte rows for b128
 // stores), weights [BK][BN+16]; both double-buffered, one barrier per K step.
 #include "boa_kernels.h"
+#include "coder_device.h"
 
 namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Epilogue mode of head.2 fused with the CDF (not a user activation): the
+// block's logits rows go to LDS, and each row's (low, prob) pair of the
+// next input byte is computed there (cdf_targets_kernel's work).
+constexpr int ACT_CDF = 3;
 
 // Eight waves per SIMD (64 VGPRs): two 16-wave blocks share a CU.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int ACT>
@@ -30,7 +36,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
 void gemm_f32_kernel(
     const float* __restrict__ X, int ldx, const float* __restrict__ W, int ldw, float* C, int ldc,
     const float* __restrict__ bias, const float* res, int ldr, int M, int N, int K,
-    int vec_store, int swizzle) {
+    int vec_store, int swizzle, CdfEpi cdf) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -39,8 +45,14 @@ void gemm_f32_kernel(
   constexpr int XQ = BM * (BK / 4), WQ = BK * (BN / 4);  // float4s per tile
   constexpr int XL = (XQ + NT - 1) / NT;  // float4 activation loads per thread
   constexpr int WL = (WQ + NT - 1) / NT;  // float4 weight loads per thread
-  __shared__ __attribute__((aligned(16))) float xs[2][BM * XS];
-  __shared__ __attribute__((aligned(16))) float ws[2][BK * WS];
+  // LDS: the K loop's double-buffered tiles; the CDF epilogue reuses the
+  // same words for the block's logits rows (stride LS)
+  constexpr int LS = BN + 4;
+  constexpr int MAIN = 2 * BM * XS + 2 * BK * WS;
+  constexpr int EPI = ACT == ACT_CDF ? BM * LS : 0;
+  __shared__ __attribute__((aligned(16))) float smem[MAIN > EPI ? MAIN : EPI];
+  float(*xs)[BM * XS] = reinterpret_cast<float(*)[BM * XS]>(smem);
+  float(*ws)[BK * WS] = reinterpret_cast<float(*)[BK * WS]>(smem + 2 * BM * XS);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -130,6 +142,42 @@ void gemm_f32_kernel(
     __syncthreads();
   }
 
+  if constexpr (ACT == ACT_CDF) {
+    // head.2 + bias into LDS (the K loop ended with a barrier, so the tile
+    // buffers are free), then per row the CDF of cdf_targets_kernel
+    static_assert(BN == 256, "one block holds whole logits rows");
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+      for (int b = 0; b < TN; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int col = wn0 + b * 16 + 4 * g + e;
+          smem[(wm0 + a * 16 + j) * LS + col] = acc[a][b][e] + sbias[col];
+        }
+    __syncthreads();
+    const int hw = tid >> 5, l = tid & 31;
+    for (int r = hw; r < BM; r += NT / 32) {
+      const int row = m_blk + r;
+      const int rr = row < M ? row : M - 1;
+      double cr[8];
+      cdf_halfwave_regs(smem + r * LS, nullptr, cdf.inv_t, l, cr);
+      // the byte after position t0 + t of lane b (0 past the chunk's end)
+      const int b = rr / cdf.T, t = rr % cdf.T;
+      const int64_t pic = (int64_t)cdf.t0 + t + 1;
+      const int64_t pos = (int64_t)b * cdf.tok_stride + pic;
+      const int sym = (pic < cdf.tok_len && pos < cdf.tok_total) ? cdf.tok_base[pos] : 0;
+      const double c_lo = cdf_entry(cr, sym);
+      const double c_hi = cdf_entry(cr, sym + 1 > 255 ? 255 : sym + 1);
+      if (row < M && l == 0) {
+        const uint32_t lo = (uint32_t)(c_lo * CDF_SCALE) + (uint32_t)sym;
+        const uint32_t hi = sym == 255 ? TOTAL : (uint32_t)(c_hi * CDF_SCALE) + (uint32_t)(sym + 1);
+        cdf.lowprob[row] = make_uint2(lo, hi - lo);
+      }
+    }
+    return;
+  }
+
   // Epilogue: lane owns C[m][n .. n+3], m = wm0 + a*16 + j, n = wn0 + b*16 + 4g.
 #pragma unroll
   for (int a = 0; a < TM; ++a) {
@@ -176,7 +224,7 @@ static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s, int swizzle = 1) 
 #define BOA_GEMM_GO(ACTv)                                                                     \
   hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM_, WN_, BK, ACTv>), dim3((unsigned)tiles),     \
                      dim3(64 * WM_ * WN_), 0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias,   \
-                     a.res, a.ldr, a.M, a.N, a.K, vec, swizzle)
+                     a.res, a.ldr, a.M, a.N, a.K, vec, swizzle, CdfEpi{})
   switch (a.act) {
     case ACT_NONE: BOA_GEMM_GO(ACT_NONE); break;
     case ACT_GELU: BOA_GEMM_GO(ACT_GELU); break;
@@ -195,6 +243,23 @@ static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s, int swizzle = 1) 
 int gemm_f32_config(const GemmArgs& a) {
   if (a.M >= 16384) return a.N >= 256 ? 0 : 1;
   return 2;
+}
+
+// head.2 of a compress tile fused with the CDF: rows of 256 logits (acc +
+// bias) stay in LDS and each row's (low, prob) of the next byte is written
+// to cdf.lowprob.  64-row blocks keep two blocks per CU (66.5 KB of LDS).
+hipError_t gemm_f32_head_cdf(const GemmArgs& a, const CdfEpi& cdf, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.N != 256 || a.K % 16 || a.ldx % 4 || a.ldw % 4 || !cdf.lowprob || cdf.T < 1)
+    return hipErrorInvalidValue;
+  constexpr int BM = 64, BN = 256;  // 128-row blocks (one per CU) measured the same
+  if (a.ldw < BN) return hipErrorInvalidValue;
+  const long long tiles = (a.M + BM - 1) / BM;
+  if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, 4, 4, 16, ACT_CDF>), dim3((unsigned)tiles), dim3(1024),
+                     0, s, a.X, a.ldx, a.W, a.ldw, nullptr, 0, a.bias, nullptr, 0, a.M, a.N, a.K,
+                     0, 1, cdf);
+  return hipGetLastError();
 }
 
 hipError_t gemm_f32(const GemmArgs& a, hipStream_t s) {

@@ -89,13 +89,17 @@ int boa_set_progress(boa_ctx* ctx, boa_progress_fn fn, void* user);
 
 /* Decode-step plan (no reference counterpart; a diagnostic of this build's
  * schedule for `lanes` lanes): how many layers keep their recurrent state in
- * the caches (the rest stream it past them), whether LayerNorm runs fused
- * into in_proj and FF1, and whether one persistent kernel runs the whole
- * batch.  boa_set_state_cache_budget sets the bytes of decode state kept in
- * the caches (< 0 restores the default, 160 MiB), which changes only the
- * cache policy of the state accesses, never the results. */
-int boa_decode_plan(const boa_ctx* ctx, int32_t lanes, int32_t* cached_layers, int32_t* fused_ln,
-                    int32_t* persistent);
+ * the caches (the rest stream it past them), and BOA_PLAN_* flags: LayerNorm
+ * fused into in_proj and FF1, one persistent kernel for the whole batch,
+ * x_proj fused into the scan, head.2 fused with the coder step.
+ * boa_set_state_cache_budget sets the bytes of decode state kept in the
+ * caches (< 0 restores the default, 160 MiB), which changes only the cache
+ * policy of the state accesses, never the results. */
+#define BOA_PLAN_FUSED_LN 1
+#define BOA_PLAN_PERSISTENT 2
+#define BOA_PLAN_FUSED_XPROJ 4
+#define BOA_PLAN_FUSED_HEAD 8
+int boa_decode_plan(const boa_ctx* ctx, int32_t lanes, int32_t* cached_layers, int32_t* flags);
 int boa_set_state_cache_budget(boa_ctx* ctx, int64_t bytes);
 
 /* Weights in the convert_boa_weights.py layout: "BOA\0" fp32, "BOA\1" fp16 or
@@ -219,11 +223,12 @@ uint32_t boa_crc32(const uint8_t* data, int64_t n);
 #define BOA_K_LN 3
 #define BOA_K_CDF 4
 #define BOA_K_CODER 5
-#define BOA_K_DECODE 6
+#define BOA_K_DECODE 6     /* decode coder step (fp32: head.2 fused in) */
 #define BOA_K_GEMM_SMALL 7 /* compress GEMMs on the smaller tile (x_proj) */
 #define BOA_K_DEC_GEMM 8   /* decode-step GEMMs (LayerNorm-fused ones included) */
 #define BOA_K_DEC_SCAN 9   /* decode-step scan */
-#define BOA_K_COUNT 10
+#define BOA_K_HEAD_CDF 10  /* compress head.2 fused with the CDF (fp32) */
+#define BOA_K_COUNT 11
 /* When enabled, every kernel launch is bracketed by HIP events recorded on
  * the launch stream; boa_profile_read synchronises and returns, for a
  * kernel class, the summed kernel time (ms), the launch count and the

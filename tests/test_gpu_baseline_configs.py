@@ -71,7 +71,7 @@ def test_c1_full_input_container(torch_dev, oracle, w_c1):
     data = synth.gen_c1()
     assert len(data) == 1 << 20
     c = _codec(64, 2, 16, 64, w=w_c1)
-    assert c.decode_plan(64)[2], "C1 decodes in the persistent kernel"
+    assert c.decode_plan(64)["persistent"], "C1 decodes in the persistent kernel"
     blob = c.compress(data, chunk_size=16384)
     want = oracle.Model(w_c1, 64, 2).compress(data, chunk_size=16384)
     assert blob == want, f"container differs ({len(blob)} vs {len(want)} bytes)"
@@ -83,12 +83,14 @@ def test_fp32_configs_container_equals_oracle(torch_dev, oracle, make_weights, n
     w = make_weights(256, 8)
     data = _config_input(name, lanes, chunk)
     c = _codec(256, 8, 16, lanes, w=w)
-    cached, fused, persistent = c.decode_plan(lanes)
-    assert not persistent
+    plan = c.decode_plan(lanes)
+    assert not plan["persistent"]
     if name == "c2":
-        assert 0 < cached < 8 and fused, "C2: first layers cached, the rest streamed, LN fused"
+        assert 0 < plan["cached_layers"] < 8, "C2: first layers cached, the rest streamed"
+        assert plan["fused_ln"] and plan["fused_xproj"] and not plan["fused_head"]
     else:
-        assert cached <= 1 and not fused, "C4: (all but) every layer streamed, separate LayerNorms"
+        assert plan["cached_layers"] <= 1, "C4: (all but) every layer streamed"
+        assert not plan["fused_ln"] and not plan["fused_xproj"] and plan["fused_head"]
     blob = c.compress(data, chunk_size=chunk)
     want = oracle.Model(w, 256, 8).compress(data, chunk_size=chunk)
     assert blob == want, f"{name}: container differs ({len(blob)} vs {len(want)} bytes)"
@@ -105,7 +107,7 @@ def test_c2_decode_cache_policies_same_bytes(torch_dev, make_weights):
     blob = c.compress(data, chunk_size=24)
     for budget, want_cached in [(0, 0), (1 << 40, 8), (-1, None)]:
         c.set_state_cache_budget(budget)
-        cached = c.decode_plan(1000)[0]
+        cached = c.decode_plan(1000)["cached_layers"]
         if want_cached is not None:
             assert cached == want_cached
         assert c.decompress(blob) == data, f"budget {budget}"
@@ -115,8 +117,8 @@ def _bf16_case(torch, oracle, make_weights, d, L, ds, name, lanes, chunk, subset
     w = make_weights(d, L, ds)
     data = _config_input(name, lanes, chunk)
     c = _codec(d, L, ds, lanes, prec="bf16", w=w)
-    cached, fused, persistent = c.decode_plan(lanes)
-    assert cached == 0 and not persistent
+    plan = c.decode_plan(lanes)
+    assert plan["cached_layers"] == 0 and not plan["persistent"]
     blob = c.compress(data, chunk_size=chunk)
     assert c.decompress(blob) == data, f"{name}: bf16 round trip"
     # stream bytes of the first `subset` chunks against the oracle's bf16
