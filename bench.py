@@ -114,6 +114,9 @@ def decode_step_profile(codec, lanes: int, steps: int = 32) -> dict:
     torch.cuda.synchronize()
     codec.profile(True)
     codec.profile_reset()
+    # a GPU-side wait first, so that every step is queued before the GPU
+    # runs it: the events then time the GPU alone, not host launch gaps
+    gpu_hold(torch)
     for _ in range(steps):
         codec.step_batch(tok.data_ptr(), lanes, logits.data_ptr())
     torch.cuda.synchronize()
@@ -121,6 +124,11 @@ def decode_step_profile(codec, lanes: int, steps: int = 32) -> dict:
     codec.profile(False)
     return {k: dict(us_per_step=v["ms"] * 1e3 / steps, launches_per_step=v["launches"] / steps,
                     work_per_step=v["work"] / steps) for k, v in p.items() if v["launches"]}
+
+
+def gpu_hold(torch, ms: float = 60.0):
+    """Queue a GPU-side busy wait of about `ms` on the current stream."""
+    torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
 
 
 def cpu_info() -> dict:
@@ -330,74 +338,80 @@ def main() -> int:
     # per-class kernel times of the compress (HIP events on the launch stream)
     kernel_ms = {k: round(v["ms"], 3) for k, v in prof.items() if v["launches"]}
     g = prof["gemm"]
-    gemm_tf = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
     peak_mm = PEAK_TFLOPS[prec]
     gemm_launch_us = g["ms"] * 1e3 / max(g["launches"], 1)
-    roof_gemm = roofline_entry(GEMM_KERNEL[prec], "mfma", gemm_tf, peak_mm, "TFLOP/s",
-                               gemm_launch_us, g["work"] / max(g["launches"], 1), "flop_per_launch",
-                               traffic=gemm_traffic_bytes() if workload == "c2" else None,
-                               launches=g["launches"], class_ms_per_compress=round(g["ms"], 1))
     sc = prof["scan"]
-    scan_gbs = sc["work"] / (sc["ms"] * 1e-3) / 1e9 if sc["ms"] > 0 else 0.0
-    roof_scan = roofline_entry(
-        f"boa::scan_chunk_kernel<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>", "hbm",
-        scan_gbs, PEAK_HBM_GBS, "GB/s", sc["ms"] * 1e3 / max(sc["launches"], 1),
-        sc["work"] / max(sc["launches"], 1), "bytes_per_launch", launches=sc["launches"],
-        class_ms_per_compress=round(sc["ms"], 1))
-    cd_ = prof["cdf"]
-    cdf_gbs = cd_["work"] / (cd_["ms"] * 1e-3) / 1e9 if cd_["ms"] > 0 else 0.0
-    roof_coder = roofline_entry("boa::cdf_targets_kernel", "hbm", cdf_gbs, PEAK_HBM_GBS, "GB/s",
-                                cd_["ms"] * 1e3 / max(cd_["launches"], 1),
-                                cd_["work"] / max(cd_["launches"], 1), "bytes_per_launch",
-                                launches=cd_["launches"])
+    scan_kernel = f"boa::scan_chunk_kernel<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>"
 
-    # The decode step's kernels, timed with HIP events on directly launched
-    # steps (boa_step_batch) after the timed region.
+    # The decode step's kernels on directly launched steps (boa_step_batch)
+    # after the timed region, each launch timed by the HIP events its
+    # dispatch packet carries (hipExtLaunchKernelGGL: the kernel's own span,
+    # as rocprofv3 measures it).
     dec = None
-    roof_dec_gemm = roof_dec_scan = None
+    dec_cls = {}
     if not args.no_decompress:
         log("decode-step kernel profile (32 directly launched steps)")
         lanes = n_chunks
-        dec = decode_step_profile(codec, lanes)
+        prof_dec = decode_step_profile(codec, lanes)
         plan = codec.decode_plan(lanes)
-        if "dec_gemm" in dec:
-            dg = dec["dec_gemm"]
-            tf = dg["work_per_step"] / (dg["us_per_step"] * 1e-6) / 1e12
-            roof_dec_gemm = roofline_entry(
-                "boa::dec_ln_gemm_kernel / dec_gemm_kernel / dec_b16_gemm* (decode-step GEMMs)",
-                "mfma", tf, peak_mm, "TFLOP/s", dg["us_per_step"] / dg["launches_per_step"],
-                dg["work_per_step"] / dg["launches_per_step"], "flop_per_launch",
-                launches_per_step=dg["launches_per_step"], us_per_step=round(dg["us_per_step"], 1))
-        if "dec_scan" in dec:
-            ds_ = dec["dec_scan"]
-            gbs = ds_["work_per_step"] / (ds_["us_per_step"] * 1e-6) / 1e9
-            roof_dec_scan = roofline_entry(
-                f"boa::{'dec_b16_scan_kernel' if prec == 'bf16' else 'dec_scan_kernel'}", "hbm",
-                gbs, PEAK_HBM_GBS, "GB/s", ds_["us_per_step"] / ds_["launches_per_step"],
-                ds_["work_per_step"] / ds_["launches_per_step"], "bytes_per_launch",
-                launches_per_step=ds_["launches_per_step"], us_per_step=round(ds_["us_per_step"], 1),
-                bytes_per_lane_layer=f"8*di*ds + {2 if prec == 'bf16' else 4}*(3*di + R)")
-        dec = {"lanes": lanes, "steps": 32, "launch": "direct (HIP events per kernel)",
+        dec = {"lanes": lanes, "steps": 32, "launch": "direct, HIP events in each dispatch",
                "plan": plan,
-               "kernel_us_per_step": {k: round(v["us_per_step"], 2) for k, v in dec.items()}}
+               "kernel_us_per_step": {k: round(v["us_per_step"], 2) for k, v in prof_dec.items()}}
+        for k, v in prof_dec.items():
+            n_l = v["launches_per_step"]
+            dec_cls[k] = dict(avg_us=v["us_per_step"] / n_l, launches_per_step=n_l,
+                              work_per_launch=v["work_per_step"] / n_l)
 
-    # The dominant kernel class of a step: its share of the measured round
-    # trip (compress classes from the profiled pass, decode classes from the
-    # per-step profile times the steps of the decompress).
-    # (cold mode: one batch of n_chunks lanes runs chunk - 1 steps)
+    # Rooflines of the kernels that take most of a round trip; `roofline`
+    # is the one with the largest total time per step (compress: its
+    # launches in the profiled pass; decode: launches per step x the launch
+    # time x the chunk - 1 steps of the cold single-batch decode).  Every
+    # launch time comes from the HIP events in its dispatch packet.
     steps_per_dec = chunk - 1
-    shares = {"compress GEMM": (g["ms"] * 1e-3, roof_gemm),
-              "compress scan": (sc["ms"] * 1e-3, roof_scan)}
-    if roof_dec_gemm:
-        shares["decode GEMMs"] = (dec["kernel_us_per_step"]["dec_gemm"] * 1e-6 * steps_per_dec,
-                                  roof_dec_gemm)
-    if roof_dec_scan:
-        shares["decode scan"] = (dec["kernel_us_per_step"]["dec_scan"] * 1e-6 * steps_per_dec,
-                                 roof_dec_scan)
-    dom = max(shares, key=lambda k: shares[k][0])
-    roofline = dict(shares[dom][1])
+    cands = {}
+
+    def add(name, kernel, bound, work_per_launch, avg_us, launches_per_rt, unit_peak, **extra):
+        if avg_us <= 0 or launches_per_rt <= 0:
+            return
+        if bound == "mfma":
+            ach = work_per_launch / (avg_us * 1e-6) / 1e12
+            e = roofline_entry(kernel, "mfma", ach, unit_peak, "TFLOP/s", avg_us, work_per_launch,
+                               "flop_per_launch", **extra)
+        else:
+            ach = work_per_launch / (avg_us * 1e-6) / 1e9
+            e = roofline_entry(kernel, "hbm", ach, PEAK_HBM_GBS, "GB/s", avg_us, work_per_launch,
+                               "bytes_per_launch", **extra)
+        e["s_per_round_trip"] = round(avg_us * 1e-6 * launches_per_rt, 3)
+        e["launches_per_round_trip"] = round(launches_per_rt)
+        cands[name] = e
+
+    add("compress GEMM", GEMM_KERNEL[prec], "mfma", g["work"] / max(g["launches"], 1),
+        gemm_launch_us, g["launches"], peak_mm,
+        traffic=gemm_traffic_bytes() if workload == "c2" else None)
+    add("compress scan", scan_kernel, "hbm", sc["work"] / max(sc["launches"], 1),
+        sc["ms"] * 1e3 / max(sc["launches"], 1), sc["launches"], None)
+    hc, cd_ = prof["head_cdf"], prof["cdf"]
+    if hc["launches"]:
+        add("compress head.2 + CDF", "boa::gemm_f32_kernel<64, 256, 4, 4, 16, 3> (head.2 with the "
+            "CDF epilogue)", "mfma", hc["work"] / hc["launches"], hc["ms"] * 1e3 / hc["launches"],
+            hc["launches"], peak_mm)
+    if cd_["launches"]:
+        add("compress CDF", "boa::cdf_targets_kernel", "hbm", cd_["work"] / cd_["launches"],
+            cd_["ms"] * 1e3 / cd_["launches"], cd_["launches"], None)
+    kn = {"dec_lngemm": ("decode LayerNorm GEMMs", "boa::dec_ln_gemm_kernel<1|2, d/16, *> "
+                         "(LN1 + in_proj + conv, LN2 + FF1 + GELU)", "mfma"),
+          "dec_gemm": ("decode GEMMs", "boa::dec_gemm_kernel / dec_b16_gemm* (x_proj, out_proj, "
+                       "FF2, heads)", "mfma"),
+          "dec_scan": ("decode scan", "boa::dec_xscan_kernel / dec_scan_kernel / dec_b16_scan_kernel",
+                       "hbm")}
+    for k, (name, kernel, bound) in kn.items():
+        if k in dec_cls:
+            v = dec_cls[k]
+            add(name, kernel, bound, v["work_per_launch"], v["avg_us"],
+                v["launches_per_step"] * steps_per_dec, peak_mm)
+    dom = max(cands, key=lambda k: cands[k]["s_per_round_trip"])
+    roofline = dict(cands[dom])
     roofline["class"] = dom
-    roofline["class_s_per_step"] = round(shares[dom][0], 2)
 
     host = None
     if not args.no_host_path:
@@ -465,11 +479,7 @@ def main() -> int:
         "roundtrip_ok": ok_all,
         "compress_kernel_ms": kernel_ms,
         "roofline": roofline,
-        "roofline_compress_gemm": roof_gemm,
-        "roofline_scan": roof_scan,
-        "roofline_coder": roof_coder,
-        "roofline_decode_gemm": roof_dec_gemm,
-        "roofline_decode_scan": roof_dec_scan,
+        "rooflines": cands,
         "decode_step": dec,
         "host_path": host,
         "cpu_baseline": cpu,

@@ -20,9 +20,9 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "boa_hip.h")
 
 BOA_OK = 0
 (K_GEMM, K_SCAN, K_CONV, K_LN, K_CDF, K_CODER, K_DECODE, K_GEMM_SMALL, K_DEC_GEMM,
- K_DEC_SCAN, K_HEAD_CDF) = range(11)
+ K_DEC_SCAN, K_HEAD_CDF, K_DEC_LNGEMM) = range(12)
 K_NAMES = ["gemm", "scan", "conv", "ln", "cdf", "coder", "decode", "gemm_small", "dec_gemm",
-           "dec_scan", "head_cdf"]
+           "dec_scan", "head_cdf", "dec_lngemm"]
 BOA_E_ARG, BOA_E_HIP, BOA_E_IO, BOA_E_FORMAT, BOA_E_STATE, BOA_E_NOMEM = -1, -2, -3, -4, -5, -6
 
 # void (*)(void* user, int32_t phase, int64_t done_bytes, int64_t total_bytes)

@@ -26,6 +26,10 @@
 
 using namespace boa;
 
+namespace boa {
+thread_local LaunchTiming g_launch_timing;
+}
+
 namespace {
 
 constexpr int VOCAB = 256;
@@ -223,17 +227,24 @@ void prof_flush(boa_ctx* c) {
   c->recs.clear();
 }
 
+// With profiling on, the launches of f() carry a start / stop event pair in
+// their dispatch packets (BOA_LAUNCH): the recorded span is the kernels'
+// own, as rocprofv3 measures it, without marker packets between launches.
 template <class F>
 hipError_t timed(boa_ctx* c, int cls, double work, F&& f) {
   if (!c->prof_on) return f();
   hipEvent_t a = take_event(c), b = take_event(c);
   if (!a || !b) return hipErrorOutOfMemory;
-  hipError_t e = hipEventRecord(a, c->stream);
+  g_launch_timing = LaunchTiming{a, b, 0};
+  hipError_t e = f();
+  const int launched = g_launch_timing.launches;
+  g_launch_timing = LaunchTiming{};
   if (e != hipSuccess) return e;
-  e = f();
-  if (e != hipSuccess) return e;
-  e = hipEventRecord(b, c->stream);
-  if (e != hipSuccess) return e;
+  if (launched == 0) {  // nothing was launched (an empty call)
+    c->ev_pool.push_back(a);
+    c->ev_pool.push_back(b);
+    return hipSuccess;
+  }
   c->recs.push_back({cls, a, b, work});
   if (c->recs.size() >= 4096) prof_flush(c);
   return hipSuccess;
@@ -616,7 +627,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     a.conv_b = W.conv_b; a.conv_out = cvt;
     if (fuse_ln) {  // LN1 in front of in_proj, in one kernel
       a.Xt = xt;
-      e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * a.N * a.K, [&] {
+      e = timed(c, BOA_K_DEC_LNGEMM, 2.0 * lanes * a.N * a.K, [&] {
         return launch_dec_ln_gemm(1, a, l == 0 ? c->emb : nullptr, tok, xt, W.ln1_w, W.ln1_b,
                                   l == 0 ? t_counter : nullptr, s);
       });
@@ -645,7 +656,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
       DecGemmArgs f{};
       f.Xt = ot; f.ldx = ld; f.W = DW.w1; f.ldw = 4 * D.d; f.C = hidt; f.ldc = ld;
       f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU;
-      e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * f.N * f.K, [&] {
+      e = timed(c, BOA_K_DEC_LNGEMM, 2.0 * lanes * f.N * f.K, [&] {
         return launch_dec_ln_gemm(2, f, nullptr, nullptr, nullptr, W.ln2_w, W.ln2_b, nullptr, s);
       });
     } else if (!e) {
@@ -1187,7 +1198,7 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
     // -exp(A_log) log2(e) once per load (mamba_kernels.cu:430-437), on the device so
     // that it is the same exp the kernels use.
     const int nA = D.di * D.ds;
-    hipLaunchKernelGGL(na2_kernel, dim3((nA + 255) / 256), dim3(256), 0, c->stream,
+    BOA_LAUNCH(na2_kernel, dim3((nA + 255) / 256), dim3(256), 0, c->stream,
                        w + o.a_log, w + o.na2, nA);
     HIP_TRY(c, hipGetLastError());
   }
@@ -1480,7 +1491,7 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
   hipStream_t s = c->stream;
   if (ensure_buf(&c->first_buf, &c->first_cap, nc))
     return fail(c, BOA_E_NOMEM, "device allocation of the first-byte buffer failed");
-  hipLaunchKernelGGL(gather_first_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s,
+  BOA_LAUNCH(gather_first_kernel, dim3((unsigned)((nc + 255) / 256)), dim3(256), 0, s,
                      d_data, chunk, n, (int)nc, c->first_buf);
   hipError_t e = hipGetLastError();
   if (!e) e = hipMemcpyAsync(h_first, c->first_buf, (size_t)nc, hipMemcpyDeviceToHost, s);
@@ -1638,7 +1649,7 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       const int64_t c0 = warm ? u0 * S + i : u0;
       const int64_t stride = warm ? S * chunk : chunk;
       uint8_t* out = d_out + c0 * chunk;
-      hipLaunchKernelGGL(decode_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, d_first,
+      BOA_LAUNCH(decode_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, d_first,
                          c->lens, c->tok, out, stride, lanes, c->t_counter);
       e = hipGetLastError();
       if (!e) e = launch_rc_dec_init(c->dec, d_payload, c->offsets, c->sizes, lanes, s);

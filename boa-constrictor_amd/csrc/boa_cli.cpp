@@ -167,7 +167,7 @@ int main(int argc, char** argv) {
     double h2d = 0, comp = 0, d2h = 0, fwd = 0, enc = 0;
     boa_last_timings(ctx, &h2d, &comp, &d2h);
     const int fwd_k[] = {BOA_K_GEMM, BOA_K_SCAN, BOA_K_CONV, BOA_K_LN, BOA_K_GEMM_SMALL,
-                         BOA_K_DEC_GEMM, BOA_K_DEC_SCAN, BOA_K_HEAD_CDF};
+                         BOA_K_DEC_GEMM, BOA_K_DEC_SCAN, BOA_K_HEAD_CDF, BOA_K_DEC_LNGEMM};
     const int enc_k[] = {BOA_K_CDF, BOA_K_CODER, BOA_K_DECODE};
     for (int k : fwd_k) { double ms = 0; boa_profile_read(ctx, k, &ms, nullptr, nullptr); fwd += ms * 1e-3; }
     for (int k : enc_k) { double ms = 0; boa_profile_read(ctx, k, &ms, nullptr, nullptr); enc += ms * 1e-3; }

@@ -1,11 +1,37 @@
 // Kernel-level interface of the MI355X codec path (internal to the library).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "boa_math.h"
 
 namespace boa {
+
+// Per-launch timing for the host profiler: while `stop` is set, BOA_LAUNCH
+// passes the events to the dispatch itself (hipExtLaunchKernelGGL), so they
+// stamp the kernel's start and end without separate marker packets -- the
+// same span rocprofv3 reports.  The first launch of a profiled call takes
+// `start`, every launch `stop` (so a helper that launches two kernels is
+// timed from the first start to the last end).  Host-side state of the
+// calling thread; see timed() in boa_api.hip.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+  int launches = 0;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
+#define BOA_LAUNCH(K, GRID, BLOCK, SHM, STREAM, ...)                                         \
+  do {                                                                                       \
+    if (::boa::g_launch_timing.stop) {                                                       \
+      hipEvent_t boa_start_ =                                                                \
+          ::boa::g_launch_timing.launches++ == 0 ? ::boa::g_launch_timing.start : nullptr;   \
+      hipExtLaunchKernelGGL(K, dim3(GRID), dim3(BLOCK), (std::uint32_t)(SHM), STREAM,        \
+                            boa_start_, ::boa::g_launch_timing.stop, 0u, __VA_ARGS__);        \
+    } else {                                                                                 \
+      hipLaunchKernelGGL(K, GRID, BLOCK, SHM, STREAM, __VA_ARGS__);                          \
+    }                                                                                        \
+  } while (0)
 
 // Workgroups are dispatched to the 8 XCDs, each with its own L2, round-robin
 // by block index.  The decode step's kernels keep every 64-lane group on one

@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void cdf_targets_kernel(const float* __restric
 hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,
                                      float inv_temp, uint2* lowprob, hipStream_t s) {
   const int rows = lanes * T;
-  hipLaunchKernelGGL(cdf_targets_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, tok, T, t0,
+  BOA_LAUNCH(cdf_targets_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, tok, T, t0,
                      rows, inv_temp, lowprob);
   return hipGetLastError();
 }
@@ -109,13 +109,13 @@ __global__ void cdf_probs_kernel(const float* __restrict__ probs, int rows, int 
 
 hipError_t launch_cdf_probs(const float* probs, int rows, int K, uint32_t* out, hipStream_t s) {
   if (rows < 1 || K < 1 || K > 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(cdf_probs_kernel, dim3((rows + 63) / 64), dim3(64), 0, s, probs, rows, K, out);
+  BOA_LAUNCH(cdf_probs_kernel, dim3((rows + 63) / 64), dim3(64), 0, s, probs, rows, K, out);
   return hipGetLastError();
 }
 
 hipError_t launch_cdf_rows(const float* logits, const float* bias, float inv_temp, int rows,
                            uint32_t* qcdf, hipStream_t s) {
-  hipLaunchKernelGGL(cdf_rows_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, bias, inv_temp,
+  BOA_LAUNCH(cdf_rows_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, bias, inv_temp,
                      rows, qcdf);
   return hipGetLastError();
 }
@@ -131,7 +131,7 @@ __global__ void rc_enc_init_kernel(RcEnc* st, int lanes) {
 }
 
 hipError_t launch_rc_enc_init(RcEnc* st, int lanes, hipStream_t s) {
-  hipLaunchKernelGGL(rc_enc_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, lanes);
+  BOA_LAUNCH(rc_enc_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, lanes);
   return hipGetLastError();
 }
 
@@ -160,7 +160,7 @@ __global__ void rc_encode_tile_kernel(const uint2* __restrict__ lowprob, TokenSr
 
 hipError_t launch_rc_encode_tile(const uint2* lowprob, TokenSrc tok, int T, int t0, int lanes,
                                  RcEnc* st, uint32_t* out, int64_t pitch_words, hipStream_t s) {
-  hipLaunchKernelGGL(rc_encode_tile_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, lowprob, tok, T,
+  BOA_LAUNCH(rc_encode_tile_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, lowprob, tok, T,
                      t0, lanes, st, out, pitch_words);
   return hipGetLastError();
 }
@@ -176,7 +176,7 @@ __global__ void rc_finish_kernel(RcEnc* states, uint32_t* out, int64_t pitch_wor
 
 hipError_t launch_rc_finish(RcEnc* st, uint32_t* out, int64_t pitch_words, int32_t* sizes_words,
                             int lanes, hipStream_t s) {
-  hipLaunchKernelGGL(rc_finish_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, out,
+  BOA_LAUNCH(rc_finish_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, out,
                      pitch_words, sizes_words, lanes);
   return hipGetLastError();
 }
@@ -230,11 +230,11 @@ __global__ __launch_bounds__(256) void compact_kernel(const uint32_t* __restrict
 hipError_t launch_compact(const uint32_t* words, int64_t pitch_words, const int32_t* sizes_words,
                           int lanes, uint64_t* offsets_words, uint32_t* payload, hipStream_t s) {
   if (lanes <= 0) return hipSuccess;
-  hipLaunchKernelGGL(scan_sizes_kernel, dim3(1), dim3(1024), 0, s, sizes_words, lanes,
+  BOA_LAUNCH(scan_sizes_kernel, dim3(1), dim3(1024), 0, s, sizes_words, lanes,
                      offsets_words);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(compact_kernel, dim3(16, lanes), dim3(256), 0, s, words, pitch_words,
+  BOA_LAUNCH(compact_kernel, dim3(16, lanes), dim3(256), 0, s, words, pitch_words,
                      sizes_words, offsets_words, payload);
   return hipGetLastError();
 }
@@ -259,7 +259,7 @@ hipError_t launch_gather_streams(const uint32_t* src, const uint64_t* src_off,
                                  uint32_t* dst, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   const unsigned blocks = (unsigned)(n < 8192 ? n : 8192);
-  hipLaunchKernelGGL(gather_streams_kernel, dim3(blocks), dim3(256), 0, s, src, src_off, dst_off,
+  BOA_LAUNCH(gather_streams_kernel, dim3(blocks), dim3(256), 0, s, src, src_off, dst_off,
                      sizes, n, dst);
   return hipGetLastError();
 }
@@ -277,7 +277,7 @@ __global__ void rc_dec_init_kernel(RcDec* st, const uint32_t* payload,
 
 hipError_t launch_rc_dec_init(RcDec* st, const uint32_t* payload, const uint64_t* offsets_words,
                               const int32_t* sizes_words, int lanes, hipStream_t s) {
-  hipLaunchKernelGGL(rc_dec_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, payload,
+  BOA_LAUNCH(rc_dec_init_kernel, dim3((lanes + 255) / 256), dim3(256), 0, s, st, payload,
                      offsets_words, sizes_words, lanes);
   return hipGetLastError();
 }
@@ -325,7 +325,7 @@ hipError_t launch_decode_step(const float* logits, const float* head_b2, float i
                               uint8_t* out, int64_t out_stride, RcDec* st, const uint32_t* payload,
                               const uint64_t* offsets_words, const int32_t* sizes_words, int lanes,
                               hipStream_t s) {
-  hipLaunchKernelGGL(decode_step_kernel, dim3(xcd_grid(lanes, 8)), dim3(256), 0, s, logits, head_b2,
+  BOA_LAUNCH(decode_step_kernel, dim3(xcd_grid(lanes, 8)), dim3(256), 0, s, logits, head_b2,
                      inv_temp, tok, lens, t_counter, out, out_stride, st, payload, offsets_words,
                      sizes_words, lanes);
   return hipGetLastError();
@@ -352,7 +352,7 @@ __global__ void rc_encode_cdf_kernel(const uint32_t* __restrict__ cdf, const uin
 hipError_t launch_rc_encode_cdf(const uint32_t* cdf, const uint8_t* syms, int n_sym, int lanes,
                                 uint32_t* out, int64_t pitch_words, int32_t* sizes_words,
                                 hipStream_t s) {
-  hipLaunchKernelGGL(rc_encode_cdf_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, cdf, syms, n_sym,
+  BOA_LAUNCH(rc_encode_cdf_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, cdf, syms, n_sym,
                      lanes, out, pitch_words, sizes_words);
   return hipGetLastError();
 }
@@ -380,7 +380,7 @@ __global__ void rc_decode_cdf_kernel(const uint32_t* __restrict__ cdf, int n_sym
 hipError_t launch_rc_decode_cdf(const uint32_t* cdf, int n_sym, int lanes, const uint32_t* in,
                                 int64_t pitch_words, const int32_t* sizes_words, uint8_t* syms,
                                 hipStream_t s) {
-  hipLaunchKernelGGL(rc_decode_cdf_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, cdf, n_sym,
+  BOA_LAUNCH(rc_decode_cdf_kernel, dim3((lanes + 63) / 64), dim3(64), 0, s, cdf, n_sym,
                      lanes, in, pitch_words, sizes_words, syms);
   return hipGetLastError();
 }

@@ -204,15 +204,15 @@ hipError_t dec_launch(const DecGemmArgs& a, hipStream_t s) {
   const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
   const dim3 grid(TM == 1 && TN == 1 ? xcd_grid(a.M, (a.N + 15) / 16) : (tiles + 3) / 4), block(256);
   switch (a.K) {
-    case 64: hipLaunchKernelGGL((dec_gemm_kernel<16, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 80: hipLaunchKernelGGL((dec_gemm_kernel<20, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 160: hipLaunchKernelGGL((dec_gemm_kernel<40, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 320: hipLaunchKernelGGL((dec_gemm_kernel<80, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((dec_gemm_kernel<32, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 256: hipLaunchKernelGGL((dec_gemm_kernel<64, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 512: hipLaunchKernelGGL((dec_gemm_kernel<128, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 1024: hipLaunchKernelGGL((dec_gemm_kernel<256, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
-    case 2048: hipLaunchKernelGGL((dec_gemm_kernel<512, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_gemm_kernel<16, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 80: BOA_LAUNCH((dec_gemm_kernel<20, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 160: BOA_LAUNCH((dec_gemm_kernel<40, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 320: BOA_LAUNCH((dec_gemm_kernel<80, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_gemm_kernel<32, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_gemm_kernel<64, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_gemm_kernel<128, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_gemm_kernel<256, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_gemm_kernel<512, TM, TN, UQ, PD>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;  // K = d, 2d or 4d of a supported d_model
   }
   return hipGetLastError();
@@ -321,7 +321,7 @@ hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, floa
     return hipErrorInvalidValue;
   const dim3 grid(xcd_grid(a.M, 4)), block(1024);
 #define BOA_HEADSTEP(KSv)                                                                     \
-  hipLaunchKernelGGL((dec_head_step_kernel<KSv>), grid, block, 0, s, a, head_b2, inv_temp, tok, \
+  BOA_LAUNCH((dec_head_step_kernel<KSv>), grid, block, 0, s, a, head_b2, inv_temp, tok, \
                      lens, t_counter, out, out_stride, st, payload, offsets_words, sizes_words)
   switch (a.K) {
     case 64: BOA_HEADSTEP(16); break;
@@ -520,13 +520,13 @@ hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, 
   const dim3 grid(xcd_grid(a.M, a.N / 64)), block(1024);
 #define BOA_LNG(NBv)                                                                          \
   if (emb)                                                                                    \
-    hipLaunchKernelGGL((dec_ln_gemm_kernel<1, NBv, true>), grid, block, 0, s, a, emb, tok, xt,  \
+    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, true>), grid, block, 0, s, a, emb, tok, xt,  \
                        lw, lb, t_counter);                                                    \
   else if (mode == 1)                                                                         \
-    hipLaunchKernelGGL((dec_ln_gemm_kernel<1, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
+    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
                        lw, lb, t_counter);                                                    \
   else                                                                                        \
-    hipLaunchKernelGGL((dec_ln_gemm_kernel<2, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
+    BOA_LAUNCH((dec_ln_gemm_kernel<2, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
                        lw, lb, t_counter);
   switch (a.K) {
     case 64: BOA_LNG(4) break;
@@ -558,7 +558,7 @@ hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* o
                                  int permute, int zs, int ze, hipStream_t s) {
   if (K % 16 || ldn % 16 || n_src > ldw_in || zs > ze) return hipErrorInvalidValue;
   const size_t n = (size_t)K * ldn;
-  hipLaunchKernelGGL(dec_weight_blk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
+  BOA_LAUNCH(dec_weight_blk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
                      ldw_in, n_src, out, K, ldn, permute, zs, ze);
   return hipGetLastError();
 }
@@ -588,7 +588,7 @@ hipError_t launch_dec_scan_params(const float* w_dt, const float* na, float* wdt
                                   int r, int rb, int ds, int di, hipStream_t s) {
   if (di % 16 || rb % 4 || ds % 4) return hipErrorInvalidValue;
   const int n = di * (rb > ds ? rb : ds);
-  hipLaunchKernelGGL(dec_scan_params_kernel, dim3((n + 255) / 256), dim3(256), 0, s, w_dt, na, wdt_q,
+  BOA_LAUNCH(dec_scan_params_kernel, dim3((n + 255) / 256), dim3(256), 0, s, w_dt, na, wdt_q,
                      na_q, r, rb, ds, di);
   return hipGetLastError();
 }
@@ -723,10 +723,10 @@ hipError_t dec_ln_launch(const float* emb, const uint8_t* tok, float* xt, const 
   const dim3 grid((M + LN - 1) / LN), block(16 * LN);
 #define BOA_DEC_LN(NBv)                                                                      \
   if (emb)                                                                                   \
-    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, true, LN>), grid, block, 0, s, emb, tok, xt, \
+    BOA_LAUNCH((dec_ln_kernel<MODE, NBv, true, LN>), grid, block, 0, s, emb, tok, xt, \
                        src, xnt, w, b, M, ld, t_counter);                                    \
   else                                                                                       \
-    hipLaunchKernelGGL((dec_ln_kernel<MODE, NBv, false, LN>), grid, block, 0, s, emb, tok,   \
+    BOA_LAUNCH((dec_ln_kernel<MODE, NBv, false, LN>), grid, block, 0, s, emb, tok,   \
                        xt, src, xnt, w, b, M, ld, t_counter);
   switch (d) {
     case 64: BOA_DEC_LN(4) break;
@@ -951,10 +951,10 @@ hipError_t launch_dec_xscan(const Dims& D, const LayerW& Lw, const float* na_q, 
   const dim3 grid(xcd_grid(M, 4 * (D.di / 128))), block(1024);
 #define BOA_XSCAN(RBv, DIv)                                                                       \
   if (state_cached)                                                                               \
-    hipLaunchKernelGGL((dec_xscan_kernel<16, RBv, DIv, true>), grid, block, 0, s, Lw, na_q, wdt_q,  \
+    BOA_LAUNCH((dec_xscan_kernel<16, RBv, DIv, true>), grid, block, 0, s, Lw, na_q, wdt_q,  \
                        w_x, ldw_x, zt, cvt, ssm, yt, M, ld, ld_state, D.r);                        \
   else                                                                                            \
-    hipLaunchKernelGGL((dec_xscan_kernel<16, RBv, DIv, false>), grid, block, 0, s, Lw, na_q, wdt_q, \
+    BOA_LAUNCH((dec_xscan_kernel<16, RBv, DIv, false>), grid, block, 0, s, Lw, na_q, wdt_q, \
                        w_x, ldw_x, zt, cvt, ssm, yt, M, ld, ld_state, D.r)
   if (D.di == 128) BOA_XSCAN(8, 128);
   else if (D.di == 256) BOA_XSCAN(8, 256);
@@ -970,10 +970,10 @@ hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, c
   const dim3 grid(xcd_grid(M, 4 * (D.di / 16)));
 #define BOA_DEC_SCAN(DSv, RBv)                                                                  \
   if (state_cached)                                                                             \
-    hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv, true>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, \
+    BOA_LAUNCH((dec_scan_kernel<DSv, RBv, true>), grid, dim3(256), 0, s, Lw, na_q, wdt_q, \
                        zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r, D.di / 16);                 \
   else                                                                                          \
-    hipLaunchKernelGGL((dec_scan_kernel<DSv, RBv, false>), grid, dim3(256), 0, s, Lw, na_q, wdt_q,\
+    BOA_LAUNCH((dec_scan_kernel<DSv, RBv, false>), grid, dim3(256), 0, s, Lw, na_q, wdt_q,\
                        zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r, D.di / 16)
   const int rb = dec_rb(D.r);
   if (D.ds == 16) {
@@ -1024,10 +1024,10 @@ hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, floa
                                  bool to_step, hipStream_t s) {
   const int n = lanes * di;
   if (to_step)
-    hipLaunchKernelGGL(state_to_step_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
+    BOA_LAUNCH(state_to_step_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
                        ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state);
   else
-    hipLaunchKernelGGL(state_to_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
+    BOA_LAUNCH(state_to_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
                        ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state);
   return hipGetLastError();
 }

@@ -290,12 +290,12 @@ namespace {
 hipError_t dec_b16_lds_launch(const DecB16Args& a, hipStream_t s) {
   const dim3 grid(((a.M + 63) / 64) * ((a.N + 63) / 64)), block(256);
   switch (a.K) {
-    case 64: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<2, 2>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<4, 4>), grid, block, 0, s, a); break;
-    case 256: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<8, 4>), grid, block, 0, s, a); break;
-    case 512: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<16, 4>), grid, block, 0, s, a); break;
-    case 1024: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<32, 4>), grid, block, 0, s, a); break;
-    case 2048: hipLaunchKernelGGL((dec_b16_gemm_lds_kernel<64, 4>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_b16_gemm_lds_kernel<2, 2>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_b16_gemm_lds_kernel<4, 4>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_b16_gemm_lds_kernel<8, 4>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_b16_gemm_lds_kernel<16, 4>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_b16_gemm_lds_kernel<32, 4>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_b16_gemm_lds_kernel<64, 4>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -306,12 +306,12 @@ hipError_t dec_b16_blk_launch(const DecB16Args& a, hipStream_t s) {
   const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {
-    case 64: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<2, TM, TN>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<4, TM, TN>), grid, block, 0, s, a); break;
-    case 256: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<8, TM, TN>), grid, block, 0, s, a); break;
-    case 512: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<16, TM, TN>), grid, block, 0, s, a); break;
-    case 1024: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<32, TM, TN>), grid, block, 0, s, a); break;
-    case 2048: hipLaunchKernelGGL((dec_b16_gemm_blk_kernel<64, TM, TN>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_b16_gemm_blk_kernel<2, TM, TN>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_b16_gemm_blk_kernel<4, TM, TN>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_b16_gemm_blk_kernel<8, TM, TN>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_b16_gemm_blk_kernel<16, TM, TN>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_b16_gemm_blk_kernel<32, TM, TN>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_b16_gemm_blk_kernel<64, TM, TN>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -332,12 +332,12 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   const int tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16);
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {
-    case 64: hipLaunchKernelGGL((dec_b16_gemm_kernel<2, 2>), grid, block, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((dec_b16_gemm_kernel<4, 2>), grid, block, 0, s, a); break;
-    case 256: hipLaunchKernelGGL((dec_b16_gemm_kernel<8, 2>), grid, block, 0, s, a); break;
-    case 512: hipLaunchKernelGGL((dec_b16_gemm_kernel<16, 2>), grid, block, 0, s, a); break;
-    case 1024: hipLaunchKernelGGL((dec_b16_gemm_kernel<32, 2>), grid, block, 0, s, a); break;
-    case 2048: hipLaunchKernelGGL((dec_b16_gemm_kernel<64, 2>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_b16_gemm_kernel<2, 2>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_b16_gemm_kernel<4, 2>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_b16_gemm_kernel<8, 2>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_b16_gemm_kernel<16, 2>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_b16_gemm_kernel<32, 2>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_b16_gemm_kernel<64, 2>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -360,7 +360,7 @@ hipError_t launch_dec_b16_weight(const float* w, int ldw_in, int n_src, uint16_t
                                  int ldn, int zs, int ze, hipStream_t s) {
   if (K % 32 || ldn % 16 || n_src > ldw_in || zs > ze) return hipErrorInvalidValue;
   const size_t n = (size_t)K * ldn;
-  hipLaunchKernelGGL(dec_b16_weight_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
+  BOA_LAUNCH(dec_b16_weight_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
                      ldw_in, n_src, out, K, ldn, zs, ze);
   return hipGetLastError();
 }
@@ -484,10 +484,10 @@ static hipError_t dec_b16_ln_go(const float* emb, const uint8_t* tok, float* xt,
                                 int* t_counter, hipStream_t s) {
   const dim3 grid((M + 15) / 16), block(256);
   switch (d) {
-    case 64: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 4, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
-    case 128: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 8, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
-    case 256: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 16, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
-    case 512: hipLaunchKernelGGL((dec_b16_ln_kernel<MODE, 32, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 64: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 4, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 128: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 8, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 256: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 16, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 512: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 32, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -585,10 +585,10 @@ hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_
   dim3 grid((M + 15) / 16, D.di / 16);
 #define BOA_B16_SCAN(DSv, RBv)                                                                  \
   if (state_cached)                                                                             \
-    hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv, true>), grid, dim3(256), 0, s, Lw, na_q,    \
+    BOA_LAUNCH((dec_b16_scan_kernel<DSv, RBv, true>), grid, dim3(256), 0, s, Lw, na_q,    \
                        wdt_q, zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r);                     \
   else                                                                                          \
-    hipLaunchKernelGGL((dec_b16_scan_kernel<DSv, RBv, false>), grid, dim3(256), 0, s, Lw, na_q,   \
+    BOA_LAUNCH((dec_b16_scan_kernel<DSv, RBv, false>), grid, dim3(256), 0, s, Lw, na_q,   \
                        wdt_q, zt, cvt, rows, ssm, yt, M, ld, ld_state, D.r)
   const int rb = dec_rb(D.r);
   if (D.ds == 16) {

@@ -406,7 +406,7 @@ bool dec_persist_fits(int d, int ds, int r, int L) {
 hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, hipStream_t s) {
   if (a.lanes <= 0 || a.maxlen <= 1) return hipSuccess;
   if (!dec_persist_fits(d, ds, a.r, a.L)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((dec_persist_kernel<4, 8>), dim3((a.lanes + PL - 1) / PL), dim3(1024), 0, s, a);
+  BOA_LAUNCH((dec_persist_kernel<4, 8>), dim3((a.lanes + PL - 1) / PL), dim3(1024), 0, s, a);
   return hipGetLastError();
 }
 

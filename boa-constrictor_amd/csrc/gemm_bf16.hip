@@ -189,7 +189,7 @@ static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 
   const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
 #define BOA_B16_GO(ACTv)                                                                  \
-  hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM_, WN_, BK, NBUF, ACTv>), dim3((unsigned)tiles), \
+  BOA_LAUNCH((gemm_bf16_kernel<BM, BN, WM_, WN_, BK, NBUF, ACTv>), dim3((unsigned)tiles), \
                      dim3(64 * WM_ * WN_), 0, s, a, swizzle)
   switch (a.act) {
     case ACT_NONE: BOA_B16_GO(ACT_NONE); break;
@@ -229,7 +229,7 @@ hipError_t launch_b16_weight_nk(const float* w, int ldw_in, int N, int K, int n_
                                 hipStream_t s) {
   if (n_pad < N || N > ldw_in) return hipErrorInvalidValue;
   const size_t n = (size_t)n_pad * K;
-  hipLaunchKernelGGL(b16_weight_nk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
+  BOA_LAUNCH(b16_weight_nk_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, w,
                      ldw_in, N, K, n_pad, out);
   return hipGetLastError();
 }

@@ -222,7 +222,7 @@ static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s, int swizzle = 1) 
   int vec = (a.N % 4 == 0) && (a.ldc % 4 == 0) && (!a.res || a.ldr % 4 == 0);
   // the activation is a template argument: the epilogue has no branch on it
 #define BOA_GEMM_GO(ACTv)                                                                     \
-  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WM_, WN_, BK, ACTv>), dim3((unsigned)tiles),     \
+  BOA_LAUNCH((gemm_f32_kernel<BM, BN, WM_, WN_, BK, ACTv>), dim3((unsigned)tiles),     \
                      dim3(64 * WM_ * WN_), 0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias,   \
                      a.res, a.ldr, a.M, a.N, a.K, vec, swizzle, CdfEpi{})
   switch (a.act) {
@@ -256,7 +256,7 @@ hipError_t gemm_f32_head_cdf(const GemmArgs& a, const CdfEpi& cdf, hipStream_t s
   if (a.ldw < BN) return hipErrorInvalidValue;
   const long long tiles = (a.M + BM - 1) / BM;
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, 4, 4, 16, ACT_CDF>), dim3((unsigned)tiles), dim3(1024),
+  BOA_LAUNCH((gemm_f32_kernel<BM, BN, 4, 4, 16, ACT_CDF>), dim3((unsigned)tiles), dim3(1024),
                      0, s, a.X, a.ldx, a.W, a.ldw, nullptr, 0, a.bias, nullptr, 0, a.M, a.N, a.K,
                      0, 1, cdf);
   return hipGetLastError();

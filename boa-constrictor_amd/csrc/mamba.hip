@@ -121,10 +121,10 @@ hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, v
   const int ut = emb ? 1 : 0;
 #define BOA_LN1(Dv)                                                                          \
   if (bf16)                                                                                  \
-    hipLaunchKernelGGL((ln1_kernel<uint16_t, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x, \
+    BOA_LAUNCH((ln1_kernel<uint16_t, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x, \
                        (uint16_t*)xn, w, b, rows);                                           \
   else                                                                                       \
-    hipLaunchKernelGGL((ln1_kernel<float, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x,    \
+    BOA_LAUNCH((ln1_kernel<float, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x,    \
                        (float*)xn, w, b, rows);
   switch (d) {
     case 64: BOA_LN1(64) break;
@@ -204,10 +204,10 @@ hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, 
     constexpr int RPB = Dv <= 256 ? 32 : 16;                                                    \
     const dim3 grid((rows + RPB - 1) / RPB), block(256);                                        \
     if (bf16)                                                                                   \
-      hipLaunchKernelGGL((ln2_kernel<uint16_t, Dv>), grid, block, 0, s, (const uint16_t*)x,     \
+      BOA_LAUNCH((ln2_kernel<uint16_t, Dv>), grid, block, 0, s, (const uint16_t*)x,     \
                          (uint16_t*)out, w, b, rows);                                           \
     else                                                                                        \
-      hipLaunchKernelGGL((ln2_kernel<float, Dv>), grid, block, 0, s, (const float*)x,           \
+      BOA_LAUNCH((ln2_kernel<float, Dv>), grid, block, 0, s, (const float*)x,           \
                          (float*)out, w, b, rows);                                              \
   }
   switch (d) {
@@ -266,10 +266,10 @@ hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, 
                              void* out, int lanes, int T, int di, bool bf16, hipStream_t s) {
   int n = lanes * di;
   if (bf16)
-    hipLaunchKernelGGL(conv_chunk_kernel<uint16_t>, dim3((n + 255) / 256), dim3(256), 0, s,
+    BOA_LAUNCH(conv_chunk_kernel<uint16_t>, dim3((n + 255) / 256), dim3(256), 0, s,
                        (const uint16_t*)xz, conv_state, w, cb, (uint16_t*)out, lanes, T, di);
   else
-    hipLaunchKernelGGL(conv_chunk_kernel<float>, dim3((n + 255) / 256), dim3(256), 0, s,
+    BOA_LAUNCH(conv_chunk_kernel<float>, dim3((n + 255) / 256), dim3(256), 0, s,
                        (const float*)xz, conv_state, w, cb, (float*)out, lanes, T, di);
   return hipGetLastError();
 }
@@ -325,11 +325,11 @@ static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const void* xz,
                                 int bs, bool bf16, hipStream_t s) {
   const size_t lds = sizeof(float) * SCAN_TB * D.R;
   if (bf16)
-    hipLaunchKernelGGL((scan_chunk_kernel<DS, RB, uint16_t>), dim3((lanes * D.di) / bs), dim3(bs),
+    BOA_LAUNCH((scan_chunk_kernel<DS, RB, uint16_t>), dim3((lanes * D.di) / bs), dim3(bs),
                        lds, s, D, Lw, (const uint16_t*)xz, (const uint16_t*)conv,
                        (const uint16_t*)delta, ssm_state, (uint16_t*)y, lanes, T);
   else
-    hipLaunchKernelGGL((scan_chunk_kernel<DS, RB, float>), dim3((lanes * D.di) / bs), dim3(bs), lds,
+    BOA_LAUNCH((scan_chunk_kernel<DS, RB, float>), dim3((lanes * D.di) / bs), dim3(bs), lds,
                        s, D, Lw, (const float*)xz, (const float*)conv, (const float*)delta,
                        ssm_state, (float*)y, lanes, T);
   return hipGetLastError();
@@ -369,7 +369,7 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
   if (!n) return hipSuccess;
   size_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (uint32_t*)p, n);
+  BOA_LAUNCH(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (uint32_t*)p, n);
   return hipGetLastError();
 }
 

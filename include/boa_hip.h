@@ -225,10 +225,11 @@ uint32_t boa_crc32(const uint8_t* data, int64_t n);
 #define BOA_K_CODER 5
 #define BOA_K_DECODE 6     /* decode coder step (fp32: head.2 fused in) */
 #define BOA_K_GEMM_SMALL 7 /* compress GEMMs on the smaller tile (x_proj) */
-#define BOA_K_DEC_GEMM 8   /* decode-step GEMMs (LayerNorm-fused ones included) */
-#define BOA_K_DEC_SCAN 9   /* decode-step scan */
+#define BOA_K_DEC_GEMM 8   /* decode-step GEMMs without a fused LayerNorm */
+#define BOA_K_DEC_SCAN 9   /* decode-step scan (x_proj fused in where it runs so) */
 #define BOA_K_HEAD_CDF 10  /* compress head.2 fused with the CDF (fp32) */
-#define BOA_K_COUNT 11
+#define BOA_K_DEC_LNGEMM 11 /* decode-step LayerNorm + in_proj / FF1 GEMMs */
+#define BOA_K_COUNT 12
 /* When enabled, every kernel launch is bracketed by HIP events recorded on
  * the launch stream; boa_profile_read synchronises and returns, for a
  * kernel class, the summed kernel time (ms), the launch count and the
