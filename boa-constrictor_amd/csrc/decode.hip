@@ -41,13 +41,19 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // logits) use unpermuted weights: row 4g+v is feature 4g+v.
 // Epilogue operands that do not depend on the GEMM (bias, residual), loaded
 // before the K loop so that their latency hides behind it.
+// With CONV, in_proj's conv-step operands too: the lane's conv state rows,
+// taps and biases of its four features.
+template <bool CONV = false>
 struct EpiPre {
   float b[4];
   float4 r;
+  float4 cs[CONV ? 4 : 1], cw[CONV ? 4 : 1];
+  float cb[CONV ? 4 : 1];
 };
 
+template <bool CONV = false>
 __device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, int m, int g,
-                                                 EpiPre& p) {
+                                                 EpiPre<CONV>& p) {
   if (m >= a.M || n0 >= a.N) return;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -56,10 +62,22 @@ __device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, i
   }
   if (a.res && !a.row_major && !(a.conv_di > 0))
     p.r = *reinterpret_cast<const float4*>(a.res + ((size_t)(n0 >> 4) * a.ldr + m) * 16 + 4 * g);
+  if (CONV && a.conv_di > 0 && n0 < a.conv_di) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int n = n0 + 4 * e + g;
+      p.cs[e] = state_ld4(reinterpret_cast<const float4*>(a.conv_state) + (size_t)n * a.ld_state + m,
+                          a.state_cached);
+      p.cw[e] = reinterpret_cast<const float4*>(a.conv_w)[n];
+      p.cb[e] = a.conv_b[n];
+    }
+  }
 }
 
-__device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4 acc, int n0, int m,
-                                             int g, const EpiPre* pre = nullptr) {
+template <bool CONV = false>
+__device__ __forceinline__ void dec_epilogue_impl(const DecGemmArgs& a, const floatx4 acc, int n0,
+                                                  int m, int g, const EpiPre<CONV> pv, bool have) {
+  const EpiPre<CONV>* pre = have ? &pv : nullptr;
   if (m >= a.M || n0 >= a.N) return;
   int nf[4];
 #pragma unroll
@@ -90,9 +108,10 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
     for (int e = 0; e < 4; ++e) {
       const int n = nf[e];
       float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
-      const float4 s0 = state_ld4(st, a.state_cached);
-      const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
-      cv[e] = conv_step_value<MATH_BR>(a.conv_b[n], s0, v[e], wv);
+      const float4 s0 = (CONV && pre) ? pre->cs[e] : state_ld4(st, a.state_cached);
+      const float4 wv = (CONV && pre) ? pre->cw[e] : reinterpret_cast<const float4*>(a.conv_w)[n];
+      const float bc = (CONV && pre) ? pre->cb[e] : a.conv_b[n];
+      cv[e] = conv_step_value<MATH_BR>(bc, s0, v[e], wv);
       state_st4(st, make_float4(s0.y, s0.z, s0.w, v[e]), a.state_cached);
     }
     float* o = a.conv_out + ((size_t)(n0 >> 4) * a.ldc + m) * 16 + 4 * g;
@@ -113,6 +132,18 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
     for (int e = 0; e < 4; ++e)
       if (nf[e] < a.N) o[e] = v[e];
   }
+}
+
+// The epilogue operands come prefetched (pre) or are loaded here (no pre);
+// the prefetched struct is passed by value so that it stays in registers.
+template <bool CONV = false>
+__device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4 acc, int n0, int m,
+                                             int g, const EpiPre<CONV>& pre) {
+  dec_epilogue_impl<CONV>(a, acc, n0, m, g, pre, true);
+}
+__device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4 acc, int n0, int m,
+                                             int g) {
+  dec_epilogue_impl<false>(a, acc, n0, m, g, EpiPre<false>{}, false);
 }
 
 // The K loop of one wave: loads run PD groups of UQ 16-k blocks ahead of the
@@ -180,10 +211,10 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
     const XcdSlot q = xcd_slot(blockIdx.x, n_tiles);
     const int m0 = q.grp * 64 + 16 * (threadIdx.x >> 6), n0 = q.j * 16;
     if (m0 >= a.M) return;  // whole waves exit; no barriers below
-    EpiPre pre;
+    EpiPre<> pre;
     dec_epi_prefetch(a, n0, m0 + i, g, pre);
     dec_mainloop<KS, TM, TN, UQ, PD>(a, n0, m0, i, g, acc);
-    dec_epilogue(a, acc[0][0], n0, m0 + i, g, &pre);
+    dec_epilogue(a, acc[0][0], n0, m0 + i, g, pre);
     return;
   }
   const int m_tiles = (a.M + 16 * TM - 1) / (16 * TM);
@@ -405,6 +436,13 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
     }
   }
   __syncthreads();
+  // the epilogue's operands (bias, and in_proj's conv state, taps and
+  // biases), loaded now so that their latency hides behind the LayerNorm
+  // and the MFMAs; the staging loads above have all been issued and waited
+  const int lane_ = tid & 63, wv_ = tid >> 6;
+  const int lr_ = 16 * (wv_ >> 2) + (lane_ & 15), fn0 = n0 + 16 * (wv_ & 3);
+  EpiPre<MODE == 1> pre;
+  dec_epi_prefetch<MODE == 1>(a, fn0, m0 + lr_, lane_ >> 4, pre);
   if (EMB && n0 == 0 && m0 + ml < a.M) {  // layer 0: x = embedding rows
 #pragma unroll
     for (int it = 0; it < SQ; ++it) {
@@ -504,7 +542,7 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
     acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av.w, bv.w, acc, 0, 0, 0);
   }
   // 4. epilogue
-  dec_epilogue(a, acc, n0 + 16 * (wv & 3), m0 + lr, g);
+  dec_epilogue<MODE == 1>(a, acc, n0 + 16 * (wv & 3), m0 + lr, g, pre);
 }
 
 bool dec_ln_gemm_fits(int d, int N) { return (d == 64 || d == 128 || d == 256) && N % 64 == 0; }
