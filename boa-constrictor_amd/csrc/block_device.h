@@ -62,7 +62,6 @@ __device__ __forceinline__ size_t dblk32(int k, int m, int ld) {
 }
 
 constexpr int RMAX = 32;  // dt_rank <= 32 (d_model <= 512)
-constexpr int SCAN_TB = 32;  // timesteps of delta rows staged in LDS per pass
 
 template <int DS, int RB>
 struct ScanCtx {

@@ -275,40 +275,68 @@ hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, 
 }
 
 // -------------------------------------------------------- selective scan
-// Thread per (lane, channel); a block never straddles two lanes, so the
-// delta rows (dt_in | B | C of one token) are shared by the whole block: they
-// are staged in LDS SCAN_TB timesteps at a time and read as broadcasts.
-// d_state 16 with dt_rank <= 16: the fp32 kernel runs five waves per SIMD
-// (96 VGPRs); the bf16 kernel runs six (80 VGPRs with a few spilled, which
-// measured faster on MI355X than five without).
-template <int DS, int RB, typename TA>
+// Thread per (lane, channel); a block covers bs channels of one lane (bs
+// divides di), so the token's delta row (dt_in | B | C) is the same for every
+// thread of the wave and is read with scalar loads into SGPRs: no LDS
+// staging and no barriers (against rows staged in LDS and read as
+// broadcasts, 9 % faster in fp32 on the C2 model and 19-21 % in bf16 on the
+// C3 and C5 models).  FULL: dt_rank equals the bound RB.  Otherwise the dt
+// inputs beyond dt_rank are zeroed, which leaves the fma chain's value
+// unchanged (the partial sum starts at +0 and so is never -0, and
+// fma(0, 0, a) = a).  d_state 16 with dt_rank <= 16 runs five (fp32, 80
+// VGPRs) or six (bf16) waves per SIMD.
+template <int DS, int RB, bool FULL>
+__device__ __forceinline__ void scan_row(const float* dr, int r, float* dv) {
+#pragma unroll
+  for (int j = 0; j < RB; ++j) {
+    const float v = dr[j];  // j < RB <= R: inside the row
+    dv[j] = FULL || j < r ? v : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < 2 * DS; ++j) dv[RB + j] = dr[r + j];
+}
+// bf16 rows: dt_rank, d_state and so the row length are even (d_model is a
+// multiple of 64), so the element pairs are read as aligned dwords
+template <int DS, int RB, bool FULL>
+__device__ __forceinline__ void scan_row(const uint16_t* dr, int r, float* dv) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(dr);
+#pragma unroll
+  for (int j = 0; j < RB / 2; ++j) {
+    const uint32_t v = w[j];
+    dv[2 * j] = FULL || 2 * j < r ? u2f(v << 16) : 0.0f;
+    dv[2 * j + 1] = FULL || 2 * j + 1 < r ? u2f(v & 0xFFFF0000u) : 0.0f;
+  }
+  const uint32_t* wb = reinterpret_cast<const uint32_t*>(dr + r);
+#pragma unroll
+  for (int j = 0; j < DS; ++j) {
+    const uint32_t v = wb[j];
+    dv[RB + 2 * j] = u2f(v << 16);
+    dv[RB + 2 * j + 1] = u2f(v & 0xFFFF0000u);
+  }
+}
+
+template <int DS, int RB, bool FULL, typename TA>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DS == 16 && RB <= 16 ? (sizeof(TA) == 2 ? 6 : 5) : 1, 8)))
-void scan_chunk_kernel(Dims D, LayerW Lw,
-                                                         const TA* __restrict__ xz,
-                                                         const TA* __restrict__ conv,
-                                                         const TA* __restrict__ delta,
-                                                         float* ssm_state, TA* y, int lanes,
-                                                         int T) {
-  extern __shared__ float s_delta[];  // [SCAN_TB][R]
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+void scan_chunk_sload_kernel(Dims D, LayerW Lw, const TA* __restrict__ xz,
+                             const TA* __restrict__ conv, const TA* __restrict__ delta,
+                             float* __restrict__ ssm_state, TA* __restrict__ y, int lanes,
+                             int T) {
   const int di = D.di, R = D.R;
-  const int c = idx % di, b = idx / di;  // the grid covers lanes * di exactly
-  float* ssm = ssm_state + (size_t)idx * DS;
+  const int base = blockIdx.x * blockDim.x;
+  const int b = base / di;
+  const int c = base - b * di + threadIdx.x;
+  float* ssm = ssm_state + (size_t)(base + threadIdx.x) * DS;
   ScanCtx<DS, RB> sc;
   scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
   const TA* drows = delta + (size_t)b * T * R;
-  for (int t0 = 0; t0 < T; t0 += SCAN_TB) {
-    const int nt = min(SCAN_TB, T - t0);
-    __syncthreads();
-    for (int q = threadIdx.x; q < nt * R; q += blockDim.x) s_delta[q] = ldv(drows + (size_t)t0 * R + q);
-    __syncthreads();
-    for (int tt = 0; tt < nt; ++tt) {
-      const size_t row = (size_t)b * T + t0 + tt;
-      const float u = ldv(conv + row * di + c);
-      const float z = ldv(xz + row * 2 * di + di + c);
-      stv(y + row * di + c, scan_token<DS, RB, sizeof(TA) == 2 ? MATH_HW : MATH_BF>(
-                                 sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z));
-    }
+  for (int t = 0; t < T; ++t) {
+    const size_t row = (size_t)b * T + t;
+    float dv[RB + 2 * DS];
+    scan_row<DS, RB, FULL>(drows + (size_t)t * R, D.r, dv);
+    const float u = ldv(conv + row * di + c);
+    const float z = ldv(xz + row * 2 * di + di + c);
+    stv(y + row * di + c, scan_token<DS, RB, sizeof(TA) == 2 ? MATH_HW : MATH_BF>(
+                              sc, dv, dv + RB, RB, u, z));
   }
   scan_store<DS, RB>(sc, ssm);
 }
@@ -323,15 +351,23 @@ template <int DS, int RB>
 static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const void* xz, const void* conv,
                                 const void* delta, float* ssm_state, void* y, int lanes, int T,
                                 int bs, bool bf16, hipStream_t s) {
-  const size_t lds = sizeof(float) * SCAN_TB * D.R;
-  if (bf16)
-    BOA_LAUNCH((scan_chunk_kernel<DS, RB, uint16_t>), dim3((lanes * D.di) / bs), dim3(bs),
-                       lds, s, D, Lw, (const uint16_t*)xz, (const uint16_t*)conv,
-                       (const uint16_t*)delta, ssm_state, (uint16_t*)y, lanes, T);
+  const dim3 grid((lanes * D.di) / bs);
+  if (bf16 && D.r == RB)
+    BOA_LAUNCH((scan_chunk_sload_kernel<DS, RB, true, uint16_t>), grid, dim3(bs), 0, s, D, Lw,
+               (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,
+               (uint16_t*)y, lanes, T);
+  else if (bf16)
+    BOA_LAUNCH((scan_chunk_sload_kernel<DS, RB, false, uint16_t>), grid, dim3(bs), 0, s, D, Lw,
+               (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,
+               (uint16_t*)y, lanes, T);
+  else if (D.r == RB)
+    BOA_LAUNCH((scan_chunk_sload_kernel<DS, RB, true, float>), grid, dim3(bs), 0, s, D, Lw,
+               (const float*)xz, (const float*)conv, (const float*)delta, ssm_state, (float*)y,
+               lanes, T);
   else
-    BOA_LAUNCH((scan_chunk_kernel<DS, RB, float>), dim3((lanes * D.di) / bs), dim3(bs), lds,
-                       s, D, Lw, (const float*)xz, (const float*)conv, (const float*)delta,
-                       ssm_state, (float*)y, lanes, T);
+    BOA_LAUNCH((scan_chunk_sload_kernel<DS, RB, false, float>), grid, dim3(bs), 0, s, D, Lw,
+               (const float*)xz, (const float*)conv, (const float*)delta, ssm_state, (float*)y,
+               lanes, T);
   return hipGetLastError();
 }
 
