@@ -341,7 +341,10 @@ def main() -> int:
     peak_mm = PEAK_TFLOPS[prec]
     gemm_launch_us = g["ms"] * 1e3 / max(g["launches"], 1)
     sc = prof["scan"]
-    scan_kernel = f"boa::scan_chunk_kernel<{ds}, {8 if d <= 128 else (16 if d <= 256 else 32)}>"
+    r_dt = -(-d // 16)
+    rb = 8 if r_dt <= 8 else (16 if r_dt <= 16 else 32)
+    scan_kernel = (f"boa::scan_chunk_sload_kernel<{ds}, {rb}, {str(r_dt == rb).lower()}, "
+                   f"{'float' if prec == 'fp32' else 'unsigned short'}>")
 
     # The decode step's kernels on directly launched steps (boa_step_batch)
     # after the timed region, each launch timed by the HIP events its
