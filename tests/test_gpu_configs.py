@@ -59,6 +59,38 @@ def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
         assert np.array_equal(st.view(np.uint32), want[:, t].view(np.uint32)), f"step {t}"
 
 
+@pytest.mark.parametrize("d,ds,prec", [(64, 16, "fp32"), (80, 16, "fp32"), (256, 16, "fp32"),
+                                       (64, 16, "bf16"), (256, 16, "bf16"), (512, 32, "bf16")])
+def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
+    """The compress scan reads its delta rows through LDS on small grids (under
+    two waves per SIMD) and through scalar loads otherwise: the same lanes'
+    logits are bit-identical between a small and a large batch, and (fp32)
+    equal to the oracle's."""
+    import boa_hip
+    torch = torch_dev
+    w = make_weights(d, 1, ds)
+    di = 2 * d
+    big = -(-2 * 64 * 1024 // di)  # the first lane count on the scalar-load form
+    small, T = 6, 20
+    rng = np.random.default_rng(7 + d + ds)
+    tok = rng.integers(0, 256, size=(big, T), dtype=np.uint8)
+    out = []
+    for lanes in (small, big):
+        c = boa_hip.Codec(d, 1, ds, lanes, 0, precision=prec)
+        c.set_stream(torch.cuda.current_stream().cuda_stream)
+        c.load_weights(w)
+        c.reset_state(lanes)
+        d_log = torch.zeros(lanes * T * 256, dtype=torch.float32, device="cuda")
+        c.forward_chunk(torch.from_numpy(np.ascontiguousarray(tok[:lanes])).cuda(), lanes, T, d_log)
+        torch.cuda.synchronize()
+        out.append(d_log.cpu().numpy().reshape(lanes, T, 256)[:small])
+        c.close()
+    assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    if prec == "fp32":
+        want = oracle.Model(w, d, 1, ds).new_state(small).forward_chunk(tok[:small])
+        assert np.array_equal(out[1].view(np.uint32), want.view(np.uint32))
+
+
 def _same_container(oracle, w, d, L, ds, data, chunk, lanes, tile=0, temperature=1.0,
                     max_chunks=0):
     m = oracle.Model(w, d, L, ds)
