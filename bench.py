@@ -360,10 +360,14 @@ def main() -> int:
         dec = {"lanes": lanes, "steps": 32, "launch": "direct, HIP events in each dispatch",
                "plan": plan,
                "kernel_us_per_step": {k: round(v["us_per_step"], 2) for k, v in prof_dec.items()}}
-        for k, v in prof_dec.items():
-            n_l = v["launches_per_step"]
-            dec_cls[k] = dict(avg_us=v["us_per_step"] / n_l, launches_per_step=n_l,
-                              work_per_launch=v["work_per_step"] / n_l)
+        # A persistent decode (d_model 64) runs the whole batch in one
+        # kernel, not these step kernels: its candidate below is the whole
+        # decompress.
+        if not plan["persistent"]:
+            for k, v in prof_dec.items():
+                n_l = v["launches_per_step"]
+                dec_cls[k] = dict(avg_us=v["us_per_step"] / n_l, launches_per_step=n_l,
+                                  work_per_launch=v["work_per_step"] / n_l)
 
     # Rooflines of the kernels that take most of a round trip; `roofline`
     # is the one with the largest total time per step (compress: its
@@ -412,6 +416,14 @@ def main() -> int:
             v = dec_cls[k]
             add(name, kernel, bound, v["work_per_launch"], v["avg_us"],
                 v["launches_per_step"] * steps_per_dec, peak_mm)
+    if dec is not None and dec["plan"]["persistent"] and K:
+        # model FLOPs per token: in_proj, x_proj, dt_proj, out_proj, FF1, FF2
+        # per layer, then head.1 and head.2
+        di, r_dt = 2 * d, -(-d // 16)
+        macs = L * (d * 2 * di + di * (r_dt + 2 * ds) + r_dt * di + di * d + 8 * d * d) + d * d + d * 256
+        flops = 2.0 * macs * (n - n_chunks)  # one model step per byte after a chunk's first
+        add("decode (persistent kernel)", "boa::dec_persist_kernel (every step of the batch in "
+            "one launch)", "mfma", flops, t_d / K * 1e6, 1, peak_mm)
     dom = max(cands, key=lambda k: cands[k]["s_per_round_trip"])
     roofline = dict(cands[dom])
     roofline["class"] = dom

@@ -103,16 +103,24 @@ __device__ __forceinline__ void dec_epilogue_impl(const DecGemmArgs& a, const fl
     return;
   }
   if (a.conv_di > 0 && n0 < a.conv_di) {
-    float cv[4];
+    // every load of the four channels before the first state store, so that
+    // they are in flight together (a store may alias a later load)
+    float4 s0[4], wv[4];
+    float bc[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int n = nf[e];
-      float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
-      const float4 s0 = (CONV && pre) ? pre->cs[e] : state_ld4(st, a.state_cached);
-      const float4 wv = (CONV && pre) ? pre->cw[e] : reinterpret_cast<const float4*>(a.conv_w)[n];
-      const float bc = (CONV && pre) ? pre->cb[e] : a.conv_b[n];
-      cv[e] = conv_step_value<MATH_BR>(bc, s0, v[e], wv);
-      state_st4(st, make_float4(s0.y, s0.z, s0.w, v[e]), a.state_cached);
+      const float4* st = reinterpret_cast<const float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
+      s0[e] = (CONV && pre) ? pre->cs[e] : state_ld4(st, a.state_cached);
+      wv[e] = (CONV && pre) ? pre->cw[e] : reinterpret_cast<const float4*>(a.conv_w)[n];
+      bc[e] = (CONV && pre) ? pre->cb[e] : a.conv_b[n];
+    }
+    float cv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)nf[e] * a.ld_state + m;
+      cv[e] = conv_step_value<MATH_BR>(bc[e], s0[e], v[e], wv[e]);
+      state_st4(st, make_float4(s0[e].y, s0[e].z, s0[e].w, v[e]), a.state_cached);
     }
     float* o = a.conv_out + ((size_t)(n0 >> 4) * a.ldc + m) * 16 + 4 * g;
     *reinterpret_cast<float4*>(o) = make_float4(cv[0], cv[1], cv[2], cv[3]);
