@@ -945,6 +945,33 @@ __global__ __launch_bounds__(1024) void dec_xscan_kernel(LayerW Lw, const float*
         state_ld4(h4 + ((size_t)((8 * cb + q + 4) * (DS / 4) + n4) * ld_state + mc) * 16 + cl, CACHED);
     h1[4 * n4] = hv.x; h1[4 * n4 + 1] = hv.y; h1[4 * n4 + 2] = hv.z; h1[4 * n4 + 3] = hv.w;
   }
+  // the two channels' conv output and z (of lane mc) and the first channel's
+  // scan parameters, also in flight during x_proj (16.45 -> 16.2 us)
+  float uz[2][2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const size_t cmp = dblk(16 * (8 * cb + q + 4 * p) + cl, mc, ld);
+    uz[p][0] = cvt[cmp];
+    uz[p][1] = zt[cmp];
+  }
+  ScanCtx<DS, RB> sc0;
+  {
+    const int c16 = 8 * cb + q, c = 16 * c16 + cl;
+    const float4* na4 = reinterpret_cast<const float4*>(na_q);
+    const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
+#pragma unroll
+    for (int n4 = 0; n4 < DS / 4; ++n4) {
+      const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + cl];
+      sc0.na[4 * n4] = av.x; sc0.na[4 * n4 + 1] = av.y; sc0.na[4 * n4 + 2] = av.z; sc0.na[4 * n4 + 3] = av.w;
+    }
+#pragma unroll
+    for (int j4 = 0; j4 < RB / 4; ++j4) {
+      const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + cl];
+      sc0.wdt[4 * j4] = wv4.x; sc0.wdt[4 * j4 + 1] = wv4.y; sc0.wdt[4 * j4 + 2] = wv4.z; sc0.wdt[4 * j4 + 3] = wv4.w;
+    }
+    sc0.bdt = Lw.b_dt[c];
+    sc0.dd = Lw.dd[c];
+  }
   // 2. x_proj: wave w < NB computes feature block w for lanes m0 .. m0 + 15
   const int wv = tid >> 6;
   if (wv < NB) {
@@ -968,23 +995,27 @@ __global__ __launch_bounds__(1024) void dec_xscan_kernel(LayerW Lw, const float*
     const int c16 = 8 * cb + q + 4 * p;
     const int c = 16 * c16 + cl;
     ScanCtx<DS, RB> sc;
+    if (p == 0) {
+      sc = sc0;
+    } else {
+#pragma unroll
+      for (int n4 = 0; n4 < DS / 4; ++n4) {
+        const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + cl];
+        sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
+      }
+#pragma unroll
+      for (int j4 = 0; j4 < RB / 4; ++j4) {
+        const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + cl];
+        sc.wdt[4 * j4] = wv4.x; sc.wdt[4 * j4 + 1] = wv4.y; sc.wdt[4 * j4 + 2] = wv4.z; sc.wdt[4 * j4 + 3] = wv4.w;
+      }
+      sc.bdt = Lw.b_dt[c];
+      sc.dd = Lw.dd[c];
+    }
 #pragma unroll
     for (int n = 0; n < DS; ++n) sc.h[n] = p == 0 ? h0[n] : h1[n];
-#pragma unroll
-    for (int n4 = 0; n4 < DS / 4; ++n4) {
-      const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + cl];
-      sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
-    }
-#pragma unroll
-    for (int j4 = 0; j4 < RB / 4; ++j4) {
-      const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + cl];
-      sc.wdt[4 * j4] = wv4.x; sc.wdt[4 * j4 + 1] = wv4.y; sc.wdt[4 * j4 + 2] = wv4.z; sc.wdt[4 * j4 + 3] = wv4.w;
-    }
-    sc.bdt = Lw.b_dt[c];
-    sc.dd = Lw.dd[c];
     const size_t cm = dblk(c, m, ld);
-    const float u = cvt[cm];
-    const float z = zt[cm];
+    const float u = uz[p][0];
+    const float z = uz[p][1];
     yt[cm] = scan_token<DS, RB, MATH_BR>(sc, row, row + RB, r, u, z);
 #pragma unroll
     for (int n4 = 0; n4 < DS / 4; ++n4)
