@@ -341,27 +341,46 @@ void scan_chunk_sload_kernel(Dims D, LayerW Lw, const TA* __restrict__ xz,
   scan_store<DS, RB>(sc, ssm);
 }
 
-// Small grids (fewer than two waves per SIMD, e.g. d_model 64 with 64
-// lanes) leave the scalar loads' latency exposed at every token: there the
-// rows are staged in LDS SCAN_TB tokens at a time and read as broadcasts
-// (C1: 40.3 ms with scalar loads against 37.2 ms staged, per compress).
-constexpr int SCAN_TB = 32;
+constexpr int SCAN_TB = 32;  // tokens of delta rows staged in LDS per pass
 
-template <int DS, int RB, typename TA>
-__global__ __launch_bounds__(256) void scan_chunk_lds_kernel(Dims D, LayerW Lw,
-                                                             const TA* __restrict__ xz,
-                                                             const TA* __restrict__ conv,
-                                                             const TA* __restrict__ delta,
-                                                             float* __restrict__ ssm_state,
-                                                             TA* __restrict__ y, int lanes, int T) {
+// Small grids (fewer than two waves per SIMD, e.g. d_model 64 with 64
+// lanes), where one thread per channel leaves most SIMDs idle and every
+// token's latency exposed: P = DS / SPT threads share a channel, each owning
+// SPT states, and the delta rows are staged in LDS SCAN_TB tokens at a time.
+// Every thread of the group computes the token's dt (the same operations, so
+// the same value) and updates its states; the output sum y = fma(h_n, C_n, y)
+// then runs over n = 0 .. DS-1 in order, handed from thread to thread of the
+// group (SPT terms each), and the group's last thread adds D u, gates and
+// stores: the bits of scan_token.  C1 (64 lanes, d_model 64): 37.2 ms per
+// compress with one thread per channel, 28.6 ms with SPT 4 (8: 28.6, 2: 31.7,
+// 1: 41.8).
+template <int DS, int RB, int SPT, typename TA>
+__global__ __launch_bounds__(256) void scan_chunk_split_kernel(Dims D, LayerW Lw,
+                                                               const TA* __restrict__ xz,
+                                                               const TA* __restrict__ conv,
+                                                               const TA* __restrict__ delta,
+                                                               float* __restrict__ ssm_state,
+                                                               TA* __restrict__ y, int lanes,
+                                                               int T, int cpb) {
+  constexpr int P = DS / SPT;
+  static_assert(DS % SPT == 0 && P <= 16 && 16 % P == 0, "a group lies within a DPP row");
+  constexpr int M = sizeof(TA) == 2 ? MATH_HW : MATH_BF;
   extern __shared__ float s_delta[];  // [SCAN_TB][R]
-  const int di = D.di, R = D.R;
-  const int base = blockIdx.x * blockDim.x;
+  const int di = D.di, R = D.R, r = D.r;
+  const int sub = threadIdx.x % P, cl = threadIdx.x / P;
+  const int base = blockIdx.x * cpb;  // cpb channels of one lane per block
   const int b = base / di;
-  const int c = base - b * di + threadIdx.x;
-  float* ssm = ssm_state + (size_t)(base + threadIdx.x) * DS;
-  ScanCtx<DS, RB> sc;
-  scan_load<DS, RB>(sc, Lw, ssm, c, di, D.r);
+  const int c = base - b * di + cl;
+  float* ssm = ssm_state + ((size_t)b * di + c) * DS + SPT * sub;
+  float h[SPT], na[SPT], wdt[RB];
+#pragma unroll
+  for (int n = 0; n < SPT; ++n) {
+    h[n] = ssm[n];
+    na[n] = Lw.na2[(size_t)c * DS + SPT * sub + n];
+  }
+#pragma unroll
+  for (int j = 0; j < RB; ++j) wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
+  const float bdt = Lw.b_dt[c], dd = Lw.dd[c];
   const TA* drows = delta + (size_t)b * T * R;
   for (int t0 = 0; t0 < T; t0 += SCAN_TB) {
     const int nt = min(SCAN_TB, T - t0);
@@ -371,13 +390,45 @@ __global__ __launch_bounds__(256) void scan_chunk_lds_kernel(Dims D, LayerW Lw,
     __syncthreads();
     for (int tt = 0; tt < nt; ++tt) {
       const size_t row = (size_t)b * T + t0 + tt;
+      const float* dv = s_delta + tt * R;
+      const float* Bv = dv + r;
+      const float* Cv = Bv + DS;
       const float u = ldv(conv + row * di + c);
       const float z = ldv(xz + row * 2 * di + di + c);
-      stv(y + row * di + c, scan_token<DS, RB, sizeof(TA) == 2 ? MATH_HW : MATH_BF>(
-                                sc, s_delta + tt * R, s_delta + tt * R + D.r, D.r, u, z));
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < RB; ++j)
+        if (j < r) acc = __builtin_fmaf(dv[j], wdt[j], acc);
+      const float dt = softplus<M>(acc + bdt);
+      const float dtu = dt * u;
+#pragma unroll
+      for (int n = 0; n < SPT; ++n) {
+        const float dA = exp2_neg_sel<M>(na[n] * dt);
+        h[n] = __builtin_fmaf(dA, h[n], Bv[SPT * sub + n] * dtu);
+      }
+      float yv = 0.0f;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        if (sub == p) {
+#pragma unroll
+          for (int n = 0; n < SPT; ++n) yv = __builtin_fmaf(h[n], Cv[SPT * p + n], yv);
+        }
+        // thread p + 1 takes the running sum: a DPP shift by one lane within
+        // rows of 16 (P divides 16, so a group never straddles a row)
+        if (p + 1 < P)
+          yv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                             __builtin_bit_cast(int, yv), __builtin_bit_cast(int, yv),
+                                             0x111, 0xF, 0xF, false));
+      }
+      if (sub == P - 1) {
+        yv = yv + dd * u;
+        const float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));
+        stv(y + row * di + c, yv * (z * sg));
+      }
     }
   }
-  scan_store<DS, RB>(sc, ssm);
+#pragma unroll
+  for (int n = 0; n < SPT; ++n) ssm[n] = h[n];
 }
 
 static int block_for(int di) {
@@ -393,14 +444,18 @@ static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const void* xz,
   const dim3 grid((lanes * D.di) / bs);
   if ((int64_t)lanes * D.di < 2 * 64 * 1024) {  // under two waves per SIMD
     const size_t lds = sizeof(float) * SCAN_TB * D.R;
+    constexpr int SPT = 4, P = DS / SPT;
+    int cpb = 256 / P;  // channels per block: a power of two dividing di
+    while (cpb > 1 && D.di % cpb) cpb >>= 1;
+    const dim3 g2((lanes * D.di) / cpb);
     if (bf16)
-      BOA_LAUNCH((scan_chunk_lds_kernel<DS, RB, uint16_t>), grid, dim3(bs), lds, s, D, Lw,
-                 (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,
-                 (uint16_t*)y, lanes, T);
+      BOA_LAUNCH((scan_chunk_split_kernel<DS, RB, SPT, uint16_t>), g2, dim3(cpb * P), lds, s, D,
+                 Lw, (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,
+                 (uint16_t*)y, lanes, T, cpb);
     else
-      BOA_LAUNCH((scan_chunk_lds_kernel<DS, RB, float>), grid, dim3(bs), lds, s, D, Lw,
+      BOA_LAUNCH((scan_chunk_split_kernel<DS, RB, SPT, float>), g2, dim3(cpb * P), lds, s, D, Lw,
                  (const float*)xz, (const float*)conv, (const float*)delta, ssm_state, (float*)y,
-                 lanes, T);
+                 lanes, T, cpb);
   } else if (bf16 && D.r == RB)
     BOA_LAUNCH((scan_chunk_sload_kernel<DS, RB, true, uint16_t>), grid, dim3(bs), 0, s, D, Lw,
                (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,

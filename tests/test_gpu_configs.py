@@ -62,10 +62,11 @@ def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
 @pytest.mark.parametrize("d,ds,prec", [(64, 16, "fp32"), (80, 16, "fp32"), (256, 16, "fp32"),
                                        (64, 16, "bf16"), (256, 16, "bf16"), (512, 32, "bf16")])
 def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
-    """The compress scan reads its delta rows through LDS on small grids (under
-    two waves per SIMD) and through scalar loads otherwise: the same lanes'
-    logits are bit-identical between a small and a large batch, and (fp32)
-    equal to the oracle's."""
+    """The compress scan splits each channel's states over four-state thread
+    groups on small grids (under two waves per SIMD) and runs one thread per
+    channel with scalar-loaded delta rows otherwise: the same lanes' logits
+    are bit-identical between a small and a large batch, and (fp32) equal to
+    the oracle's."""
     import boa_hip
     torch = torch_dev
     w = make_weights(d, 1, ds)
