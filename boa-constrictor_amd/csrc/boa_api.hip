@@ -359,6 +359,16 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
   if (!e)
     e = timed(c, BOA_K_LN, 2.0 * 2 * rows * D.d,
               [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, true, s); });
+  // d_model 256: FF1 + GELU + FF2 in one kernel, the hidden layer kept in
+  // LDS (MI355X, C3 probe: bf16 GEMMs 131.9 -> 125.1 ms, compress 17.52 ->
+  // 18.07 MB/s).  At d_model 512 the fused form, with 64-row blocks that
+  // re-read both weight matrices per block, was slower (553 -> 707 ms).
+  if (D.d == 256) {
+    if (e) return e;
+    const FfnB16Args f{(const uint16_t*)c->xn, B.w1, B.w2, W.b1, W.b2, c->x, c->x,
+                       l == D.L - 1 ? (uint16_t*)c->y : nullptr, rows, D.d};
+    return timed(c, BOA_K_GEMM, 2.0 * rows * 8.0 * D.d * D.d, [&] { return ffn_bf16(f, s); });
+  }
   if (!e) e = gemmb(c, c->xn, B.w1, c->hid, 4 * D.d, true, nullptr, W.b1, nullptr, 0, rows, 4 * D.d,
                     D.d, ACT_GELU);
   if (!e)

@@ -128,6 +128,22 @@ struct GemmB16Args {
   int M, N, K, act;
 };
 hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s);
+// FF1 + GELU + FF2 (+ b2 + residual) of the bf16 compress pass in one kernel:
+// X bf16 [M][D] (LN2's output), W1 bf16 [4D][D], W2 bf16 [D][4D] (the
+// gemm_bf16 layouts), res and C fp32 [M][D] (may alias), C2 an optional bf16
+// copy of C.  D = 256.
+struct FfnB16Args {
+  const uint16_t* X;
+  const uint16_t* W1;
+  const uint16_t* W2;
+  const float* b1;
+  const float* b2;
+  const float* res;
+  float* C;
+  uint16_t* C2;
+  int M, D;
+};
+hipError_t ffn_bf16(const FfnB16Args& a, hipStream_t s);
 hipError_t launch_b16_weight_nk(const float* w, int ldw_in, int N, int K, int n_pad, uint16_t* out,
                                 hipStream_t s);
 

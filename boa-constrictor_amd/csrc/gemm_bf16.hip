@@ -215,6 +215,195 @@ hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s) {
   return launch_b16<128, 64, 4, 2, 64>(a, s);
 }
 
+// ------------------------------------------------------ FF1 + GELU + FF2
+// The feed-forward pair in one kernel: a block of 1024 threads owns BM rows
+// and keeps their FF2 accumulators (BM x D fp32) in registers while the
+// hidden layer passes through LDS HC columns at a time:
+//   h = bf16(gelu(x . W1[c]^T + b1[c]))   (HC hidden columns of chunk c)
+//   acc += h . W2[:, c]^T
+// then acc + b2 + residual.  The hidden layer (4 D bf16 per row) never
+// reaches HBM.  Every MFMA chain is the unfused GEMMs' (k-steps of 32 in
+// ascending order from 0, k = 32 s + 8 g + e in operand slot (g, e); FF2's
+// chain continues from chunk to chunk), and both epilogues are theirs, so
+// the bits are those of gemm_bf16(FF1, GELU) + gemm_bf16(FF2).
+// LDS rows are K-contiguous bf16 with 8 elements of padding.
+template <int D, int BM, int HC, int WM2, int WN2, int WM1, int WN1>
+__global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
+  constexpr int H = 4 * D;
+  constexpr int XP = D + 8, HP = HC + 8;
+  constexpr int NC = H / HC;
+  constexpr int TM2 = BM / WM2 / 16, TN2 = D / WN2 / 16;    // FF2 tiles per wave
+  constexpr int TM1 = BM / WM1 / 16, TN1 = HC / WN1 / 16;   // FF1 tiles per wave
+  static_assert(WM2 * WN2 == 16 && WM1 * WN1 <= 16, "16 waves");
+  static_assert(TM2 >= 1 && TN2 >= 1 && TM1 >= 1 && TN1 >= 1, "tile shapes");
+  constexpr int XQ = BM * D / 8, W1Q = HC * D / 8, W2Q = D * HC / 8;  // 16-byte chunks
+  constexpr int XL = (XQ + 1023) / 1024, W1L = (W1Q + 1023) / 1024, W2L = (W2Q + 1023) / 1024;
+  __shared__ __attribute__((aligned(16))) uint16_t xs[BM * XP];
+  __shared__ __attribute__((aligned(16))) uint16_t w1s[HC * XP];
+  __shared__ __attribute__((aligned(16))) uint16_t hs[BM * HP];
+  __shared__ __attribute__((aligned(16))) uint16_t w2s[D * HP];
+  __shared__ float b1s[HC], b2s[D];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const int m_blk = blockIdx.x * BM;
+
+  // the block's rows and b2
+#pragma unroll
+  for (int it = 0; it < XL; ++it) {
+    const int q = tid + it * 1024;
+    if (XQ % 1024 == 0 || q < XQ) {
+      const int row = q / (D / 8), c8 = q % (D / 8);
+      const int gm = min(m_blk + row, a.M - 1);
+      *reinterpret_cast<u32x4*>(&xs[row * XP + 8 * c8]) =
+          *reinterpret_cast<const u32x4*>(a.X + (size_t)gm * D + 8 * c8);
+    }
+  }
+  for (int c = tid; c < D; c += 1024) b2s[c] = a.b2 ? a.b2[c] : 0.0f;
+
+  u32x4 w1r[W1L], w2r[W2L];
+  float b1r = 0.0f;
+  auto load_chunk = [&](int ch) {
+#pragma unroll
+    for (int it = 0; it < W1L; ++it) {
+      const int q = tid + it * 1024;
+      if (W1Q % 1024 == 0 || q < W1Q) {
+        const int row = q / (D / 8), c8 = q % (D / 8);
+        w1r[it] = *reinterpret_cast<const u32x4*>(a.W1 + (size_t)(ch * HC + row) * D + 8 * c8);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < W2L; ++it) {
+      const int q = tid + it * 1024;
+      if (W2Q % 1024 == 0 || q < W2Q) {
+        const int row = q / (HC / 8), c8 = q % (HC / 8);
+        w2r[it] = *reinterpret_cast<const u32x4*>(a.W2 + (size_t)row * H + ch * HC + 8 * c8);
+      }
+    }
+    if (tid < HC) b1r = a.b1 ? a.b1[ch * HC + tid] : 0.0f;
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int it = 0; it < W1L; ++it) {
+      const int q = tid + it * 1024;
+      if (W1Q % 1024 == 0 || q < W1Q)
+        *reinterpret_cast<u32x4*>(&w1s[(q / (D / 8)) * XP + 8 * (q % (D / 8))]) = w1r[it];
+    }
+#pragma unroll
+    for (int it = 0; it < W2L; ++it) {
+      const int q = tid + it * 1024;
+      if (W2Q % 1024 == 0 || q < W2Q)
+        *reinterpret_cast<u32x4*>(&w2s[(q / (HC / 8)) * HP + 8 * (q % (HC / 8))]) = w2r[it];
+    }
+    if (tid < HC) b1s[tid] = b1r;
+  };
+
+  // FF2 accumulators: wave (wm2, wn2) owns rows 16 TM2 wm2 + 16 p + j, features
+  // 16 TN2 wn2 + 16 q + 4 g + v
+  const int wm2 = wave / WN2, wn2 = wave % WN2;
+  const int wm1 = wave / WN1, wn1 = wave % WN1;
+  const bool ff1_wave = wave < WM1 * WN1;
+  floatx4 acc2[TM2][TN2];
+#pragma unroll
+  for (int p = 0; p < TM2; ++p)
+#pragma unroll
+    for (int q = 0; q < TN2; ++q) acc2[p][q] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  load_chunk(0);
+  for (int ch = 0; ch < NC; ++ch) {
+    __syncthreads();  // the previous chunk's w1s, hs and w2s are no longer read
+    store_chunk();
+    if (ch + 1 < NC) load_chunk(ch + 1);
+    __syncthreads();
+    // FF1 on chunk ch: hidden columns ch HC + 16 TN1 wn1 + 16 q + 4 g + v
+    if (ff1_wave) {
+      floatx4 acc1[TM1][TN1];
+#pragma unroll
+      for (int p = 0; p < TM1; ++p)
+#pragma unroll
+        for (int q = 0; q < TN1; ++q) acc1[p][q] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) {
+        bf16x8 af[TN1], bf[TM1];
+#pragma unroll
+        for (int q = 0; q < TN1; ++q)
+          af[q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                                 &w1s[(16 * (TN1 * wn1 + q) + j) * XP + 32 * ks + 8 * g]));
+#pragma unroll
+        for (int p = 0; p < TM1; ++p)
+          bf[p] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                                 &xs[(16 * (TM1 * wm1 + p) + j) * XP + 32 * ks + 8 * g]));
+#pragma unroll
+        for (int p = 0; p < TM1; ++p)
+#pragma unroll
+          for (int q = 0; q < TN1; ++q)
+            acc1[p][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[q], bf[p], acc1[p][q], 0, 0, 0);
+      }
+#pragma unroll
+      for (int p = 0; p < TM1; ++p)
+#pragma unroll
+        for (int q = 0; q < TN1; ++q) {
+          const int n = 16 * (TN1 * wn1 + q) + 4 * g;
+          uint16_t o[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) o[v] = f32_to_bf16(gelu<MATH_HW>(acc1[p][q][v] + b1s[n + v]));
+          *reinterpret_cast<ushort4*>(&hs[(16 * (TM1 * wm1 + p) + j) * HP + n]) =
+              make_ushort4(o[0], o[1], o[2], o[3]);
+        }
+    }
+    __syncthreads();
+    // FF2's k-steps of chunk ch
+#pragma unroll
+    for (int ks = 0; ks < HC / 32; ++ks) {
+      bf16x8 af[TN2], bf[TM2];
+#pragma unroll
+      for (int q = 0; q < TN2; ++q)
+        af[q] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                               &w2s[(16 * (TN2 * wn2 + q) + j) * HP + 32 * ks + 8 * g]));
+#pragma unroll
+      for (int p = 0; p < TM2; ++p)
+        bf[p] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                                               &hs[(16 * (TM2 * wm2 + p) + j) * HP + 32 * ks + 8 * g]));
+#pragma unroll
+      for (int p = 0; p < TM2; ++p)
+#pragma unroll
+        for (int q = 0; q < TN2; ++q)
+          acc2[p][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[q], bf[p], acc2[p][q], 0, 0, 0);
+    }
+  }
+  // FF2's epilogue: + b2, + residual, fp32 out (and the bf16 copy)
+#pragma unroll
+  for (int p = 0; p < TM2; ++p) {
+    const int m = m_blk + 16 * (TM2 * wm2 + p) + j;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int q = 0; q < TN2; ++q) {
+      const int n = 16 * (TN2 * wn2 + q) + 4 * g;
+      const float4 rv = *reinterpret_cast<const float4*>(a.res + (size_t)m * D + n);
+      const float r4[4] = {rv.x, rv.y, rv.z, rv.w};
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (acc2[p][q][e] + b2s[n + e]) + r4[e];
+      *reinterpret_cast<float4*>(a.C + (size_t)m * D + n) = make_float4(v[0], v[1], v[2], v[3]);
+      if (a.C2)
+        *reinterpret_cast<ushort4*>(a.C2 + (size_t)m * D + n) =
+            make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+    }
+  }
+}
+
+hipError_t ffn_bf16(const FfnB16Args& a, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  const unsigned blocks = (unsigned)((a.M + 127) / 128);
+  switch (a.D) {
+    case 256:
+      BOA_LAUNCH((ffn_bf16_kernel<256, 128, 64, 4, 4, 4, 4>), dim3(blocks), dim3(1024), 0, s, a);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // Weight relayout for the bf16 compress GEMM: W [K][ldw_in] fp32 (the fp32
 // compress layout) -> [n_pad][K] bf16, rows n >= N zero.
 __global__ void b16_weight_nk_kernel(const float* __restrict__ w, int ldw_in, int N, int K,
