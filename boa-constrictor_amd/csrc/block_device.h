@@ -54,6 +54,25 @@ __device__ __forceinline__ void state_st4(float4* p, float4 v, bool cached) {
   if (cached) *p = v;
   else st_stream(p, v);
 }
+// bf16 precision keeps the step-layout conv state as four bf16 (8 bytes) per
+// channel and lane: its values are the bf16-rounded in_proj outputs, so the
+// narrow form is exact and halves the state's traffic.
+typedef unsigned short stream_h4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 state_ld4h(const ushort4* p, bool cached) {
+  stream_h4 v;
+  if (cached) {
+    const ushort4 t = *p;
+    v = stream_h4{t.x, t.y, t.z, t.w};
+  } else {
+    v = __builtin_nontemporal_load(reinterpret_cast<const stream_h4*>(p));
+  }
+  return make_float4(bf16_to_f32(v[0]), bf16_to_f32(v[1]), bf16_to_f32(v[2]), bf16_to_f32(v[3]));
+}
+__device__ __forceinline__ void state_st4h(ushort4* p, float4 f, bool cached) {
+  const stream_h4 v{f32_to_bf16(f.x), f32_to_bf16(f.y), f32_to_bf16(f.z), f32_to_bf16(f.w)};
+  if (cached) *p = make_ushort4(v[0], v[1], v[2], v[3]);
+  else __builtin_nontemporal_store(v, reinterpret_cast<stream_h4*>(p));
+}
 __device__ __forceinline__ size_t dblk(int k, int m, int ld) {
   return ((size_t)(k >> 4) * ld + m) * 16 + dperm(k & 15);
 }

@@ -508,10 +508,10 @@ hipError_t ensure_state_layout(boa_ctx* c, int want_step) {
     hipError_t e = want_step
         ? launch_state_relayout(conv_state_of(c, l), ssm_state_of(c, l), dec_conv_of(c, l),
                                 dec_ssm_of(c, l), c->cfg.max_lanes, D.di, D.ds, c->ld_dec, true,
-                                c->stream)
+                                c->bf16, c->stream)
         : launch_state_relayout(dec_conv_of(c, l), dec_ssm_of(c, l), conv_state_of(c, l),
                                 ssm_state_of(c, l), c->cfg.max_lanes, D.di, D.ds, c->ld_dec, false,
-                                c->stream);
+                                c->bf16, c->stream);
     if (e) return e;
   }
   c->state_mode = want_step;
@@ -712,7 +712,8 @@ hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* 
     const LayerW& W = c->layers[l];
     const boa_ctx::DecW& DW = c->dlayers[l];
     const boa_ctx::B16W& B = c->b16d[l];
-    float* conv = dec_conv_of(c, l) + (size_t)lane0 * 4;
+    // the conv state of bf16 is four bf16 (two floats' bytes) per channel and lane
+    float* conv = dec_conv_of(c, l) + (size_t)lane0 * 2;
     float* ssm = dec_ssm_of(c, l) + (size_t)lane0 * 64;
     const bool cached = l < n_cached;
     e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {

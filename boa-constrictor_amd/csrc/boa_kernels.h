@@ -272,9 +272,11 @@ hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_
 
 // chunk layout: conv [lane][c][4], ssm [lane][c][n]; step layout: conv
 // [c][lane][4], ssm [c/16][n/4][lane][c%16][n%4] with lane stride ld_state.
+// conv_b16: the step-layout conv state is four bf16 per channel and lane
+// (bf16 precision), else four floats
 hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, float* conv_out,
                                  float* ssm_out, int lanes, int di, int ds, int ld_state,
-                                 bool to_step, hipStream_t s);
+                                 bool to_step, bool conv_b16, hipStream_t s);
 
 // CDF + coder kernels.
 hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,

@@ -1081,25 +1081,39 @@ hipError_t launch_dec_scan(const Dims& D, const LayerW& Lw, const float* na_q, c
 // --------------------------------------------------- state layout changes
 // chunk layout: conv [lane][c][4], ssm [lane][c][n]
 // step layout:  conv [c][lane][4], ssm [c/16][n/4][lane][c%16][n%4] (lane stride ld_state)
+// (bf16 precision: the step-layout conv state is four bf16 per channel and
+// lane, see state_ld4h)
 __global__ void state_to_step_kernel(const float* conv_in, const float* ssm_in, float* conv_out,
-                                     float* ssm_out, int lanes, int di, int ds, int ld_state) {
+                                     float* ssm_out, int lanes, int di, int ds, int ld_state,
+                                     int conv_b16) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= lanes * di) return;
   const int b = idx / di, c = idx % di;
-  reinterpret_cast<float4*>(conv_out)[(size_t)c * ld_state + b] =
-      reinterpret_cast<const float4*>(conv_in)[idx];
+  const float4 cv = reinterpret_cast<const float4*>(conv_in)[idx];
+  if (conv_b16)
+    reinterpret_cast<ushort4*>(conv_out)[(size_t)c * ld_state + b] =
+        make_ushort4(f32_to_bf16(cv.x), f32_to_bf16(cv.y), f32_to_bf16(cv.z), f32_to_bf16(cv.w));
+  else
+    reinterpret_cast<float4*>(conv_out)[(size_t)c * ld_state + b] = cv;
   for (int n = 0; n < ds; ++n)
     ssm_out[((((size_t)(c >> 4) * (ds >> 2) + (n >> 2)) * ld_state + b) * 16 + (c & 15)) * 4 +
             (n & 3)] = ssm_in[(size_t)idx * ds + n];
 }
 
 __global__ void state_to_chunk_kernel(const float* conv_in, const float* ssm_in, float* conv_out,
-                                      float* ssm_out, int lanes, int di, int ds, int ld_state) {
+                                      float* ssm_out, int lanes, int di, int ds, int ld_state,
+                                      int conv_b16) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= lanes * di) return;
   const int b = idx / di, c = idx % di;
-  reinterpret_cast<float4*>(conv_out)[idx] =
-      reinterpret_cast<const float4*>(conv_in)[(size_t)c * ld_state + b];
+  if (conv_b16) {
+    const ushort4 h = reinterpret_cast<const ushort4*>(conv_in)[(size_t)c * ld_state + b];
+    reinterpret_cast<float4*>(conv_out)[idx] =
+        make_float4(bf16_to_f32(h.x), bf16_to_f32(h.y), bf16_to_f32(h.z), bf16_to_f32(h.w));
+  } else {
+    reinterpret_cast<float4*>(conv_out)[idx] =
+        reinterpret_cast<const float4*>(conv_in)[(size_t)c * ld_state + b];
+  }
   for (int n = 0; n < ds; ++n)
     ssm_out[(size_t)idx * ds + n] =
         ssm_in[((((size_t)(c >> 4) * (ds >> 2) + (n >> 2)) * ld_state + b) * 16 + (c & 15)) * 4 +
@@ -1108,14 +1122,14 @@ __global__ void state_to_chunk_kernel(const float* conv_in, const float* ssm_in,
 
 hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, float* conv_out,
                                  float* ssm_out, int lanes, int di, int ds, int ld_state,
-                                 bool to_step, hipStream_t s) {
+                                 bool to_step, bool conv_b16, hipStream_t s) {
   const int n = lanes * di;
   if (to_step)
     BOA_LAUNCH(state_to_step_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
-                       ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state);
+                       ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state, conv_b16 ? 1 : 0);
   else
     BOA_LAUNCH(state_to_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
-                       ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state);
+                       ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state, conv_b16 ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -80,16 +80,16 @@ __device__ __forceinline__ void dec_b16_epilogue(const DecB16Args& a, const floa
   }
   // bf16 32-blocked output; in_proj runs the conv step on its x half
   uint16_t o[4];
-  if (a.conv_di > 0 && nb < a.conv_di) {
+  if (a.conv_di > 0 && nb < a.conv_di) {  // conv state: four bf16 per channel and lane
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int n = nb + e;
       const float x0 = bf16r(v[e]);  // the compress pass reads xz in bf16
-      float4* st = reinterpret_cast<float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
-      const float4 s0 = state_ld4(st, a.state_cached);
+      ushort4* st = reinterpret_cast<ushort4*>(a.conv_state) + (size_t)n * a.ld_state + m;
+      const float4 s0 = state_ld4h(st, a.state_cached);
       const float4 wv = reinterpret_cast<const float4*>(a.conv_w)[n];
       o[e] = f32_to_bf16(conv_step_value<MATH_HW>(a.conv_b[n], s0, x0, wv));
-      state_st4(st, make_float4(s0.y, s0.z, s0.w, x0), a.state_cached);
+      state_st4h(st, make_float4(s0.y, s0.z, s0.w, x0), a.state_cached);
     }
     *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) = make_ushort4(o[0], o[1], o[2], o[3]);
     return;

@@ -92,6 +92,49 @@ def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
         assert np.array_equal(out[1].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("d,ds,prec", [(256, 16, "fp32"), (256, 16, "bf16"), (512, 32, "bf16")])
+def test_state_carries_across_modes(torch_dev, make_weights, d, ds, prec):
+    """The recurrent state moves between the chunk layout (forward_chunk) and
+    the step layout (step_batch; bf16 keeps its conv state as bf16 there):
+    chunk then steps, and steps then chunk, give the logits of one chunk pass
+    over all tokens, bit for bit."""
+    import boa_hip
+    torch = torch_dev
+    w = make_weights(d, 2, ds)
+    lanes, T1, T2 = 7, 9, 6
+    T = T1 + T2
+    rng = np.random.default_rng(11 + d + ds)
+    tok = rng.integers(0, 256, size=(lanes, T), dtype=np.uint8)
+    c = boa_hip.Codec(d, 2, ds, lanes, 0, precision=prec)
+    c.set_stream(torch.cuda.current_stream().cuda_stream)
+    c.load_weights(w)
+
+    def chunk(t0, t1):
+        out = torch.zeros(lanes * (t1 - t0) * 256, dtype=torch.float32, device="cuda")
+        c.forward_chunk(torch.from_numpy(np.ascontiguousarray(tok[:, t0:t1])).cuda(), lanes,
+                        t1 - t0, out)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().reshape(lanes, t1 - t0, 256)
+
+    def steps(t0, t1):
+        out = []
+        d_s = torch.zeros(lanes * 256, dtype=torch.float32, device="cuda")
+        for t in range(t0, t1):
+            c.step_batch(torch.from_numpy(np.ascontiguousarray(tok[:, t])).cuda(), lanes, d_s, True)
+            torch.cuda.synchronize()
+            out.append(d_s.cpu().numpy().reshape(lanes, 256).copy())
+        return np.stack(out, axis=1)
+
+    c.reset_state(lanes)
+    want = chunk(0, T)
+    c.reset_state(lanes)
+    got = np.concatenate([chunk(0, T1), steps(T1, T)], axis=1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "chunk -> steps"
+    c.reset_state(lanes)
+    got = np.concatenate([steps(0, T1), chunk(T1, T)], axis=1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "steps -> chunk"
+
+
 def _same_container(oracle, w, d, L, ds, data, chunk, lanes, tile=0, temperature=1.0,
                     max_chunks=0):
     m = oracle.Model(w, d, L, ds)
