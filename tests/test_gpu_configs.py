@@ -197,6 +197,14 @@ def test_container_edges(torch_dev, oracle, w_c1, n, chunk, lanes, max_chunks):
     _same_container(oracle, w_c1, 64, 2, 16, data, chunk, lanes=lanes, max_chunks=max_chunks)
 
 
+def test_container_tiles_shorter_than_the_conv(torch_dev, oracle, w_c1):
+    """Tiles of 100 tokens over 403-byte chunks end with a 2-token tile: the
+    conv reads its inputs and writes its state across tile boundaries,
+    including tiles shorter than its 4 taps."""
+    data = synth.gen_c1()[:6 * 403]
+    _same_container(oracle, w_c1, 64, 2, 16, data, 403, lanes=3, tile=100)
+
+
 def test_container_4096_lanes(torch_dev, oracle, w_c1):
     """C4's lane count (4096 chunks decoded in one batch) at a short chunk."""
     data = synth.gen_c4(4096 * 40 + 17)
