@@ -68,8 +68,11 @@ def np_forward(tensors, tokens, d, L, ds):
     return hh @ t["head.2.weight"].T + t["head.2.bias"]
 
 
-@pytest.mark.parametrize("d,L,ds", [(64, 2, 16), (32, 1, 32)])
+@pytest.mark.parametrize("d,L,ds", [(64, 2, 16), (32, 1, 32), (80, 1, 16), (256, 2, 16),
+                                    (512, 1, 32)])
 def test_forward_matches_float64_restatement(oracle, weights_dir, d, L, ds):
+    """Up to C2's width (K = 1024 in FF2) and C5's (d_model 512, d_state 32,
+    K = 2048), and d_model 80 (dt_rank 5, rows not a multiple of 32)."""
     tensors = synth.random_weight_tensors(d, L, ds, seed=1)
     path = weights_dir / f"np_{d}_{L}_{ds}.bin"
     synth.write_weights(str(path), tensors)
