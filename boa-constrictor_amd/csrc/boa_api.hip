@@ -308,11 +308,25 @@ float* ssm_state_of(boa_ctx* c, int l) {
   return c->ssm_state + (size_t)l * c->cfg.max_lanes * c->D.di * c->D.ds;
 }
 
+#ifndef BOA_LN_FUSE
+#define BOA_LN_FUSE 1
+#endif
+
 hipError_t gemm(boa_ctx* c, const float* X, int ldx, const float* W, int ldw, float* C, int ldc,
                 const float* bias, const float* res, int ldr, int M, int N, int K, int act) {
   GemmArgs a{X, ldx, W, ldw, C, ldc, bias, res, ldr, M, N, K, act};
   const int cls = gemm_f32_config(a) == 0 ? BOA_K_GEMM : BOA_K_GEMM_SMALL;
   return timed(c, cls, 2.0 * M * N * K, [&] { return gemm_f32(a, c->stream); });
+}
+
+// A 256-wide fp32 GEMM with the next LayerNorm in its epilogue (mode 1: LN1
+// of acc + bias + res, which also goes to C; mode 2: LN2 of acc + bias).
+hipError_t gemm_ln(boa_ctx* c, const float* X, int ldx, const float* W, int ldw, float* C, int ldc,
+                   const float* bias, const float* res, int ldr, int M, int K, const float* ln_w,
+                   const float* ln_b, float* out, int mode) {
+  GemmArgs a{X, ldx, W, ldw, C, ldc, bias, res, ldr, M, 256, K, ACT_NONE};
+  const LnEpi ln{ln_w, ln_b, out, 256, mode};
+  return timed(c, BOA_K_GEMM, 2.0 * M * 256 * K, [&] { return gemm_f32_ln(a, ln, c->stream); });
 }
 
 // bf16 GEMM of the compress pass: X bf16 [M][K], W bf16 [N_pad][K].
@@ -387,13 +401,19 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
   hipStream_t s = c->stream;
   hipError_t e;
   const double ln_bytes = 3.0 * 4 * rows * D.d;
-  e = timed(c, BOA_K_LN, ln_bytes, [&] {
-    return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
-                               false, s)
-                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
-                               W.ln1_b, rows, D.d, false, s);
-  });
-  if (e) return e;
+  // d_model 256 in 128 x 256 tiles: LN2 runs in out_proj's epilogue and the
+  // next layer's LN1 in FF2's (the rows are whole in one block)
+  const bool fuse_ln = BOA_LN_FUSE && D.d == 256 && gemm_f32_config(GemmArgs{
+      nullptr, 0, nullptr, 0, nullptr, 0, nullptr, nullptr, 0, rows, 256, 256, ACT_NONE}) == 0;
+  if (l == 0 || !fuse_ln) {
+    e = timed(c, BOA_K_LN, ln_bytes, [&] {
+      return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
+                                 false, s)
+                    : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn,
+                                 W.ln1_w, W.ln1_b, rows, D.d, false, s);
+    });
+    if (e) return e;
+  }
   if ((e = gemm(c, c->xn, D.d, W.w_in, D.ld_in, c->xz, 2 * D.di, W.b_in, nullptr, 0, rows,
                 2 * D.di, D.d, ACT_NONE)))
     return e;
@@ -413,15 +433,26 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
                              false, s);
   });
   if (e) return e;
-  if ((e = gemm(c, c->y, D.di, W.w_out, D.ld_out, c->xn, D.d, W.b_out, nullptr, 0, rows, D.d, D.di,
-                ACT_NONE)))
-    return e;
-  e = timed(c, BOA_K_LN, ln_bytes,
-            [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, false, s); });
-  if (e) return e;
+  if (fuse_ln) {
+    if ((e = gemm_ln(c, c->y, D.di, W.w_out, D.ld_out, nullptr, 0, W.b_out, nullptr, 0, rows, D.di,
+                     W.ln2_w, W.ln2_b, c->xn, 2)))
+      return e;
+  } else {
+    if ((e = gemm(c, c->y, D.di, W.w_out, D.ld_out, c->xn, D.d, W.b_out, nullptr, 0, rows, D.d,
+                  D.di, ACT_NONE)))
+      return e;
+    e = timed(c, BOA_K_LN, ln_bytes,
+              [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, false, s); });
+    if (e) return e;
+  }
   if ((e = gemm(c, c->xn, D.d, W.w1, D.ld_1, c->hid, 4 * D.d, W.b1, nullptr, 0, rows, 4 * D.d, D.d,
                 ACT_GELU)))
     return e;
+  if (fuse_ln && l + 1 < D.L) {
+    const LayerW Wn = layer_at(c, l + 1);
+    return gemm_ln(c, c->hid, 4 * D.d, W.w2, D.ld_2, c->x, D.d, W.b2, c->x, D.d, rows, 4 * D.d,
+                   Wn.ln1_w, Wn.ln1_b, c->xn, 1);
+  }
   return gemm(c, c->hid, 4 * D.d, W.w2, D.ld_2, c->x, D.d, W.b2, c->x, D.d, rows, D.d, 4 * D.d,
               ACT_NONE);
 }

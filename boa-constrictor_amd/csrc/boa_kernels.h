@@ -72,6 +72,18 @@ struct CdfEpi {
   uint2* lowprob;           // [M] (low, prob) of the next byte per row
 };
 hipError_t gemm_f32_head_cdf(const GemmArgs& a, const CdfEpi& cdf, hipStream_t s);
+// A 256-wide GEMM (out_proj, FF2 at d_model 256) with the following
+// LayerNorm in its epilogue: LN2 (sequential per-row sums) of acc + bias, or
+// LN1 (the 32-lane tree) of acc + bias + residual, whose un-normalised rows
+// are also stored to C (the residual stream).  The normalised rows go to out.
+struct LnEpi {
+  const float* w;
+  const float* b;
+  float* out;
+  int ldo;
+  int mode;  // 1 = LN1, 2 = LN2
+};
+hipError_t gemm_f32_ln(const GemmArgs& a, const LnEpi& ln, hipStream_t s);
 // Tile configuration gemm_f32 picks: 0 = 128x256 (bulk GEMMs of a compress
 // tile), 1 = 128x64 (narrow compress GEMMs), 2 = 32x32 (decode-step sizes).
 int gemm_f32_config(const GemmArgs& a);

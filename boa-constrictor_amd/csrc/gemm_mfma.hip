@@ -29,6 +29,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // block's logits rows go to LDS, and each row's (low, prob) pair of the
 // next input byte is computed there (cdf_targets_kernel's work).
 constexpr int ACT_CDF = 3;
+// Epilogue modes of a 256-wide GEMM followed by a LayerNorm (see gemm_f32_ln).
+constexpr int ACT_LN1 = 4, ACT_LN2 = 5;
 
 // Eight waves per SIMD (64 VGPRs): two 16-wave blocks share a CU.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int ACT>
@@ -36,7 +38,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
 void gemm_f32_kernel(
     const float* __restrict__ X, int ldx, const float* __restrict__ W, int ldw, float* C, int ldc,
     const float* __restrict__ bias, const float* res, int ldr, int M, int N, int K,
-    int vec_store, int swizzle, CdfEpi cdf) {
+    int vec_store, int swizzle, CdfEpi cdf, LnEpi ln) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -49,7 +51,7 @@ void gemm_f32_kernel(
   // same words for the block's logits rows (stride LS)
   constexpr int LS = BN + 4;
   constexpr int MAIN = 2 * BM * XS + 2 * BK * WS;
-  constexpr int EPI = ACT == ACT_CDF ? BM * LS : 0;
+  constexpr int EPI = ACT == ACT_CDF ? BM * LS : ((ACT == ACT_LN1 || ACT == ACT_LN2) ? 64 * (BN + 3) : 0);
   __shared__ __attribute__((aligned(16))) float smem[MAIN > EPI ? MAIN : EPI];
   float(*xs)[BM * XS] = reinterpret_cast<float(*)[BM * XS]>(smem);
   float(*ws)[BK * WS] = reinterpret_cast<float(*)[BK * WS]>(smem + 2 * BM * XS);
@@ -178,6 +180,103 @@ void gemm_f32_kernel(
     return;
   }
 
+  if constexpr (ACT == ACT_LN1 || ACT == ACT_LN2) {
+    // Whole 256-feature rows in the block, 64 rows at a time through LDS
+    // (the K loop ended with a barrier, so the tile buffers are free).  Row
+    // stride RS = 257 keeps LN2's thread-per-row reads conflict-free; the
+    // rows' statistics follow the 64 rows.
+    static_assert(BN == 256 && BM == 128 && WAVES_M == 4, "64-row halves of whole rows");
+    constexpr int D = 256, RS = D + 1;
+    float* stat = smem + 64 * RS;
+    for (int half = 0; half < 2; ++half) {
+      if (wm0 / 64 == half) {
+#pragma unroll
+        for (int a = 0; a < TM; ++a) {
+          const int rl = wm0 - 64 * half + a * 16 + j;
+#pragma unroll
+          for (int b = 0; b < TN; ++b) {
+            const int n = wn0 + b * 16 + 4 * g;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) smem[rl * RS + n + e] = acc[a][b][e] + sbias[n + e];
+          }
+        }
+      }
+      __syncthreads();
+      if (ACT == ACT_LN1) {  // + residual; the sum is the residual stream's next value
+#pragma unroll 1
+        for (int it = 0; it < 4; ++it) {
+          const int rl = (tid >> 6) + 16 * it, c = 4 * (tid & 63);
+          const int m = m_blk + 64 * half + rl;
+          if (m < M) {
+            float* v = smem + rl * RS + c;
+            const float4 r = *reinterpret_cast<const float4*>(res + (size_t)m * ldr + c);
+            const float4 o = make_float4(v[0] + r.x, v[1] + r.y, v[2] + r.z, v[3] + r.w);
+            *reinterpret_cast<float4*>(C + (size_t)m * ldc + c) = o;
+            v[0] = o.x; v[1] = o.y; v[2] = o.z; v[3] = o.w;
+          }
+        }
+        __syncthreads();
+        // ln1_kernel's order: half-wave per row, lane l sums l, l+32, ...,
+        // then the shuffle-down tree; lane 0 holds the totals
+        const int hw = tid >> 5, l = tid & 31;
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int row_i = hw + 32 * rr;
+          const float* row = smem + row_i * RS;
+          float sm = 0.0f, sq = 0.0f;
+#pragma unroll
+          for (int e = 0; e < D / 32; ++e) {
+            const float v = row[l + 32 * e];
+            sm = sm + v;
+            sq = sq + v * v;
+          }
+#pragma unroll
+          for (int off = 16; off > 0; off >>= 1) {
+            sm = sm + __shfl_down(sm, off, 32);
+            sq = sq + __shfl_down(sq, off, 32);
+          }
+          if (l == 0) {
+            const float mean = sm / (float)D;
+            const float var = sq / (float)D - mean * mean;
+            stat[2 * row_i] = mean;
+            stat[2 * row_i + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+          }
+        }
+      } else if (tid < 64) {  // ln2_kernel's order: one thread per row, elements in order
+        const float* row = smem + tid * RS;
+        float sm = 0.0f, sq = 0.0f;
+        for (int i = 0; i < D; ++i) {
+          const float e = row[i];
+          sm = sm + e;
+          sq = sq + e * e;
+        }
+        const float mean = sm / (float)D;
+        const float var = sq / (float)D - mean * mean;
+        stat[2 * tid] = mean;
+        stat[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+      }
+      __syncthreads();
+      // normalise: thread t takes columns 4(t % 64) .. +3 of rows t / 64 + 16i
+#pragma unroll 1
+      for (int it = 0; it < 4; ++it) {
+        const int rl = (tid >> 6) + 16 * it, c = 4 * (tid & 63);
+        const int m = m_blk + 64 * half + rl;
+        const float mean = stat[2 * rl], inv_std = stat[2 * rl + 1];
+        const float* v = smem + rl * RS + c;
+        const float4 wv = *reinterpret_cast<const float4*>(ln.w + c);
+        const float4 bv = *reinterpret_cast<const float4*>(ln.b + c);
+        float4 o;
+        o.x = ((v[0] - mean) * inv_std) * wv.x + bv.x;
+        o.y = ((v[1] - mean) * inv_std) * wv.y + bv.y;
+        o.z = ((v[2] - mean) * inv_std) * wv.z + bv.z;
+        o.w = ((v[3] - mean) * inv_std) * wv.w + bv.w;
+        if (m < M) *reinterpret_cast<float4*>(ln.out + (size_t)m * ln.ldo + c) = o;
+      }
+      __syncthreads();  // the next half reuses the rows
+    }
+    return;
+  }
+
   // Epilogue: lane owns C[m][n .. n+3], m = wm0 + a*16 + j, n = wn0 + b*16 + 4g.
 #pragma unroll
   for (int a = 0; a < TM; ++a) {
@@ -224,7 +323,7 @@ static hipError_t launch_cfg(const GemmArgs& a, hipStream_t s, int swizzle = 1) 
 #define BOA_GEMM_GO(ACTv)                                                                     \
   BOA_LAUNCH((gemm_f32_kernel<BM, BN, WM_, WN_, BK, ACTv>), dim3((unsigned)tiles),     \
                      dim3(64 * WM_ * WN_), 0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias,   \
-                     a.res, a.ldr, a.M, a.N, a.K, vec, swizzle, CdfEpi{})
+                     a.res, a.ldr, a.M, a.N, a.K, vec, swizzle, CdfEpi{}, LnEpi{})
   switch (a.act) {
     case ACT_NONE: BOA_GEMM_GO(ACT_NONE); break;
     case ACT_GELU: BOA_GEMM_GO(ACT_GELU); break;
@@ -258,7 +357,28 @@ hipError_t gemm_f32_head_cdf(const GemmArgs& a, const CdfEpi& cdf, hipStream_t s
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
   BOA_LAUNCH((gemm_f32_kernel<BM, BN, 4, 4, 16, ACT_CDF>), dim3((unsigned)tiles), dim3(1024),
                      0, s, a.X, a.ldx, a.W, a.ldw, nullptr, 0, a.bias, nullptr, 0, a.M, a.N, a.K,
-                     0, 1, cdf);
+                     0, 1, cdf, LnEpi{});
+  return hipGetLastError();
+}
+
+hipError_t gemm_f32_ln(const GemmArgs& a, const LnEpi& ln, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.N != 256 || a.K % 16 || a.ldx % 4 || a.ldw < 256 || a.ldw % 4 || !ln.out || !ln.w ||
+      !ln.b || ln.ldo % 4 || ln.ldo < 256 || (ln.mode == 1 && (!a.res || !a.C || a.ldr % 4 ||
+      a.ldc % 4)))
+    return hipErrorInvalidValue;
+  const long long tiles = (a.M + 127) / 128;
+  if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
+  if (ln.mode == 1)
+    BOA_LAUNCH((gemm_f32_kernel<128, 256, 4, 4, 16, ACT_LN1>), dim3((unsigned)tiles), dim3(1024),
+               0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias, a.res, a.ldr, a.M, a.N, a.K, 1, 1,
+               CdfEpi{}, ln);
+  else if (ln.mode == 2)
+    BOA_LAUNCH((gemm_f32_kernel<128, 256, 4, 4, 16, ACT_LN2>), dim3((unsigned)tiles), dim3(1024),
+               0, s, a.X, a.ldx, a.W, a.ldw, a.C, a.ldc, a.bias, a.res, a.ldr, a.M, a.N, a.K, 1, 1,
+               CdfEpi{}, ln);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

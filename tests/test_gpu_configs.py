@@ -92,6 +92,40 @@ def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
         assert np.array_equal(out[1].view(np.uint32), want.view(np.uint32))
 
 
+def test_layernorm_in_gemm_epilogues(torch_dev, oracle, make_weights):
+    """At d_model 256 with 16384 rows or more in a call (128 x 256 GEMM
+    tiles) the fp32 pass runs LN2 in out_proj's epilogue and the next layer's
+    LN1 in FF2's.  Its logits equal, bit for bit, those of the same tokens in
+    short calls (separate LayerNorm kernels), and the oracle's for two lanes."""
+    import boa_hip
+    torch = torch_dev
+    d, L, ds = 256, 2, 16
+    w = make_weights(d, L, ds)
+    lanes, T, Ts = 66, 256, 32  # 16896 rows in one call, 2112 in each short one
+    rng = np.random.default_rng(23)
+    tok = rng.integers(0, 256, size=(lanes, T), dtype=np.uint8)
+    c = boa_hip.Codec(d, L, ds, lanes, 0, precision="fp32")
+    c.set_stream(torch.cuda.current_stream().cuda_stream)
+    c.load_weights(w)
+
+    def chunk(t0, t1):
+        out = torch.zeros(lanes * (t1 - t0) * 256, dtype=torch.float32, device="cuda")
+        c.forward_chunk(torch.from_numpy(np.ascontiguousarray(tok[:, t0:t1])).cuda(), lanes,
+                        t1 - t0, out)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().reshape(lanes, t1 - t0, 256)
+
+    c.reset_state(lanes)
+    whole = chunk(0, T)
+    c.reset_state(lanes)
+    parts = np.concatenate([chunk(t, t + Ts) for t in range(0, T, Ts)], axis=1)
+    c.close()
+    assert np.array_equal(whole.view(np.uint32), parts.view(np.uint32))
+    pick = [0, lanes - 1]
+    want = oracle.Model(w, d, L, ds).new_state(2).forward_chunk(np.ascontiguousarray(tok[pick]))
+    assert np.array_equal(whole[pick].view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("d,ds,prec", [(256, 16, "fp32"), (256, 16, "bf16"), (512, 32, "bf16")])
 def test_state_carries_across_modes(torch_dev, make_weights, d, ds, prec):
     """The recurrent state moves between the chunk layout (forward_chunk) and
