@@ -349,11 +349,17 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
   const boa_ctx::B16W& B = c->b16c[l];
   hipStream_t s = c->stream;
   const double ln_bytes = 3.0 * 4 * rows * D.d;
-  hipError_t e = timed(c, BOA_K_LN, ln_bytes, [&] {
-    return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d, true, s)
-                  : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn, W.ln1_w,
-                               W.ln1_b, rows, D.d, true, s);
-  });
+  // d_model 256 (the fused FF kernel, whole rows per block): LN2 runs in its
+  // prologue and the next layer's LN1 in its epilogue
+  const bool fuse_ln = BOA_LN_FUSE && D.d == 256;
+  hipError_t e = hipSuccess;
+  if (l == 0 || !fuse_ln)
+    e = timed(c, BOA_K_LN, ln_bytes, [&] {
+      return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
+                                 true, s)
+                    : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn,
+                                 W.ln1_w, W.ln1_b, rows, D.d, true, s);
+    });
   if (!e) e = gemmb(c, c->xn, B.w_in, c->xz, 2 * D.di, true, nullptr, W.b_in, nullptr, 0, rows,
                     2 * D.di, D.d, ACT_NONE);
   if (!e)
@@ -370,7 +376,7 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
     });
   if (!e) e = gemmb(c, c->y, B.w_out, c->xn, D.d, true, nullptr, W.b_out, nullptr, 0, rows, D.d,
                     D.di, ACT_NONE);
-  if (!e)
+  if (!e && !fuse_ln)
     e = timed(c, BOA_K_LN, 2.0 * 2 * rows * D.d,
               [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, true, s); });
   // d_model 256: FF1 + GELU + FF2 in one kernel, the hidden layer kept in
@@ -379,8 +385,18 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
   // re-read both weight matrices per block, was slower (553 -> 707 ms).
   if (D.d == 256) {
     if (e) return e;
-    const FfnB16Args f{(const uint16_t*)c->xn, B.w1, B.w2, W.b1, W.b2, c->x, c->x,
-                       l == D.L - 1 ? (uint16_t*)c->y : nullptr, rows, D.d};
+    FfnB16Args f{(const uint16_t*)c->xn, B.w1, B.w2, W.b1, W.b2, c->x, c->x,
+                 l == D.L - 1 ? (uint16_t*)c->y : nullptr, rows, D.d};
+    if (fuse_ln) {
+      f.ln2_w = W.ln2_w;
+      f.ln2_b = W.ln2_b;
+      if (l + 1 < D.L) {
+        const LayerW Wn = layer_at(c, l + 1);
+        f.ln1_w = Wn.ln1_w;
+        f.ln1_b = Wn.ln1_b;
+        f.xn = (uint16_t*)c->xn;
+      }
+    }
     return timed(c, BOA_K_GEMM, 2.0 * rows * 8.0 * D.d * D.d, [&] { return ffn_bf16(f, s); });
   }
   if (!e) e = gemmb(c, c->xn, B.w1, c->hid, 4 * D.d, true, nullptr, W.b1, nullptr, 0, rows, 4 * D.d,

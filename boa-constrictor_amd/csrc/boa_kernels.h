@@ -143,7 +143,9 @@ hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s);
 // FF1 + GELU + FF2 (+ b2 + residual) of the bf16 compress pass in one kernel:
 // X bf16 [M][D] (LN2's output), W1 bf16 [4D][D], W2 bf16 [D][4D] (the
 // gemm_bf16 layouts), res and C fp32 [M][D] (may alias), C2 an optional bf16
-// copy of C.  D = 256.
+// copy of C.  D = 256.  With ln2_w/ln2_b, X is out_proj's output and LN2 is
+// applied to it in the kernel; with xn (may alias X), the next layer's LN1
+// of C (ln1_w, ln1_b) is stored there in bf16.
 struct FfnB16Args {
   const uint16_t* X;
   const uint16_t* W1;
@@ -154,6 +156,11 @@ struct FfnB16Args {
   float* C;
   uint16_t* C2;
   int M, D;
+  const float* ln2_w = nullptr;
+  const float* ln2_b = nullptr;
+  const float* ln1_w = nullptr;
+  const float* ln1_b = nullptr;
+  uint16_t* xn = nullptr;
 };
 hipError_t ffn_bf16(const FfnB16Args& a, hipStream_t s);
 hipError_t launch_b16_weight_nk(const float* w, int ldw_in, int N, int K, int n_pad, uint16_t* out,

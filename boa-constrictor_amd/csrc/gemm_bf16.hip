@@ -227,7 +227,13 @@ hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s) {
 // chain continues from chunk to chunk), and both epilogues are theirs, so
 // the bits are those of gemm_bf16(FF1, GELU) + gemm_bf16(FF2).
 // LDS rows are K-contiguous bf16 with 8 elements of padding.
-template <int D, int BM, int HC, int WM2, int WN2, int WM1, int WN1>
+// LNF bit 1: the block's rows of X are out_proj's output and LN2 runs on them
+// in LDS before FF1, in ln2_kernel's order (one thread per row, elements in
+// order, statistics from the bf16 values) and with its bf16 rounding of the
+// result.  LNF bit 2: the fp32 output rows also pass through LDS, where the
+// next layer's LN1 runs in ln1_kernel's order (half-wave per row, the
+// 32-lane tree) and stores xn in bf16.
+template <int D, int BM, int HC, int WM2, int WN2, int WM1, int WN1, int LNF>
 __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
   constexpr int H = 4 * D;
   constexpr int XP = D + 8, HP = HC + 8;
@@ -238,11 +244,20 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
   static_assert(TM2 >= 1 && TN2 >= 1 && TM1 >= 1 && TN1 >= 1, "tile shapes");
   constexpr int XQ = BM * D / 8, W1Q = HC * D / 8, W2Q = D * HC / 8;  // 16-byte chunks
   constexpr int XL = (XQ + 1023) / 1024, W1L = (W1Q + 1023) / 1024, W2L = (W2Q + 1023) / 1024;
-  __shared__ __attribute__((aligned(16))) uint16_t xs[BM * XP];
-  __shared__ __attribute__((aligned(16))) uint16_t w1s[HC * XP];
-  __shared__ __attribute__((aligned(16))) uint16_t hs[BM * HP];
-  __shared__ __attribute__((aligned(16))) uint16_t w2s[D * HP];
+  // one LDS buffer: the K loop's xs, w1s, hs, w2s; after it, the LN1
+  // epilogue's fp32 rows (stride RS)
+  constexpr int XS_B = BM * XP * 2, W1S_B = HC * XP * 2, HS_B = BM * HP * 2, W2S_B = D * HP * 2;
+  constexpr int MAIN_B = XS_B + W1S_B + HS_B + W2S_B;
+  constexpr int RS = D + 4;
+  constexpr int EPI_B = (LNF & 2) ? BM * RS * 4 : 0;
+  static_assert(XS_B % 16 == 0 && W1S_B % 16 == 0 && HS_B % 16 == 0, "16-byte aligned parts");
+  __shared__ __attribute__((aligned(16))) unsigned char smem[MAIN_B > EPI_B ? MAIN_B : EPI_B];
+  uint16_t* const xs = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* const w1s = reinterpret_cast<uint16_t*>(smem + XS_B);
+  uint16_t* const hs = reinterpret_cast<uint16_t*>(smem + XS_B + W1S_B);
+  uint16_t* const w2s = reinterpret_cast<uint16_t*>(smem + XS_B + W1S_B + HS_B);
   __shared__ float b1s[HC], b2s[D];
+  __shared__ float lnst[2 * BM];  // LN2: per-row (mean, 1 / std)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, j = lane & 15;
@@ -310,6 +325,57 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
     for (int q = 0; q < TN2; ++q) acc2[p][q] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   load_chunk(0);
+  if constexpr ((LNF & 1) != 0) {
+    // LN2 in place in xs while chunk 0's weights load (splitting the sums
+    // and the sums of squares over two waves measured the same)
+    __syncthreads();
+    if (tid < BM) {
+      const uint16_t* row = xs + tid * XP;
+      float sm = 0.0f, sq = 0.0f;
+      for (int c8 = 0; c8 < D / 8; ++c8) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(row + 8 * c8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = u2f(w[e] << 16), hi = u2f(w[e] & 0xFFFF0000u);
+          sm = sm + lo;
+          sq = sq + lo * lo;
+          sm = sm + hi;
+          sq = sq + hi * hi;
+        }
+      }
+      const float mean = sm / (float)D;
+      const float var = sq / (float)D - mean * mean;
+      lnst[2 * tid] = mean;
+      lnst[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < XL; ++it) {
+      const int q = tid + it * 1024;
+      if (XQ % 1024 == 0 || q < XQ) {
+        const int row = q / (D / 8), c8 = q % (D / 8);
+        u32x4* px = reinterpret_cast<u32x4*>(&xs[row * XP + 8 * c8]);
+        const u32x4 w = *px;
+        const float mean = lnst[2 * row], inv_std = lnst[2 * row + 1];
+        const float4 wa = *reinterpret_cast<const float4*>(a.ln2_w + 8 * c8);
+        const float4 wb = *reinterpret_cast<const float4*>(a.ln2_w + 8 * c8 + 4);
+        const float4 ba = *reinterpret_cast<const float4*>(a.ln2_b + 8 * c8);
+        const float4 bb = *reinterpret_cast<const float4*>(a.ln2_b + 8 * c8 + 4);
+        const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = u2f(w[e] << 16), hi = u2f(w[e] & 0xFFFF0000u);
+          const uint32_t ol = f32_to_bf16(((lo - mean) * inv_std) * wv[2 * e] + bv[2 * e]);
+          const uint32_t oh = f32_to_bf16(((hi - mean) * inv_std) * wv[2 * e + 1] + bv[2 * e + 1]);
+          o[e] = ol | (oh << 16);
+        }
+        *px = o;
+      }
+    }
+    // the chunk loop's first barrier orders these stores before FF1's reads
+  }
   for (int ch = 0; ch < NC; ++ch) {
     __syncthreads();  // the previous chunk's w1s, hs and w2s are no longer read
     store_chunk();
@@ -372,9 +438,12 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
     }
   }
   // FF2's epilogue: + b2, + residual, fp32 out (and the bf16 copy)
+  float* const rows = reinterpret_cast<float*>(smem);
+  if constexpr ((LNF & 2) != 0) __syncthreads();  // every wave is past its last reads of hs, w2s
 #pragma unroll
   for (int p = 0; p < TM2; ++p) {
-    const int m = m_blk + 16 * (TM2 * wm2 + p) + j;
+    const int rl = 16 * (TM2 * wm2 + p) + j;
+    const int m = m_blk + rl;
     if (m >= a.M) continue;
 #pragma unroll
     for (int q = 0; q < TN2; ++q) {
@@ -385,9 +454,62 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = (acc2[p][q][e] + b2s[n + e]) + r4[e];
       *reinterpret_cast<float4*>(a.C + (size_t)m * D + n) = make_float4(v[0], v[1], v[2], v[3]);
+      if ((LNF & 2) != 0)
+        *reinterpret_cast<float4*>(rows + rl * RS + n) = make_float4(v[0], v[1], v[2], v[3]);
       if (a.C2)
         *reinterpret_cast<ushort4*>(a.C2 + (size_t)m * D + n) =
             make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+    }
+  }
+  if constexpr ((LNF & 2) != 0) {
+    __syncthreads();
+    // the next layer's LN1: half-wave hw takes rows hw, hw + 32, ...; lane l
+    // sums elements l, l + 32, ... in order, then the shuffle-down tree, and
+    // lane 0's totals are broadcast; the normalised rows overwrite the LDS rows
+    const int hw = tid >> 5, l = tid & 31;
+#pragma unroll 1
+    for (int rl = hw; rl < BM; rl += 32) {
+      float* row = rows + rl * RS;
+      float sm = 0.0f, sq = 0.0f;
+#pragma unroll
+      for (int e = 0; e < D / 32; ++e) {
+        const float v = row[l + 32 * e];
+        sm = sm + v;
+        sq = sq + v * v;
+      }
+#pragma unroll
+      for (int off = 16; off > 0; off >>= 1) {
+        sm = sm + __shfl_down(sm, off, 32);
+        sq = sq + __shfl_down(sq, off, 32);
+      }
+      sm = __shfl(sm, 0, 32);
+      sq = __shfl(sq, 0, 32);
+      const float mean = sm / (float)D;
+      const float var = sq / (float)D - mean * mean;
+      const float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
+#pragma unroll
+      for (int e = 0; e < D / 32; ++e) {
+        const int idx = l + 32 * e;
+        row[idx] = ((row[idx] - mean) * inv_std) * a.ln1_w[idx] + a.ln1_b[idx];
+      }
+    }
+    __syncthreads();
+    // bf16 xn, eight features (16 bytes) per store
+#pragma unroll
+    for (int it = 0; it < XL; ++it) {
+      const int q = tid + it * 1024;
+      if (XQ % 1024 == 0 || q < XQ) {
+        const int rl = q / (D / 8), c8 = q % (D / 8);
+        const int m = m_blk + rl;
+        if (m < a.M) {
+          const float* v = rows + rl * RS + 8 * c8;
+          u32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = (uint32_t)f32_to_bf16(v[2 * e]) | ((uint32_t)f32_to_bf16(v[2 * e + 1]) << 16);
+          *reinterpret_cast<u32x4*>(a.xn + (size_t)m * D + 8 * c8) = o;
+        }
+      }
     }
   }
 }
@@ -396,9 +518,19 @@ hipError_t ffn_bf16(const FfnB16Args& a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   const unsigned blocks = (unsigned)((a.M + 127) / 128);
   switch (a.D) {
-    case 256:
-      BOA_LAUNCH((ffn_bf16_kernel<256, 128, 64, 4, 4, 4, 4>), dim3(blocks), dim3(1024), 0, s, a);
+    case 256: {
+      const bool ln2 = a.ln2_w && a.ln2_b, ln1 = a.xn && a.ln1_w && a.ln1_b;
+      if ((a.ln2_w || a.ln2_b) && !ln2) return hipErrorInvalidValue;
+      if ((a.xn || a.ln1_w || a.ln1_b) && !ln1) return hipErrorInvalidValue;
+#define BOA_FFN(F) \
+  BOA_LAUNCH((ffn_bf16_kernel<256, 128, 64, 4, 4, 4, 4, F>), dim3(blocks), dim3(1024), 0, s, a)
+      if (ln2 && ln1) BOA_FFN(3);
+      else if (ln2) BOA_FFN(1);
+      else if (ln1) BOA_FFN(2);
+      else BOA_FFN(0);
+#undef BOA_FFN
       break;
+    }
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

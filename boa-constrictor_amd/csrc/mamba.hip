@@ -224,75 +224,162 @@ hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, 
 
 // ------------------------------------------------------------------ conv1d
 // The conv is no recurrence (an output needs its own input and the three
-// before it), so a thread takes TB consecutive tokens of one channel,
-// reading the three inputs before its block from xz (or, for the first
-// block, from the state).  The first block's thread also writes the new
-// state, the last four inputs of (old state, tile), after having read the
-// old one, so no other thread touches the state.  Against one thread per
+// before it), so a thread takes TB consecutive tokens of CP adjacent
+// channels, reading the three inputs before its block from xz (or, for the
+// first block, from the state).  The first block's thread also writes the
+// new state, the last four inputs of (old state, tile), after having read
+// the old one, so no other thread touches the state.  Against one thread per
 // channel walking the whole tile: C2 probe 27.8 -> 26.4 ms per compress,
-// C1 4.3 -> 0.47 ms (TB 16 and 32 gave the same or less).
-template <typename TA, int TB>
+// C1 4.3 -> 0.47 ms (TB 16 and 32 gave the same or less).  CP: four fp32
+// channels (16-byte accesses; C2 probe 28.9 -> 26.7 ms, two: 29.1) and two
+// bf16 channels (4-byte accesses; C3 probe 41.6 -> 29.9 ms, four: 31.1).
+
+// CP consecutive activations as floats (one 2 CP- or 4 CP-byte access)
+template <int CP>
+__device__ __forceinline__ void ldcp(const float* p, float* v) {
+  if constexpr (CP == 1) {
+    v[0] = *p;
+  } else if constexpr (CP == 2) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x; v[1] = t.y;
+  } else {
+    ld4(p, v);
+  }
+}
+template <int CP>
+__device__ __forceinline__ void ldcp(const uint16_t* p, float* v) {
+  if constexpr (CP == 1) {
+    v[0] = bf16_to_f32(*p);
+  } else if constexpr (CP == 2) {
+    const uint32_t t = *reinterpret_cast<const uint32_t*>(p);
+    v[0] = u2f(t << 16); v[1] = u2f(t & 0xFFFF0000u);
+  } else {
+    ld4(p, v);
+  }
+}
+template <int CP>
+__device__ __forceinline__ void stcp(float* p, const float* v) {
+  if constexpr (CP == 1) {
+    *p = v[0];
+  } else if constexpr (CP == 2) {
+    *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+  } else {
+    st4(p, v);
+  }
+}
+template <int CP>
+__device__ __forceinline__ void stcp(uint16_t* p, const float* v) {
+  if constexpr (CP == 1) {
+    *p = f32_to_bf16(v[0]);
+  } else if constexpr (CP == 2) {
+    *reinterpret_cast<uint32_t*>(p) =
+        (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+  } else {
+    st4(p, v);
+  }
+}
+
+template <typename TA, int TB, int CP>
 __global__ __launch_bounds__(256) void conv_chunk_tp_kernel(const TA* __restrict__ xz,
                                                             float* __restrict__ conv_state,
                                                             const float* __restrict__ w,
                                                             const float* __restrict__ cb,
                                                             TA* __restrict__ out, int lanes, int T,
                                                             int di, int ntb) {
+  const int dq = di / CP;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)lanes * ntb * di) return;
-  const int c = (int)(idx % di);
-  const int64_t rest = idx / di;
+  if (idx >= (int64_t)lanes * ntb * dq) return;
+  const int c = (int)(idx % dq) * CP;
+  const int64_t rest = idx / dq;
   const int tb = (int)(rest % ntb), b = (int)(rest / ntb);
   const int t0 = tb * TB;
-  const float4 wv = reinterpret_cast<const float4*>(w)[c];
-  const float bias = cb[c];
   constexpr int M = sizeof(TA) == 2 ? MATH_HW : MATH_BF;
+  float4 wv[CP];
+  float bias[CP];
+#pragma unroll
+  for (int k = 0; k < CP; ++k) {
+    wv[k] = reinterpret_cast<const float4*>(w)[c + k];
+    bias[k] = cb[c + k];
+  }
   const TA* xp = xz + (size_t)b * T * (2 * di) + c;
   TA* op = out + (size_t)b * T * di + c;
   float4* st = reinterpret_cast<float4*>(conv_state) + (size_t)b * di + c;
-  float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f);
-  float xm3, xm2, xm1;
+  float4 s0[CP];
+  float xm3[CP], xm2[CP], xm1[CP];
   if (tb == 0) {
-    s0 = *st;
-    xm3 = s0.y; xm2 = s0.z; xm1 = s0.w;
+#pragma unroll
+    for (int k = 0; k < CP; ++k) {
+      s0[k] = st[k];
+      xm3[k] = s0[k].y; xm2[k] = s0[k].z; xm1[k] = s0[k].w;
+    }
   } else {  // t0 >= TB >= 3
-    xm3 = ldv(xp + (size_t)(t0 - 3) * 2 * di);
-    xm2 = ldv(xp + (size_t)(t0 - 2) * 2 * di);
-    xm1 = ldv(xp + (size_t)(t0 - 1) * 2 * di);
+    ldcp<CP>(xp + (size_t)(t0 - 3) * 2 * di, xm3);
+    ldcp<CP>(xp + (size_t)(t0 - 2) * 2 * di, xm2);
+    ldcp<CP>(xp + (size_t)(t0 - 1) * 2 * di, xm1);
   }
   const int nt = min(TB, T - t0);
-  float xv[TB];
-#pragma unroll
-  for (int u = 0; u < TB; ++u) xv[u] = u < nt ? ldv(xp + (size_t)(t0 + u) * 2 * di) : 0.0f;
+  float xv[TB][CP];
 #pragma unroll
   for (int u = 0; u < TB; ++u) {
     if (u < nt) {
-      stv(op + (size_t)(t0 + u) * di, conv_value<M>(bias, xm3, xm2, xm1, xv[u], wv));
-      xm3 = xm2; xm2 = xm1; xm1 = xv[u];
+      ldcp<CP>(xp + (size_t)(t0 + u) * 2 * di, xv[u]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CP; ++k) xv[u][k] = 0.0f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < TB; ++u) {
+    if (u < nt) {
+      float o[CP];
+#pragma unroll
+      for (int k = 0; k < CP; ++k) {
+        o[k] = conv_value<M>(bias[k], xm3[k], xm2[k], xm1[k], xv[u][k], wv[k]);
+        xm3[k] = xm2[k]; xm2[k] = xm1[k]; xm1[k] = xv[u][k];
+      }
+      stcp<CP>(op + (size_t)(t0 + u) * di, o);
     }
   }
   if (tb == 0) {
     // the last four of (s0.x, s0.y, s0.z, s0.w, x_0 .. x_{T-1})
-    float q[4] = {s0.x, s0.y, s0.z, s0.w};
     const int k0 = T < 4 ? T : 4;  // inputs of the tile among the last four
-    for (int k = 0; k < 4 - k0; ++k) q[k] = q[k + k0];
-    for (int k = 0; k < k0; ++k) q[4 - k0 + k] = ldv(xp + (size_t)(T - k0 + k) * 2 * di);
-    *st = make_float4(q[0], q[1], q[2], q[3]);
+#pragma unroll
+    for (int k = 0; k < CP; ++k) {
+      float q[4] = {s0[k].x, s0[k].y, s0[k].z, s0[k].w};
+      for (int i = 0; i < 4 - k0; ++i) q[i] = q[i + k0];
+      for (int i = 0; i < k0; ++i) q[4 - k0 + i] = ldv(xp + (size_t)(T - k0 + i) * 2 * di + k);
+      st[k] = make_float4(q[0], q[1], q[2], q[3]);
+    }
   }
 }
+
+#ifndef BOA_CONV_CP_B16
+#define BOA_CONV_CP_B16 2
+#endif
+#ifndef BOA_CONV_CP_F32
+#define BOA_CONV_CP_F32 4
+#endif
 
 hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, const float* cb,
                              void* out, int lanes, int T, int di, bool bf16, hipStream_t s) {
   constexpr int TB = 8;
   const int ntb = (T + TB - 1) / TB;
-  const int64_t n64 = (int64_t)lanes * ntb * di;
   if (T <= 0) return hipSuccess;
-  if (bf16)
-    BOA_LAUNCH((conv_chunk_tp_kernel<uint16_t, TB>), dim3((unsigned)((n64 + 255) / 256)), dim3(256),
-               0, s, (const uint16_t*)xz, conv_state, w, cb, (uint16_t*)out, lanes, T, di, ntb);
-  else
-    BOA_LAUNCH((conv_chunk_tp_kernel<float, TB>), dim3((unsigned)((n64 + 255) / 256)), dim3(256),
-               0, s, (const float*)xz, conv_state, w, cb, (float*)out, lanes, T, di, ntb);
+  if (bf16) {
+    constexpr int CP = BOA_CONV_CP_B16;
+    if (di % CP) return hipErrorInvalidValue;
+    const int64_t n64 = (int64_t)lanes * ntb * (di / CP);
+    BOA_LAUNCH((conv_chunk_tp_kernel<uint16_t, TB, CP>), dim3((unsigned)((n64 + 255) / 256)),
+               dim3(256), 0, s, (const uint16_t*)xz, conv_state, w, cb, (uint16_t*)out, lanes, T,
+               di, ntb);
+  } else {
+    constexpr int CP = BOA_CONV_CP_F32;
+    if (di % CP) return hipErrorInvalidValue;
+    const int64_t n64 = (int64_t)lanes * ntb * (di / CP);
+    BOA_LAUNCH((conv_chunk_tp_kernel<float, TB, CP>), dim3((unsigned)((n64 + 255) / 256)),
+               dim3(256), 0, s, (const float*)xz, conv_state, w, cb, (float*)out, lanes, T, di,
+               ntb);
+  }
   return hipGetLastError();
 }
 
