@@ -230,9 +230,11 @@ hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, 
 // new state, the last four inputs of (old state, tile), after having read
 // the old one, so no other thread touches the state.  Against one thread per
 // channel walking the whole tile: C2 probe 27.8 -> 26.4 ms per compress,
-// C1 4.3 -> 0.47 ms (TB 16 and 32 gave the same or less).  CP: four fp32
-// channels (16-byte accesses; C2 probe 28.9 -> 26.7 ms, two: 29.1) and two
-// bf16 channels (4-byte accesses; C3 probe 41.6 -> 29.9 ms, four: 31.1).
+// C1 4.3 -> 0.47 ms.  A thread takes up to 128 tokens, in condition-free
+// sub-blocks of eight loads in flight, as long as about a million threads
+// remain (against eight tokens per thread: C3 probe 19.2 -> 16.4 ms, C5
+// probe 155 -> 103 ms; C1, C2 the same), and CP adjacent channels: four in
+// fp32 (16-byte accesses), two in bf16 (4-byte accesses).
 
 // CP consecutive activations as floats (one 2 CP- or 4 CP-byte access)
 template <int CP>
@@ -286,6 +288,8 @@ __global__ __launch_bounds__(256) void conv_chunk_tp_kernel(const TA* __restrict
                                                             const float* __restrict__ cb,
                                                             TA* __restrict__ out, int lanes, int T,
                                                             int di, int ntb) {
+  constexpr int SB = 8;  // tokens loaded together
+  static_assert(TB % SB == 0, "whole sub-blocks");
   const int dq = di / CP;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)lanes * ntb * dq) return;
@@ -318,27 +322,33 @@ __global__ __launch_bounds__(256) void conv_chunk_tp_kernel(const TA* __restrict
     ldcp<CP>(xp + (size_t)(t0 - 1) * 2 * di, xm1);
   }
   const int nt = min(TB, T - t0);
-  float xv[TB][CP];
+  int u = 0;
+  // whole sub-blocks: SB loads in flight, no per-token conditions
+#pragma unroll 1
+  for (; u + SB <= nt; u += SB) {
+    float xv[SB][CP];
 #pragma unroll
-  for (int u = 0; u < TB; ++u) {
-    if (u < nt) {
-      ldcp<CP>(xp + (size_t)(t0 + u) * 2 * di, xv[u]);
-    } else {
+    for (int v = 0; v < SB; ++v) ldcp<CP>(xp + (size_t)(t0 + u + v) * 2 * di, xv[v]);
 #pragma unroll
-      for (int k = 0; k < CP; ++k) xv[u][k] = 0.0f;
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < TB; ++u) {
-    if (u < nt) {
+    for (int v = 0; v < SB; ++v) {
       float o[CP];
 #pragma unroll
       for (int k = 0; k < CP; ++k) {
-        o[k] = conv_value<M>(bias[k], xm3[k], xm2[k], xm1[k], xv[u][k], wv[k]);
-        xm3[k] = xm2[k]; xm2[k] = xm1[k]; xm1[k] = xv[u][k];
+        o[k] = conv_value<M>(bias[k], xm3[k], xm2[k], xm1[k], xv[v][k], wv[k]);
+        xm3[k] = xm2[k]; xm2[k] = xm1[k]; xm1[k] = xv[v][k];
       }
-      stcp<CP>(op + (size_t)(t0 + u) * di, o);
+      stcp<CP>(op + (size_t)(t0 + u + v) * di, o);
     }
+  }
+  for (; u < nt; ++u) {  // the tile's last tokens
+    float x0[CP], o[CP];
+    ldcp<CP>(xp + (size_t)(t0 + u) * 2 * di, x0);
+#pragma unroll
+    for (int k = 0; k < CP; ++k) {
+      o[k] = conv_value<M>(bias[k], xm3[k], xm2[k], xm1[k], x0[k], wv[k]);
+      xm3[k] = xm2[k]; xm2[k] = xm1[k]; xm1[k] = x0[k];
+    }
+    stcp<CP>(op + (size_t)(t0 + u) * di, o);
   }
   if (tb == 0) {
     // the last four of (s0.x, s0.y, s0.z, s0.w, x_0 .. x_{T-1})
@@ -359,28 +369,39 @@ __global__ __launch_bounds__(256) void conv_chunk_tp_kernel(const TA* __restrict
 #ifndef BOA_CONV_CP_F32
 #define BOA_CONV_CP_F32 4
 #endif
+#ifndef BOA_CONV_MIN_THREADS
+#define BOA_CONV_MIN_THREADS (1 << 20)
+#endif
+
+template <typename TA, int CP>
+static hipError_t conv_go(const void* xz, float* conv_state, const float* w, const float* cb,
+                          void* out, int lanes, int T, int di, hipStream_t s) {
+  if (di % CP) return hipErrorInvalidValue;
+  // tokens per thread: the most (up to 128) that still leave about a million
+  // threads, which spreads a thread's weight loads and its three-input halo
+  // over more outputs
+  const int64_t per_tb = (int64_t)lanes * (di / CP);
+  int TB = 128;
+  while (TB > 8 && per_tb * ((T + TB - 1) / TB) < BOA_CONV_MIN_THREADS) TB /= 2;
+  const int ntb = (T + TB - 1) / TB;
+  const dim3 grid((unsigned)((per_tb * ntb + 255) / 256)), block(256);
+  const TA* x = (const TA*)xz;
+  TA* o = (TA*)out;
+  switch (TB) {
+    case 128: BOA_LAUNCH((conv_chunk_tp_kernel<TA, 128, CP>), grid, block, 0, s, x, conv_state, w, cb, o, lanes, T, di, ntb); break;
+    case 64: BOA_LAUNCH((conv_chunk_tp_kernel<TA, 64, CP>), grid, block, 0, s, x, conv_state, w, cb, o, lanes, T, di, ntb); break;
+    case 32: BOA_LAUNCH((conv_chunk_tp_kernel<TA, 32, CP>), grid, block, 0, s, x, conv_state, w, cb, o, lanes, T, di, ntb); break;
+    case 16: BOA_LAUNCH((conv_chunk_tp_kernel<TA, 16, CP>), grid, block, 0, s, x, conv_state, w, cb, o, lanes, T, di, ntb); break;
+    default: BOA_LAUNCH((conv_chunk_tp_kernel<TA, 8, CP>), grid, block, 0, s, x, conv_state, w, cb, o, lanes, T, di, ntb); break;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, const float* cb,
                              void* out, int lanes, int T, int di, bool bf16, hipStream_t s) {
-  constexpr int TB = 8;
-  const int ntb = (T + TB - 1) / TB;
   if (T <= 0) return hipSuccess;
-  if (bf16) {
-    constexpr int CP = BOA_CONV_CP_B16;
-    if (di % CP) return hipErrorInvalidValue;
-    const int64_t n64 = (int64_t)lanes * ntb * (di / CP);
-    BOA_LAUNCH((conv_chunk_tp_kernel<uint16_t, TB, CP>), dim3((unsigned)((n64 + 255) / 256)),
-               dim3(256), 0, s, (const uint16_t*)xz, conv_state, w, cb, (uint16_t*)out, lanes, T,
-               di, ntb);
-  } else {
-    constexpr int CP = BOA_CONV_CP_F32;
-    if (di % CP) return hipErrorInvalidValue;
-    const int64_t n64 = (int64_t)lanes * ntb * (di / CP);
-    BOA_LAUNCH((conv_chunk_tp_kernel<float, TB, CP>), dim3((unsigned)((n64 + 255) / 256)),
-               dim3(256), 0, s, (const float*)xz, conv_state, w, cb, (float*)out, lanes, T, di,
-               ntb);
-  }
-  return hipGetLastError();
+  if (bf16) return conv_go<uint16_t, BOA_CONV_CP_B16>(xz, conv_state, w, cb, out, lanes, T, di, s);
+  return conv_go<float, BOA_CONV_CP_F32>(xz, conv_state, w, cb, out, lanes, T, di, s);
 }
 
 // -------------------------------------------------------- selective scan
