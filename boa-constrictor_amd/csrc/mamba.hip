@@ -473,8 +473,10 @@ void scan_chunk_sload_kernel(Dims D, LayerW Lw, const TA* __restrict__ xz,
 
 constexpr int SCAN_TB = 32;  // tokens of delta rows staged in LDS per pass
 
-// Small grids (fewer than two waves per SIMD, e.g. d_model 64 with 64
-// lanes), where one thread per channel leaves most SIMDs idle and every
+// Small grids (under one wave per SIMD, e.g. d_model 64 with 64 lanes;
+// the warm-start C2 probe's 250 lanes x 512 channels ran at 4.08 MB/s split
+// against 4.85 with one thread per channel, its 125 lanes at 3.99 against
+// 3.76), where one thread per channel leaves most SIMDs idle and every
 // token's latency exposed: P = DS / SPT threads share a channel, each owning
 // SPT states, and the delta rows are staged in LDS SCAN_TB tokens at a time.
 // Every thread of the group computes the token's dt (the same operations, so
@@ -567,12 +569,16 @@ static int block_for(int di) {
   return 0;
 }
 
+#ifndef BOA_SCAN_SPLIT_BELOW
+#define BOA_SCAN_SPLIT_BELOW (64 * 1024)  // threads: one wave per SIMD
+#endif
+
 template <int DS, int RB>
 static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const void* xz, const void* conv,
                                 const void* delta, float* ssm_state, void* y, int lanes, int T,
                                 int bs, bool bf16, hipStream_t s) {
   const dim3 grid((lanes * D.di) / bs);
-  if ((int64_t)lanes * D.di < 2 * 64 * 1024) {  // under two waves per SIMD
+  if ((int64_t)lanes * D.di < BOA_SCAN_SPLIT_BELOW) {
     const size_t lds = sizeof(float) * SCAN_TB * D.R;
     constexpr int SPT = 4, P = DS / SPT;
     int cpb = 256 / P;  // channels per block: a power of two dividing di

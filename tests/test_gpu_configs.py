@@ -63,7 +63,7 @@ def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
                                        (64, 16, "bf16"), (256, 16, "bf16"), (512, 32, "bf16")])
 def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
     """The compress scan splits each channel's states over four-state thread
-    groups on small grids (under two waves per SIMD) and runs one thread per
+    groups on small grids (under one wave per SIMD) and runs one thread per
     channel with scalar-loaded delta rows otherwise: the same lanes' logits
     are bit-identical between a small and a large batch, and (fp32) equal to
     the oracle's."""
@@ -71,7 +71,7 @@ def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
     torch = torch_dev
     w = make_weights(d, 1, ds)
     di = 2 * d
-    big = -(-2 * 64 * 1024 // di)  # the first lane count on the scalar-load form
+    big = -(-64 * 1024 // di)  # the first lane count on the scalar-load form
     small, T = 6, 20
     rng = np.random.default_rng(7 + d + ds)
     tok = rng.integers(0, 256, size=(big, T), dtype=np.uint8)
