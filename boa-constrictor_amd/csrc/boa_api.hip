@@ -124,6 +124,16 @@ struct boa_ctx {
   uint8_t* tok = nullptr;
   int* t_counter = nullptr;     // decode step counter (device)
 
+  // group-synchronous decode step (dec_group_step_kernel): its plan, a host
+  // copy and a device copy, and one allocation (gaux) holding the per-group
+  // barrier counters, decoded positions and the abort flag; group_step = 0
+  // (the default) runs the launch chain instead
+  int group_step = 0;
+  int n_cus = 0;
+  GroupPlan* h_gplan = nullptr;
+  GroupPlan* d_gplan = nullptr;
+  unsigned* gaux = nullptr;
+
   // decompress: every step is replayed from a HIP graph on dec_stream; the
   // executable graph is kept while the step's launch arguments stay the same
   hipStream_t dec_stream = nullptr;
@@ -136,6 +146,7 @@ struct boa_ctx {
     const uint32_t* payload = nullptr;
     float inv_temp = 0.0f;
     hipStream_t stream = nullptr;
+    bool group = false;
   } dec_key;
   int32_t* h_sizes = nullptr;  // pinned
 
@@ -606,6 +617,80 @@ bool dec_fuse_xproj(const boa_ctx* c, int lanes) {
 // apart against 2.527 fused).
 bool dec_fuse_head(int lanes) { return lanes >= 2048; }
 
+// gaux words: the barrier counters of the 16 lane groups, 64 words (256
+// bytes) apart; the groups' decoded positions; their members' records of
+// the dispatch offset (16 per group); the abort flag
+constexpr int kGauxBar = 0, kGauxTGroup = 16 * 64, kGauxORec = kGauxTGroup + 64,
+              kGauxAbort = kGauxORec + 16 * 16, kGauxWords = kGauxAbort + 64;
+
+// fp32 d_model 256 up to 1024 lanes: every step in one launch of the
+// group-synchronous kernel, which runs the launch chain's fused kernels
+// (LayerNorm and x_proj fused, head.2 with the coder step) as its phases
+bool dec_use_group(const boa_ctx* c, int lanes) {
+  return c->group_step && !c->bf16 && c->d_gplan && dec_group_fits(c->D, lanes, c->n_cus) &&
+         dec_fuse_ln(c, lanes) && dec_fuse_xproj(c, lanes);
+}
+
+// model FLOPs of one decode step (the GEMMs: per layer in_proj, x_proj,
+// out_proj, FF1, FF2; then head.1 and head.2)
+double dec_step_flops(const boa_ctx* c, int lanes) {
+  const Dims& D = c->D;
+  const double layer = (double)D.d * 2 * D.di + (double)D.di * c->n_xdec + (double)D.di * D.d +
+                       2.0 * D.d * 4 * D.d;
+  return 2.0 * lanes * (D.L * layer + (double)D.d * D.d + (double)D.d * VOCAB);
+}
+
+// The group step's plan for lanes [0, lanes): the arguments step_range and
+// decode_steps give the chain's kernels (dgemm's for the plain GEMMs).
+void build_group_plan(boa_ctx* c, int lanes, uint8_t* out, int64_t chunk,
+                      const uint32_t* payload) {
+  const Dims& D = c->D;
+  const int ld = c->ld_dec;
+  GroupPlan& P = *c->h_gplan;
+  P = GroupPlan{};
+  const int n_cached = dec_cached_layers(c, lanes);
+  auto gemm = [&](const float* X, const float* W, float* C, const float* bias, const float* res,
+                  int N, int K, int act) {
+    DecGemmArgs a{};
+    a.Xt = X; a.ldx = ld; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ld;
+    a.bias = bias; a.res = res; a.ldr = ld; a.M = lanes; a.N = N; a.K = K; a.act = act;
+    return a;
+  };
+  for (int l = 0; l < D.L; ++l) {
+    const LayerW& W = c->layers[l];
+    const boa_ctx::DecW& DW = c->dlayers[l];
+    GroupLayerPlan& g = P.layer[l];
+    const bool cached = l < n_cached;
+    DecGemmArgs& a = g.in;  // LN1 + in_proj + conv
+    a.state_cached = cached ? 1 : 0;
+    a.Xt = c->dxt; a.ldx = ld; a.W = DW.w_in; a.ldw = 2 * D.di; a.C = c->dzt; a.ldc = ld;
+    a.bias = W.b_in; a.M = lanes; a.N = 2 * D.di; a.K = D.d; a.act = ACT_NONE;
+    a.conv_di = D.di; a.conv_state = dec_conv_of(c, l); a.ld_state = ld; a.conv_w = W.conv_w;
+    a.conv_b = W.conv_b; a.conv_out = c->dcvt;
+    g.out = gemm(c->dyt, DW.w_out, c->dot, W.b_out, nullptr, D.d, D.di, ACT_NONE);
+    DecGemmArgs& f = g.ff1;  // LN2 + FF1 + GELU
+    f.Xt = c->dot; f.ldx = ld; f.W = DW.w1; f.ldw = 4 * D.d; f.C = c->dhidt; f.ldc = ld;
+    f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU;
+    g.ff2 = gemm(c->dhidt, DW.w2, c->dxt, W.b2, c->dxt, D.d, 4 * D.d, ACT_NONE);
+    g.lw = W;
+    g.na = DW.na; g.wdt = DW.w_dt; g.w_x = DW.w_x; g.ssm = dec_ssm_of(c, l);
+    g.ldw_x = (int)round_up(c->n_xdec, 16); g.cached = cached ? 1 : 0;
+  }
+  P.head1 = gemm(c->dxt, c->dhw1, c->dot, c->hb1, nullptr, D.d, D.d, ACT_RELU);
+  DecGemmArgs& h = P.head2;
+  h.Xt = c->dot; h.ldx = ld; h.W = c->dhw2; h.ldw = VOCAB; h.M = lanes; h.N = VOCAB; h.K = D.d;
+  h.act = ACT_NONE; h.row_major = 1;
+  P.emb = c->emb; P.xt = c->dxt; P.zt = c->dzt; P.cvt = c->dcvt; P.yt = c->dyt;
+  P.head_b2 = c->hb2; P.tok = c->tok; P.lens = c->lens; P.out = out; P.out_stride = chunk;
+  P.states = c->dec; P.payload = payload; P.offsets = c->offsets; P.sizes = c->sizes;
+  P.bar = c->gaux + kGauxBar;
+  P.t_group = reinterpret_cast<int*>(c->gaux + kGauxTGroup);
+  P.o_rec = reinterpret_cast<int*>(c->gaux + kGauxORec);
+  P.t_counter = c->t_counter;
+  P.abort = reinterpret_cast<int*>(c->gaux + kGauxAbort);
+  P.inv_t = c->inv_temp; P.L = D.L; P.M = lanes; P.ld = ld; P.r = D.r;
+}
+
 // Grow-only device buffer: reallocated only when a call needs more.
 template <class T>
 hipError_t ensure_buf(T** p, int64_t* cap, int64_t need) {
@@ -807,6 +892,19 @@ hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias
   return step_range(c, 0, lanes, c->stream, c->t_counter, tok, add_bias, logits);
 }
 
+// After a batch decoded with the group step: a barrier that timed out, or a
+// workgroup outside its group's XCD, leaves the abort flag set and the
+// batch's symbols undefined.  The counters are reset for later calls.
+int check_group_abort(boa_ctx* c) {
+  int ab = 0;
+  if (hipMemcpy(&ab, c->gaux + kGauxAbort, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(c, BOA_E_HIP, "decode step: reading the group step's status failed");
+  if (!ab) return BOA_OK;
+  (void)hipMemset(c->gaux, 0, kGauxWords * sizeof(unsigned));
+  return fail(c, BOA_E_HIP, ab == 2 ? "decode step: workgroups were not dispatched round-robin over the XCDs"
+                                    : "decode step: a lane-group barrier timed out");
+}
+
 int check_ready(boa_ctx* c) {
   if (!c) return BOA_E_ARG;
   if (!c->loaded) return fail(c, BOA_E_STATE, "no weights loaded");
@@ -903,7 +1001,21 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
   // (dec_head_step_kernel), so the logits stay on chip; below that, and in
   // bf16, head.2 and the coder step are separate launches
   const bool fuse_head = !c->bf16 && dec_fuse_head(lanes);
+  // fp32 d_model 256 up to 1024 lanes: one launch per step (its plan goes to
+  // the device after the previous batch's steps, and the groups' decoded
+  // positions restart at 0)
+  const bool group = dec_use_group(c, lanes);
+  if (group) {
+    build_group_plan(c, lanes, out, chunk, d_payload);
+    hipError_t e = hipMemcpyAsync(c->d_gplan, c->h_gplan, sizeof(GroupPlan),
+                                  hipMemcpyHostToDevice, s);
+    if (!e) e = launch_fill_zero(c->gaux + kGauxTGroup, 64 * sizeof(unsigned), s);
+    if (e) return e;
+  }
   auto one_step = [&](hipStream_t gs) -> hipError_t {
+    if (group)
+      return timed(c, BOA_K_DEC_STEP, dec_step_flops(c, lanes),
+                   [&] { return launch_dec_group_step(c->d_gplan, lanes, gs); });
     hipError_t e =
         step_range(c, 0, lanes, gs, c->t_counter, c->tok, false, c->dlogits, !fuse_head);
     if (e) return e;
@@ -952,11 +1064,12 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
   // these or a buffer of the context)
   boa_ctx::GraphKey key;
   key.lanes = lanes; key.out = out; key.stride = chunk; key.payload = d_payload;
-  key.inv_temp = c->inv_temp; key.stream = c->dec_stream;
+  key.inv_temp = c->inv_temp; key.stream = c->dec_stream; key.group = group;
   const boa_ctx::GraphKey& k0 = c->dec_key;
   const bool same = c->dec_exec && k0.lanes == key.lanes && k0.out == key.out &&
                     k0.stride == key.stride && k0.payload == key.payload &&
-                    k0.inv_temp == key.inv_temp && k0.stream == key.stream;
+                    k0.inv_temp == key.inv_temp && k0.stream == key.stream &&
+                    k0.group == key.group;
   if (!same) {
     if (c->dec_exec) {
       e = hipStreamSynchronize(c->dec_stream);  // its last replay has finished
@@ -1063,6 +1176,18 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
     boa_destroy(c);
     return BOA_E_NOMEM;
   }
+  {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&c->n_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      c->n_cus = 0;
+  }
+  c->h_gplan = new (std::nothrow) GroupPlan{};
+  if (!c->h_gplan || dalloc(&c->d_gplan, 1) || dalloc(&c->gaux, kGauxWords) ||
+      hipMemset(c->gaux, 0, kGauxWords * sizeof(unsigned)) != hipSuccess) {
+    boa_destroy(c);
+    return BOA_E_NOMEM;
+  }
   *out = c;
   return BOA_OK;
 }
@@ -1081,6 +1206,8 @@ void boa_destroy(boa_ctx* c) {
   dfree(c->hid); dfree(c->logits); dfree(c->lowprob);
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
   dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
+  dfree(c->d_gplan); dfree(c->gaux);
+  delete c->h_gplan;
   if (c->h_sizes) (void)hipHostFree(c->h_sizes);
   drop_dec_graph(c);
   dfree(c->first_buf); dfree(c->reorder_words); dfree(c->reorder_off); dfree(c->reorder_sz);
@@ -1134,11 +1261,20 @@ int boa_decode_plan(const boa_ctx* c, int32_t lanes, int32_t* cached_layers, int
   const bool pers = !c->bf16 && dec_persist_fits(D.d, D.ds, D.r, D.L);
   const bool chain32 = !pers && !c->bf16;
   if (cached_layers) *cached_layers = pers ? D.L : dec_cached_layers(c, lanes);
+  const bool group = chain32 && dec_use_group(c, lanes);
   if (flags)
     *flags = (chain32 && dec_fuse_ln(c, lanes) ? BOA_PLAN_FUSED_LN : 0) |
              (pers ? BOA_PLAN_PERSISTENT : 0) |
              (chain32 && dec_fuse_xproj(c, lanes) ? BOA_PLAN_FUSED_XPROJ : 0) |
-             (chain32 && dec_fuse_head(lanes) ? BOA_PLAN_FUSED_HEAD : 0);
+             ((chain32 && dec_fuse_head(lanes)) || group ? BOA_PLAN_FUSED_HEAD : 0) |
+             (group ? BOA_PLAN_GROUP_STEP : 0);
+  return BOA_OK;
+}
+
+int boa_set_decode_group(boa_ctx* c, int32_t enable) {
+  if (!c) return BOA_E_ARG;
+  drop_dec_graph(c);
+  c->group_step = enable ? 1 : 0;
   return BOA_OK;
 }
 
@@ -1724,6 +1860,7 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       }
       e = hipStreamSynchronize(s);
       if (e) return hip_fail(c, e, "decode sync");
+      if (dec_use_group(c, lanes) && (rc = check_group_abort(c))) return rc;
       for (int b = 0; b < lanes; ++b) c->prog_base += lens[b];
       if (c->progress) c->progress(c->progress_user, 1, c->prog_base, c->prog_total);
     }

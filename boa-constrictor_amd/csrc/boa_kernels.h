@@ -259,6 +259,52 @@ struct PersistArgs {
 bool dec_persist_fits(int d, int ds, int r, int L);
 hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, hipStream_t s);
 
+// ---- group-synchronous decode step (decode.hip) ------------------------
+// One launch runs a whole step (every layer, the head, the CDF, the search
+// and the coder advance) for d_model 256, d_state 16, fp32, at most 1024
+// lanes.  Its grid is the launch chain's: xcd_grid(lanes, 16) workgroups of
+// 1024 threads, one per CU; a workgroup joins the 64-lane group of the XCD
+// it runs on.  The phases are the chain's kernels, in the chain's order and
+// with its bits; between phases the group's 16 workgroups meet at a barrier
+// of their own (a counter in device memory).  Every wait is bounded: a
+// timeout, or a dispatch that is not round-robin over the XCDs, sets *abort
+// and ends the launch, and the host reports an error.
+constexpr int GROUP_MAX_LAYERS = 16;
+struct GroupLayerPlan {
+  DecGemmArgs in, out, ff1, ff2;  // LN1 + in_proj + conv, out_proj, LN2 + FF1, FF2
+  LayerW lw;                       // LayerNorm weights, dt bias, D
+  const float *na, *wdt, *w_x;     // scan parameters (quad layout), x_proj (k-blocked)
+  float* ssm;                      // step-layout SSM state
+  int ldw_x, cached;
+};
+struct GroupPlan {
+  GroupLayerPlan layer[GROUP_MAX_LAYERS];
+  DecGemmArgs head1, head2;  // head.2: row-major, no bias (added with the CDF)
+  const float* emb;
+  float* xt;                 // residual stream (layer 0 stores the embedding rows)
+  const float *zt, *cvt;     // in_proj's z half and conv output
+  float* yt;                 // scan output
+  const float* head_b2;
+  uint8_t* tok;
+  const int32_t* lens;
+  uint8_t* out;
+  int64_t out_stride;
+  RcDec* states;
+  const uint32_t* payload;
+  const uint64_t* offsets;
+  const int32_t* sizes;
+  unsigned* bar;   // per 64-lane group: one barrier counter, 256 bytes apart
+  int* t_group;    // per 64-lane group: the last decoded position
+  int* o_rec;      // per 64-lane group: 16 words, each member's dispatch offset
+  int* t_counter;  // the launch chain's step counter, kept in step
+  int* abort;
+  float inv_t;
+  int L, M, ld, r;
+};
+constexpr int GROUP_MAX_LANES = 1024;
+bool dec_group_fits(const Dims& D, int lanes, int n_cus);
+hipError_t launch_dec_group_step(const GroupPlan* d_plan, int lanes, hipStream_t s);
+
 // ---- decode step, bf16 precision (decode_bf16.hip) ----------------------
 // Activations bf16 in the 32-blocked layout (feature k of lane m at
 // ((k/32) ld + m) 32 + k%32), the residual stream fp32 k-blocked.
