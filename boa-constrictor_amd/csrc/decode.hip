@@ -452,9 +452,30 @@ hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, floa
 // rows' round trip through memory, and the block's waves share their
 // operand loads.  Layer 0's LN1 gathers the embedding rows and the n-block
 // 0 blocks store them as x.
+// Copy of block vb's 64 weight rows into ws (global_load_lds_dwordx4: a
+// wave's 64 float4s are one contiguous 1 KB span at both ends): float4
+// r = tid % 256 of 16-k block q = 4 it + tid / 256.
+template <int NB>
+__device__ __forceinline__ void dec_ln_gemm_issue_w(const DecGemmArgs& a, int vb, float* ws,
+                                                    int tid) {
+  const XcdSlot blk = xcd_slot(vb, a.N / 64);
+  if (blk.grp * 64 >= a.M) return;
+  const int n0 = blk.j * 64, r = tid & 255;
+  const float4* W4 = reinterpret_cast<const float4*>(a.W);
+#pragma unroll
+  for (int it = 0; it < NB / 4; ++it) {
+    const int q = 4 * it + (tid >> 8);
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(W4 + ((size_t)q * a.ldw + n0) * 4 + r),
+        (__attribute__((address_space(3))) void*)(reinterpret_cast<float4*>(ws) + q * 256 + (r & ~63)),
+        16, 0, 0);
+  }
+}
+
 // The block's work for virtual block vb, with its LDS passed in: xs and ws
-// of NB * 1024 floats each, lwb of 2 d, stats of 128.
-template <int MODE, int NB, bool EMB, bool COH>
+// of NB * 1024 floats each, lwb of 2 d, stats of 128.  With WPRE the weight
+// rows have been issued into ws already (dec_ln_gemm_issue_w).
+template <int MODE, int NB, bool EMB, bool COH, bool WPRE = false>
 __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const float* __restrict__ emb,
                                                  const uint8_t* __restrict__ tok, float* xt,
                                                  const float* __restrict__ lw,
@@ -499,13 +520,15 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   // barrier keeps them after the stores, whose wait would otherwise cover
   // them too): LN GEMMs 13.4 -> 13.2 us at 1000 lanes
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!WPRE) {
 #pragma unroll
-  for (int it = 0; it < SQ; ++it) {
-    const int q = 4 * it + (tid >> 8);
-    __builtin_amdgcn_global_load_lds(
-        (const void*)(W4 + ((size_t)q * a.ldw + n0) * 4 + r),
-        (__attribute__((address_space(3))) void*)(reinterpret_cast<float4*>(ws) + q * 256 + (r & ~63)),
-        16, 0, 0);
+    for (int it = 0; it < SQ; ++it) {
+      const int q = 4 * it + (tid >> 8);
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(W4 + ((size_t)q * a.ldw + n0) * 4 + r),
+          (__attribute__((address_space(3))) void*)(reinterpret_cast<float4*>(ws) + q * 256 + (r & ~63)),
+          16, 0, 0);
+    }
   }
   // LDS barrier without the fence of __syncthreads, which would wait for the
   // weight copies too: this wave's LDS stores are complete at lgkmcnt(0)
@@ -982,43 +1005,104 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
 template <int DS, int RB>
 constexpr int xscan_lds_floats() { return 16 * (((RB + 2 * DS + 15) / 16) * 16 + 4); }
 
+// Thread tid's lane and channels in virtual block vb of the x_proj + scan:
+// lane m0 + lm (loads clamp it to mc), channel 16 (8 cb + q + 4 p) + cl of
+// channel pass p = 0, 1.
+template <int DI>
+struct XscanPos {
+  int cb, m0, cl, lm, q, m, mc;
+  __device__ __forceinline__ XscanPos(int vb, int tid, int M) {
+    const XcdSlot blk = xcd_slot(vb, 4 * (DI / 128));  // 4 16-lane tiles x DI/128 channel blocks
+    cb = blk.j % (DI / 128);
+    m0 = blk.grp * 64 + (blk.j / (DI / 128)) * 16;
+    cl = tid & 15; lm = (tid >> 4) & 15; q = tid >> 8;
+    m = m0 + lm;
+    mc = min(m, M - 1);  // lanes past M load a valid row and store nothing
+  }
+};
+
+// The loads of the x_proj + scan that depend on no other workgroup: both
+// channels' state and the first channel's scan parameters.
+template <int DS, int RB>
+struct XscanPre {
+  float h0[DS], h1[DS];
+  ScanCtx<DS, RB> sc0;
+};
+template <int DS, int RB, int DI, bool CACHED>
+__device__ __forceinline__ void xscan_load_state(XscanPre<DS, RB>& pr, const XscanPos<DI>& ps,
+                                                 const float* ssm, int ld_state) {
+  const float4* h4 = reinterpret_cast<const float4*>(ssm);
+#pragma unroll
+  for (int n4 = 0; n4 < DS / 4; ++n4) {
+    const float4 hv = state_ld4(
+        h4 + ((size_t)((8 * ps.cb + ps.q) * (DS / 4) + n4) * ld_state + ps.mc) * 16 + ps.cl, CACHED);
+    pr.h0[4 * n4] = hv.x; pr.h0[4 * n4 + 1] = hv.y; pr.h0[4 * n4 + 2] = hv.z; pr.h0[4 * n4 + 3] = hv.w;
+  }
+#pragma unroll
+  for (int n4 = 0; n4 < DS / 4; ++n4) {
+    const float4 hv = state_ld4(
+        h4 + ((size_t)((8 * ps.cb + ps.q + 4) * (DS / 4) + n4) * ld_state + ps.mc) * 16 + ps.cl,
+        CACHED);
+    pr.h1[4 * n4] = hv.x; pr.h1[4 * n4 + 1] = hv.y; pr.h1[4 * n4 + 2] = hv.z; pr.h1[4 * n4 + 3] = hv.w;
+  }
+}
+template <int DS, int RB, int DI>
+__device__ __forceinline__ void xscan_load_params(XscanPre<DS, RB>& pr, const XscanPos<DI>& ps,
+                                                  const LayerW& Lw, const float* na_q,
+                                                  const float* wdt_q) {
+  const int c16 = 8 * ps.cb + ps.q, c = 16 * c16 + ps.cl;
+  const float4* na4 = reinterpret_cast<const float4*>(na_q);
+  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
+  ScanCtx<DS, RB>& sc0 = pr.sc0;
+#pragma unroll
+  for (int n4 = 0; n4 < DS / 4; ++n4) {
+    const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + ps.cl];
+    sc0.na[4 * n4] = av.x; sc0.na[4 * n4 + 1] = av.y; sc0.na[4 * n4 + 2] = av.z; sc0.na[4 * n4 + 3] = av.w;
+  }
+#pragma unroll
+  for (int j4 = 0; j4 < RB / 4; ++j4) {
+    const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + ps.cl];
+    sc0.wdt[4 * j4] = wv4.x; sc0.wdt[4 * j4 + 1] = wv4.y; sc0.wdt[4 * j4 + 2] = wv4.z; sc0.wdt[4 * j4 + 3] = wv4.w;
+  }
+  sc0.bdt = Lw.b_dt[c];
+  sc0.dd = Lw.dd[c];
+}
+// Both, for the group step to issue ahead of its barrier (lanes past M as
+// the body: a whole block past M loads nothing).
+template <int DS, int RB, int DI, bool CACHED>
+__device__ __forceinline__ void dec_xscan_pre(XscanPre<DS, RB>& pr, const LayerW& Lw,
+                                              const float* na_q, const float* wdt_q,
+                                              const float* ssm, int M, int ld_state, int vb,
+                                              int tid) {
+  const XscanPos<DI> ps(vb, tid, M);
+  if (ps.m0 >= M) return;
+  xscan_load_state<DS, RB, DI, CACHED>(pr, ps, ssm, ld_state);
+  xscan_load_params<DS, RB, DI>(pr, ps, Lw, na_q, wdt_q);
+}
+
 // The block's work for virtual block vb, its x_proj rows in LDS at rown.
-template <int DS, int RB, int DI, bool CACHED, bool COH>
+// pl holds the independent loads: made here, or with PRE by dec_xscan_pre.
+template <int DS, int RB, int DI, bool CACHED, bool COH, bool PRE = false>
 __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __restrict__ na_q,
                                                const float* __restrict__ wdt_q,
                                                const float* __restrict__ w_x, int ldw_x,
                                                const float* __restrict__ zt,
                                                const float* __restrict__ cvt, float* ssm, float* yt,
                                                int M, int ld, int ld_state, int r, int vb,
-                                               float* rown, int tid) {
+                                               float* rown, int tid, XscanPre<DS, RB>& pl) {
   constexpr int NB = (RB + 2 * DS + 15) / 16;  // 16-feature blocks of the x_proj row
-  constexpr int CB = DI / 128;                 // 128-channel blocks per 16-lane tile
   constexpr int RS = NB * 16 + 4;              // LDS row stride (floats, 16-byte aligned)
   static_assert(NB <= 16 && DI % 128 == 0, "one wave per x_proj feature block");
-  const XcdSlot blk = xcd_slot(vb, 4 * CB);  // 4 16-lane tiles x CB channel blocks
-  const int cb = blk.j % CB;
-  const int m0 = blk.grp * 64 + (blk.j / CB) * 16;
+  const XscanPos<DI> ps(vb, tid, M);
+  const int cb = ps.cb, m0 = ps.m0, cl = ps.cl, lm = ps.lm, q = ps.q, m = ps.m, mc = ps.mc;
   if (m0 >= M) return;  // the whole block, before the barrier
-  const int cl = tid & 15, lm = (tid >> 4) & 15, q = tid >> 8;
-  const int m = m0 + lm;
-  const int mc = min(m, M - 1);  // lanes past M load a valid row and store nothing
   float4* h4 = reinterpret_cast<float4*>(ssm);
   // 1. both channels' state (16-channel blocks 8 cb + q and 8 cb + q + 4),
   // in flight during x_proj (loading the second one only after the first
   // channel's scan measured 18.2 against 16.6 us per launch at 1000 lanes)
-  float h0[DS], h1[DS];
-#pragma unroll
-  for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 hv =
-        state_ld4(h4 + ((size_t)((8 * cb + q) * (DS / 4) + n4) * ld_state + mc) * 16 + cl, CACHED);
-    h0[4 * n4] = hv.x; h0[4 * n4 + 1] = hv.y; h0[4 * n4 + 2] = hv.z; h0[4 * n4 + 3] = hv.w;
-  }
-#pragma unroll
-  for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 hv =
-        state_ld4(h4 + ((size_t)((8 * cb + q + 4) * (DS / 4) + n4) * ld_state + mc) * 16 + cl, CACHED);
-    h1[4 * n4] = hv.x; h1[4 * n4 + 1] = hv.y; h1[4 * n4 + 2] = hv.z; h1[4 * n4 + 3] = hv.w;
-  }
+  if constexpr (!PRE) xscan_load_state<DS, RB, DI, CACHED>(pl, ps, ssm, ld_state);
+  const float* h0 = pl.h0;
+  const float* h1 = pl.h1;
   // the two channels' conv output and z (of lane mc) and the first channel's
   // scan parameters, also in flight during x_proj (16.45 -> 16.2 us)
   float uz[2][2];
@@ -1028,24 +1112,8 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
     uz[p][0] = act_ld<COH>(cvt, cmp);
     uz[p][1] = act_ld<COH>(zt, cmp);
   }
-  ScanCtx<DS, RB> sc0;
-  {
-    const int c16 = 8 * cb + q, c = 16 * c16 + cl;
-    const float4* na4 = reinterpret_cast<const float4*>(na_q);
-    const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
-#pragma unroll
-    for (int n4 = 0; n4 < DS / 4; ++n4) {
-      const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + cl];
-      sc0.na[4 * n4] = av.x; sc0.na[4 * n4 + 1] = av.y; sc0.na[4 * n4 + 2] = av.z; sc0.na[4 * n4 + 3] = av.w;
-    }
-#pragma unroll
-    for (int j4 = 0; j4 < RB / 4; ++j4) {
-      const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + cl];
-      sc0.wdt[4 * j4] = wv4.x; sc0.wdt[4 * j4 + 1] = wv4.y; sc0.wdt[4 * j4 + 2] = wv4.z; sc0.wdt[4 * j4 + 3] = wv4.w;
-    }
-    sc0.bdt = Lw.b_dt[c];
-    sc0.dd = Lw.dd[c];
-  }
+  if constexpr (!PRE) xscan_load_params<DS, RB, DI>(pl, ps, Lw, na_q, wdt_q);
+  const ScanCtx<DS, RB>& sc0 = pl.sc0;
   // 2. x_proj: wave w < NB computes feature block w for lanes m0 .. m0 + 15
   const int wv = tid >> 6;
   if (wv < NB) {
@@ -1107,8 +1175,9 @@ __global__ __launch_bounds__(1024) void dec_xscan_kernel(LayerW Lw, const float*
                                                          float* ssm, float* yt, int M, int ld,
                                                          int ld_state, int r) {
   __shared__ __align__(16) float rown[xscan_lds_floats<DS, RB>()];
+  XscanPre<DS, RB> pl;
   dec_xscan_body<DS, RB, DI, CACHED, false>(Lw, na_q, wdt_q, w_x, ldw_x, zt, cvt, ssm, yt, M, ld,
-                                            ld_state, r, blockIdx.x, rown, threadIdx.x);
+                                            ld_state, r, blockIdx.x, rown, threadIdx.x, pl);
 }
 
 bool dec_xscan_fits(const Dims& D) {
@@ -1229,10 +1298,18 @@ hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, floa
 // The wait is bounded: after kGroupSpin polls, or once another workgroup
 // has set *abort, it sets *abort and returns false, and the caller ends the
 // launch.
+// It comes in two halves so that loads of the next phase that depend on
+// no other workgroup can be issued between them and overlap the wait:
+// group_stores_done (every wave's stores of the phase complete), then
+// group_wait (arrive and wait).  group_wait's workgroup barriers wait for
+// LDS only, so such loads stay in flight; but thread 0's polls wait on every
+// load of wave 0, so wave 0 issues its share after group_wait returns.
 constexpr int kGroupSpin = 1 << 20;
-__device__ __forceinline__ bool group_sync(unsigned* ctr, int* abort, int* s_ok) {
+__device__ __forceinline__ void group_stores_done() {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
+}
+__device__ __forceinline__ bool group_wait(unsigned* ctr, int* abort, int* s_ok) {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (threadIdx.x == 0) {
     const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned target = (old & ~15u) + 16u;
@@ -1250,8 +1327,12 @@ __device__ __forceinline__ bool group_sync(unsigned* ctr, int* abort, int* s_ok)
     }
     *s_ok = ok;
   }
-  __syncthreads();
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   return *s_ok != 0;
+}
+__device__ __forceinline__ bool group_sync(unsigned* ctr, int* abort, int* s_ok) {
+  group_stores_done();
+  return group_wait(ctr, abort, s_ok);
 }
 
 // LDS of the step: the LayerNorm-GEMM phases' (two 64 x 256 tiles, the
@@ -1261,6 +1342,36 @@ constexpr int GROUP_LDS_FLOATS = 2 * 16 * 1024 + 2 * 256 + 128;
 static_assert(16 * HS_LS + 2 * 16 * 260 + 16 <= GROUP_LDS_FLOATS, "head step LDS");
 static_assert(xscan_lds_floats<16, 16>() <= GROUP_LDS_FLOATS, "scan LDS");
 
+// Each phase of the group step takes the thread index through an opaque
+// move, so that the compiler derives the phase's addresses there instead of
+// keeping those of every phase live across the layer loop (and spilling
+// them).
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// The boundary after LN1 + in_proj + conv, then x_proj + scan: the scan's
+// state and first scan parameters are loaded across the barrier (wave 0's
+// after it, see group_wait).
+template <bool CACHED>
+__device__ __forceinline__ bool xscan_phase(const GroupLayerPlan& lp, const GroupPlan* P, int M,
+                                            int vb, float* lds, unsigned* ctr, int* abort,
+                                            int* s_ok) {
+  XscanPre<16, 16> pl;
+  group_stores_done();
+  int tid = opaque_tid();
+  if (tid >= 64) dec_xscan_pre<16, 16, 512, CACHED>(pl, lp.lw, lp.na, lp.wdt, lp.ssm, M, P->ld, vb, tid);
+  if (!group_wait(ctr, abort, s_ok)) return false;
+  if (tid < 64) dec_xscan_pre<16, 16, 512, CACHED>(pl, lp.lw, lp.na, lp.wdt, lp.ssm, M, P->ld, vb, tid);
+  tid = opaque_tid();
+  dec_xscan_body<16, 16, 512, CACHED, true, true>(lp.lw, lp.na, lp.wdt, lp.w_x, lp.ldw_x, P->zt,
+                                                  P->cvt, lp.ssm, P->yt, M, P->ld, P->ld, P->r, vb,
+                                                  lds, tid, pl);
+  return true;
+}
+
 // One decode step of every lane (boa_gpu.hpp:1034-1053 for the model,
 // range_coder_kernels.cu:504-627 for the CDF, search and coder advance):
 // per layer LN1 + in_proj + conv, x_proj + scan, out_proj, LN2 + FF1 + GELU,
@@ -1269,14 +1380,6 @@ static_assert(xscan_lds_floats<16, 16>() <= GROUP_LDS_FLOATS, "scan LDS");
 // of the chain's kernel for that phase runs (every phase maps blocks with
 // xcd_slot(vb, 16)), so results are the chain's bit for bit.
 __global__ __launch_bounds__(1024) void dec_group_step_kernel(const GroupPlan* __restrict__ P) {
-  // each phase takes the thread index through an opaque move, so that the
-  // compiler derives the phase's addresses there instead of keeping those of
-  // every phase live across the layer loop (and spilling them)
-  auto tid_ = [] {
-    int t = threadIdx.x;
-    asm volatile("" : "+v"(t));
-    return t;
-  };
   __shared__ __align__(16) float lds[GROUP_LDS_FLOATS];
   __shared__ int s_ok;
   if (*P->abort) return;  // an earlier launch gave up: the batch has failed
@@ -1326,33 +1429,49 @@ __global__ __launch_bounds__(1024) void dec_group_step_kernel(const GroupPlan* _
   float* lwb = lds + 32 * 1024;
   float* st = lwb + 2 * 256;
   const int L = P->L;
+  // a phase boundary with loads of the next phase issued across it
+  auto boundary = [&](auto&& issue) {
+    group_stores_done();
+    const int tid = opaque_tid();
+    if (tid >= 64) issue(tid);
+    if (!group_wait(ctr, abort, &s_ok)) return false;
+    if (tid < 64) issue(tid);
+    return true;
+  };
   for (int l = 0; l < L; ++l) {
     const GroupLayerPlan& lp = P->layer[l];
+    // LN1 + in_proj + conv; from layer 1 on, its weight rows were issued
+    // into ws across the last barrier
     if (l == 0)
       dec_ln_gemm_body<1, 16, true, true>(lp.in, P->emb, P->tok, P->xt, lp.lw.ln1_w, lp.lw.ln1_b,
-                                          vb, xs, ws, lwb, st, tid_());
+                                          vb, xs, ws, lwb, st, opaque_tid());
     else
-      dec_ln_gemm_body<1, 16, false, true>(lp.in, nullptr, nullptr, nullptr, lp.lw.ln1_w,
-                                           lp.lw.ln1_b, vb, xs, ws, lwb, st, tid_());
+      dec_ln_gemm_body<1, 16, false, true, true>(lp.in, nullptr, nullptr, nullptr, lp.lw.ln1_w,
+                                                 lp.lw.ln1_b, vb, xs, ws, lwb, st, opaque_tid());
+    // x_proj + scan, its state and first scan parameters loaded across the
+    // barrier (the cache policy of the state is a template argument, so
+    // each branch holds a whole boundary and body)
+    if (lp.cached) {
+      if (!xscan_phase<true>(lp, P, M, vb, lds, ctr, abort, &s_ok)) return;
+    } else {
+      if (!xscan_phase<false>(lp, P, M, vb, lds, ctr, abort, &s_ok)) return;
+    }
     if (!group_sync(ctr, abort, &s_ok)) return;
-    if (lp.cached)
-      dec_xscan_body<16, 16, 512, true, true>(lp.lw, lp.na, lp.wdt, lp.w_x, lp.ldw_x, P->zt,
-                                              P->cvt, lp.ssm, P->yt, M, P->ld, P->ld, P->r, vb, lds,
-                                              tid_());
-    else
-      dec_xscan_body<16, 16, 512, false, true>(lp.lw, lp.na, lp.wdt, lp.w_x, lp.ldw_x, P->zt,
-                                               P->cvt, lp.ssm, P->yt, M, P->ld, P->ld, P->r, vb, lds,
-                                               tid_());
+    if (threadIdx.x < 256) dec_gemm_wave<128, 1, 8, true>(lp.out, vb, opaque_tid());
+    // LN2 + FF1 + GELU, its weight rows issued into ws across the barrier
+    if (!boundary([&](int tid) { dec_ln_gemm_issue_w<16>(lp.ff1, vb, ws, tid); })) return;
+    dec_ln_gemm_body<2, 16, false, true, true>(lp.ff1, nullptr, nullptr, nullptr, lp.lw.ln2_w,
+                                               lp.lw.ln2_b, vb, xs, ws, lwb, st, opaque_tid());
     if (!group_sync(ctr, abort, &s_ok)) return;
-    if (threadIdx.x < 256) dec_gemm_wave<128, 1, 8, true>(lp.out, vb, tid_());
-    if (!group_sync(ctr, abort, &s_ok)) return;
-    dec_ln_gemm_body<2, 16, false, true>(lp.ff1, nullptr, nullptr, nullptr, lp.lw.ln2_w,
-                                         lp.lw.ln2_b, vb, xs, ws, lwb, st, tid_());
-    if (!group_sync(ctr, abort, &s_ok)) return;
-    if (threadIdx.x < 256) dec_gemm_wave<256, 1, 8, true>(lp.ff2, vb, tid_());
-    if (!group_sync(ctr, abort, &s_ok)) return;
+    if (threadIdx.x < 256) dec_gemm_wave<256, 1, 8, true>(lp.ff2, vb, opaque_tid());
+    if (l + 1 < L) {
+      const DecGemmArgs& nin = P->layer[l + 1].in;
+      if (!boundary([&](int tid) { dec_ln_gemm_issue_w<16>(nin, vb, ws, tid); })) return;
+    } else if (!group_sync(ctr, abort, &s_ok)) {
+      return;
+    }
   }
-  if (threadIdx.x < 256) dec_gemm_wave<64, 1, 8, true>(P->head1, vb, tid_());
+  if (threadIdx.x < 256) dec_gemm_wave<64, 1, 8, true>(P->head1, vb, opaque_tid());
   if (!group_sync(ctr, abort, &s_ok)) return;
   if (gs.j < 4)  // 16 lanes per workgroup
     dec_head_step_body<64, true>(P->head2, P->head_b2, P->inv_t, P->tok, P->lens, t, P->out,
@@ -1360,7 +1479,7 @@ __global__ __launch_bounds__(1024) void dec_group_step_kernel(const GroupPlan* _
                                  gs.grp * 64 + 16 * gs.j, lds,
                                  reinterpret_cast<double(*)[260]>(lds + 16 * HS_LS),
                                  reinterpret_cast<uint32_t*>(lds + 16 * HS_LS + 2 * 16 * 260),
-                                 tid_());
+                                 opaque_tid());
   // every member has read t_group (before the first barrier)
   if (gs.j == 0 && threadIdx.x == 0) {
     P->t_group[gs.grp] = t;
