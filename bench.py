@@ -41,6 +41,7 @@ PEAK_HBM_GBS = 8000.0     # MI355X HBM3E peak
 GEMM_KERNEL = {"fp32": "boa::gemm_f32_kernel<128, 256, 4, 4, 16, 0|1|2>",
                "bf16": "boa::gemm_bf16_kernel<256, 256, 4, 4, 64, 1|2, 0|1|2>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_f32_c2_traffic.json")
+DEC_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dec_ln_gemm_c2_traffic.json")
 
 
 def gemm_traffic_bytes():
@@ -51,6 +52,23 @@ def gemm_traffic_bytes():
             t = json.load(f)
         return round((t["fetch_kib_per_dispatch"] * t["fetch_scale"] +
                       t["write_kib_per_dispatch"] * t["write_scale"]) * 1024)
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def dec_ln_gemm_traffic_bytes():
+    """HBM bytes per launch of the decode LayerNorm GEMMs at the C2 model and
+    1000 lanes (in_proj and FF1 launch equally often per step: their mean),
+    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs, scaled by the
+    copy-kernel calibration."""
+    try:
+        with open(DEC_TRAFFIC_FILE) as f:
+            t = json.load(f)
+        ip = t["in_proj_fetch_kib_per_dispatch"] * t["fetch_scale"] + \
+            t["in_proj_write_kib_per_dispatch"] * t["write_scale"]
+        ff = t["ff1_fetch_kib_per_dispatch"] * t["fetch_scale"] + \
+            t["ff1_write_kib_per_dispatch"] * t["write_scale"]
+        return round((ip + ff) / 2 * 1024)
     except (OSError, KeyError, ValueError):
         return None
 
@@ -411,11 +429,13 @@ def main() -> int:
                        "FF2, heads)", "mfma"),
           "dec_scan": ("decode scan", "boa::dec_xscan_kernel / dec_scan_kernel / dec_b16_scan_kernel",
                        "hbm")}
+    c2_lanes = args.config == "c2" and not args.warm_start and n_chunks == 1000
     for k, (name, kernel, bound) in kn.items():
         if k in dec_cls:
             v = dec_cls[k]
+            extra = {"traffic": dec_ln_gemm_traffic_bytes()} if k == "dec_lngemm" and c2_lanes else {}
             add(name, kernel, bound, v["work_per_launch"], v["avg_us"],
-                v["launches_per_step"] * steps_per_dec, peak_mm)
+                v["launches_per_step"] * steps_per_dec, peak_mm, **extra)
     if dec is not None and dec["plan"]["persistent"] and K:
         # model FLOPs per token: in_proj, x_proj, dt_proj, out_proj, FF1, FF2
         # per layer, then head.1 and head.2
