@@ -112,6 +112,13 @@ struct boa_ctx {
   float *x = nullptr, *xn = nullptr, *xz = nullptr, *cv = nullptr, *delta = nullptr, *y = nullptr,
         *hid = nullptr, *logits = nullptr;
   uint2* lowprob = nullptr;
+  // compress: tile k's (low, prob) pairs are coded on enc_stream while tile
+  // k + 1's forward pass runs on the caller's stream; the two buffers
+  // alternate (lowprob is the one the next forward pass writes)
+  uint2* lowprob_alt = nullptr;
+  hipStream_t enc_stream = nullptr;
+  hipEvent_t lp_ready[2] = {nullptr, nullptr}, lp_free[2] = {nullptr, nullptr};
+  hipEvent_t enc_done = nullptr;
 
   // coder scratch
   int64_t words_cap = 0;  // per-lane pitch x lanes
@@ -290,14 +297,26 @@ int ensure_rows(boa_ctx* c, int64_t rows) {
   if (rows <= c->rows_cap) return BOA_OK;
   const Dims& D = c->D;
   dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
-  dfree(c->hid); dfree(c->logits); dfree(c->lowprob);
+  dfree(c->hid); dfree(c->logits); dfree(c->lowprob); dfree(c->lowprob_alt);
   c->rows_cap = 0;
   size_t r = (size_t)rows;
   if (dalloc(&c->x, r * D.d) || dalloc(&c->xn, r * D.d) || dalloc(&c->xz, r * 2 * D.di) ||
       dalloc(&c->cv, r * D.di) || dalloc(&c->delta, r * D.R) || dalloc(&c->y, r * D.di) ||
-      dalloc(&c->hid, r * 4 * D.d) || dalloc(&c->logits, r * VOCAB) || dalloc(&c->lowprob, r))
+      dalloc(&c->hid, r * 4 * D.d) || dalloc(&c->logits, r * VOCAB) || dalloc(&c->lowprob, r) ||
+      dalloc(&c->lowprob_alt, r))
     return fail(c, BOA_E_NOMEM, "device allocation of activation buffers failed");
   c->rows_cap = rows;
+  return BOA_OK;
+}
+
+// The coder stream and its events (created once per context, default priority).
+int ensure_enc_stream(boa_ctx* c) {
+  hipError_t e = hipSuccess;
+  if (!c->enc_stream) e = hipStreamCreateWithFlags(&c->enc_stream, hipStreamNonBlocking);
+  for (hipEvent_t* p : {&c->lp_ready[0], &c->lp_ready[1], &c->lp_free[0], &c->lp_free[1],
+                        &c->enc_done})
+    if (!e && !*p) e = hipEventCreateWithFlags(p, hipEventDisableTiming);
+  if (e) return hip_fail(c, e, "coder stream");
   return BOA_OK;
 }
 
@@ -1203,7 +1222,8 @@ void boa_destroy(boa_ctx* c) {
   dfree(c->dxt); dfree(c->dxnt); dfree(c->dot); dfree(c->dzt); dfree(c->dcvt); dfree(c->ddeltat);
   dfree(c->dyt); dfree(c->dhidt); dfree(c->dlogits);
   dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
-  dfree(c->hid); dfree(c->logits); dfree(c->lowprob);
+  if (c->enc_stream) (void)hipStreamSynchronize(c->enc_stream);
+  dfree(c->hid); dfree(c->logits); dfree(c->lowprob); dfree(c->lowprob_alt);
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
   dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
   dfree(c->d_gplan); dfree(c->gaux);
@@ -1214,6 +1234,9 @@ void boa_destroy(boa_ctx* c) {
   for (hipEvent_t e : c->prog_ev)
     if (e) (void)hipEventDestroy(e);
   if (c->dec_stream) (void)hipStreamDestroy(c->dec_stream);
+  if (c->enc_stream) (void)hipStreamDestroy(c->enc_stream);
+  for (hipEvent_t e : {c->lp_ready[0], c->lp_ready[1], c->lp_free[0], c->lp_free[1], c->enc_done})
+    if (e) (void)hipEventDestroy(e);
   if (c->dec_fork) (void)hipEventDestroy(c->dec_fork);
   if (c->dec_join) (void)hipEventDestroy(c->dec_join);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
@@ -1682,6 +1705,7 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
   const int64_t T = auto_tile(c, chunk, (int)std::min<int64_t>(B, units));
   if ((rc = ensure_rows(c, (int64_t)B * T))) return rc;
   if ((rc = ensure_words(c, pitch))) return rc;
+  if ((rc = ensure_enc_stream(c))) return rc;
   hipStream_t s = c->stream;
   if (ensure_buf(&c->first_buf, &c->first_cap, nc))
     return fail(c, BOA_E_NOMEM, "device allocation of the first-byte buffer failed");
@@ -1709,8 +1733,12 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
       if (e) return hip_fail(c, e, "rc init");
       int64_t pend = -1;
       int slot = 0;
-      for (int64_t t0 = 0; t0 < chunk; t0 += T) {
+      int k = 0;  // tile index: buffer k & 1
+      for (int64_t t0 = 0; t0 < chunk; t0 += T, ++k) {
         const int Tt = (int)std::min<int64_t>(T, chunk - t0);
+        // the coder of tile k - 2 has finished reading this tile's buffer
+        if (k >= 2) e = hipStreamWaitEvent(s, c->lp_free[k & 1], 0);
+        if (e) return hip_fail(c, e, "compress tile");
         if (c->bf16) {  // bf16: head.2 stores the logits, the CDF kernel reads them
           e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
           if (!e)
@@ -1721,17 +1749,23 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
         } else {
           e = forward_tile_cdf(c, tok, lanes, Tt, (int)t0);
         }
+        if (!e) e = hipEventRecord(c->lp_ready[k & 1], s);
+        if (!e) e = hipStreamWaitEvent(c->enc_stream, c->lp_ready[k & 1], 0);
         if (!e)
           e = timed(c, BOA_K_CODER, 8.0 * lanes * Tt, [&] {
             return launch_rc_encode_tile(c->lowprob, tok, Tt, (int)t0, lanes, c->enc, c->words,
-                                         pitch, s);
+                                         pitch, c->enc_stream);
           });
+        if (!e) e = hipEventRecord(c->lp_free[k & 1], c->enc_stream);
+        std::swap(c->lowprob, c->lowprob_alt);
         if (!e && c->progress)
           e = progress_mark(c, 0, std::min(processed, done + (int64_t)lanes * (t0 + Tt)), processed,
                             &pend, &slot);
         if (e) return hip_fail(c, e, "compress tile");
       }
-      e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
+      e = hipEventRecord(c->enc_done, c->enc_stream);  // the batch's last tile is coded
+      if (!e) e = hipStreamWaitEvent(s, c->enc_done, 0);
+      if (!e) e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
       if (!e) e = hipMemcpyAsync(c->h_sizes, c->sizes, sizeof(int32_t) * lanes, hipMemcpyDeviceToHost, s);
       if (!e) e = hipStreamSynchronize(s);
       if (e) return hip_fail(c, e, "finish");

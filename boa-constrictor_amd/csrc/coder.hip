@@ -151,9 +151,23 @@ __global__ void rc_encode_tile_kernel(const uint2* __restrict__ lowprob, TokenSr
   RcEnc st = states[b];
   uint32_t* o = out + (size_t)b * pitch_words;
   const uint2* lp = lowprob + (size_t)b * T;
-  for (int64_t t = t0; t < end; ++t) {
-    const uint2 v = lp[t - t0];
-    enc_put(st, v.x, v.y, o);
+  // The coder state is the only serial dependence: the (low, prob) pairs
+  // are read EPF positions ahead, one batch in flight while the previous
+  // batch is coded, so a lane waits on memory once per batch instead of
+  // once per symbol.
+  constexpr int EPF = 16;
+  const int n = (int)(end - t0);
+  uint2 cur[EPF], nxt[EPF];
+#pragma unroll
+  for (int i = 0; i < EPF; ++i) cur[i] = i < n ? lp[i] : make_uint2(0u, 0u);
+  for (int q = 0; q < n; q += EPF) {
+#pragma unroll
+    for (int i = 0; i < EPF; ++i) nxt[i] = q + EPF + i < n ? lp[q + EPF + i] : make_uint2(0u, 0u);
+#pragma unroll
+    for (int i = 0; i < EPF; ++i)
+      if (q + i < n) enc_put(st, cur[i].x, cur[i].y, o);
+#pragma unroll
+    for (int i = 0; i < EPF; ++i) cur[i] = nxt[i];
   }
   states[b] = st;
 }

@@ -471,91 +471,161 @@ void scan_chunk_sload_kernel(Dims D, LayerW Lw, const TA* __restrict__ xz,
   scan_store<DS, RB>(sc, ssm);
 }
 
-constexpr int SCAN_TB = 32;  // tokens of delta rows staged in LDS per pass
+// Token-blocked form for small grids (under one wave per SIMD with one
+// thread per channel, e.g. d_model 64 with 64 lanes: 128 waves for 1024
+// SIMDs, every token's latency exposed).  A block holds TBK_CPB channels of
+// one lane, 16 threads each, and the work of a pass of TB tokens is split by
+// kind instead of by state:
+//   1. thread (c, k) computes tokens k, k + 16, ...'s scalars once: dt (the
+//      dt_proj chain and softplus), dt u, D u and the gate z sigmoid(z);
+//   2. thread (c, k) runs its SPT states through the pass's tokens,
+//      h = fma(2^(na dt), h, B (dt u)), and leaves each token's h in LDS;
+//   3. thread (c, k) sums y = fma(h_n, C_n, y) over n = 0 .. DS-1 in order
+//      for tokens k, k + 16, ..., adds D u, gates and stores.
+// Every element sees scan_token's operations in scan_token's order, so the
+// bits are scan_chunk_sload_kernel's.  The per-token scalars are computed
+// once per channel and the recurrence's critical path per token is its fma.
+// The next pass's delta rows, u and z are loaded into registers while the
+// current pass computes, so global latency is exposed once per kernel rather
+// than per pass.  Within a wave the channel index runs fastest: u, z and y
+// move as 64-byte rows, and the LDS strides below keep a wave's 64 lanes on
+// distinct banks in phases 2 and 3.
+// C1 (64 lanes, d_model 64): 4.7 ms of scan per compress, against 37.2 with
+// one thread per channel and 28.6 with four threads per channel each owning
+// four states (each recomputing the token's dt and gate, the output sum
+// handed along by DPP).  On large grids the h round trip through LDS and the
+// barriers cost more than they save: C2's 1000 lanes compress at 5.05 MB/s
+// this way against 5.63 with one thread per channel, C3's 8192 bf16 lanes at
+// 9.1 against 19.6; 250 lanes x 512 channels are even (4.89 both).
+constexpr int TBK_CPB = 16;  // channels per block (di is a multiple of 16)
 
-// Small grids (under one wave per SIMD, e.g. d_model 64 with 64 lanes;
-// the warm-start C2 probe's 250 lanes x 512 channels ran at 4.08 MB/s split
-// against 4.85 with one thread per channel, its 125 lanes at 3.99 against
-// 3.76), where one thread per channel leaves most SIMDs idle and every
-// token's latency exposed: P = DS / SPT threads share a channel, each owning
-// SPT states, and the delta rows are staged in LDS SCAN_TB tokens at a time.
-// Every thread of the group computes the token's dt (the same operations, so
-// the same value) and updates its states; the output sum y = fma(h_n, C_n, y)
-// then runs over n = 0 .. DS-1 in order, handed from thread to thread of the
-// group (SPT terms each), and the group's last thread adds D u, gates and
-// stores: the bits of scan_token.  C1 (64 lanes, d_model 64): 37.2 ms per
-// compress with one thread per channel, 28.6 ms with SPT 4 (8: 28.6, 2: 31.7,
-// 1: 41.8).
-template <int DS, int RB, int SPT, typename TA>
-__global__ __launch_bounds__(256) void scan_chunk_split_kernel(Dims D, LayerW Lw,
-                                                               const TA* __restrict__ xz,
-                                                               const TA* __restrict__ conv,
-                                                               const TA* __restrict__ delta,
-                                                               float* __restrict__ ssm_state,
-                                                               TA* __restrict__ y, int lanes,
-                                                               int T, int cpb) {
-  constexpr int P = DS / SPT;
-  static_assert(DS % SPT == 0 && P <= 16 && 16 % P == 0, "a group lies within a DPP row");
+template <int DS>
+struct TblkShape {
+  static constexpr int G = 16, SPT = DS / G;
+  static constexpr int TB = DS == 16 ? 32 : 16;  // tokens per pass
+  static constexpr int TPT = TB / G;              // phase 1/3 tokens per thread
+  static constexpr int HS = DS + 1;               // a token's h row
+  // per-channel strides, 4 mod 64 words: lanes (c, k) of a wave land on
+  // c * 4 + k (+ 17 k in phase 3) -- 64 distinct banks
+  static constexpr int TSTR = TB * 4 + ((4 - TB * 4 % 64) + 64) % 64;
+  static constexpr int CSTR = TB * HS + ((4 - TB * HS % 64) + 64) % 64;
+  template <int RB>
+  static constexpr int lds_floats() {
+    return TB * (RB + 2 * DS) + TBK_CPB * TSTR + TBK_CPB * CSTR;
+  }
+};
+
+template <int DS, int RB, typename TA>
+__global__ __launch_bounds__(256) void scan_chunk_tblk_kernel(Dims D, LayerW Lw,
+                                                              const TA* __restrict__ xz,
+                                                              const TA* __restrict__ conv,
+                                                              const TA* __restrict__ delta,
+                                                              float* __restrict__ ssm_state,
+                                                              TA* __restrict__ y, int lanes,
+                                                              int T) {
+  using S = TblkShape<DS>;
+  constexpr int G = S::G, SPT = S::SPT, TB = S::TB, TPT = S::TPT, HS = S::HS;
+  constexpr int NT = TBK_CPB * G;                   // threads
+  constexpr int ND = (TB * (RB + 2 * DS) + NT - 1) / NT;  // delta staging loads per thread
+  static_assert(DS % G == 0 && TB % G == 0, "whole states and tokens per thread");
   constexpr int M = sizeof(TA) == 2 ? MATH_HW : MATH_BF;
-  extern __shared__ float s_delta[];  // [SCAN_TB][R]
+  extern __shared__ __align__(16) float smem[];  // s_tok is read as float4
   const int di = D.di, R = D.R, r = D.r;
-  const int sub = threadIdx.x % P, cl = threadIdx.x / P;
-  const int base = blockIdx.x * cpb;  // cpb channels of one lane per block
+  const int cl = threadIdx.x % TBK_CPB, k = threadIdx.x / TBK_CPB;
+  float* s_delta = smem;                                                 // [TB][R]
+  float* s_tok = smem + TB * (RB + 2 * DS) + cl * S::TSTR;               // [TB][4]
+  float* s_h = smem + TB * (RB + 2 * DS) + TBK_CPB * S::TSTR + cl * S::CSTR;  // [TB][HS]
+  const int base = blockIdx.x * TBK_CPB;
   const int b = base / di;
-  const int c = base - b * di + cl;
-  float* ssm = ssm_state + ((size_t)b * di + c) * DS + SPT * sub;
+  const int c0 = base - b * di, c = c0 + cl;
+  float* ssm = ssm_state + ((size_t)b * di + c) * DS + SPT * k;
   float h[SPT], na[SPT], wdt[RB];
 #pragma unroll
   for (int n = 0; n < SPT; ++n) {
     h[n] = ssm[n];
-    na[n] = Lw.na2[(size_t)c * DS + SPT * sub + n];
+    na[n] = Lw.na2[(size_t)c * DS + SPT * k + n];
   }
 #pragma unroll
   for (int j = 0; j < RB; ++j) wdt[j] = j < r ? Lw.w_dt[(size_t)j * di + c] : 0.0f;
   const float bdt = Lw.b_dt[c], dd = Lw.dd[c];
   const TA* drows = delta + (size_t)b * T * R;
-  for (int t0 = 0; t0 < T; t0 += SCAN_TB) {
-    const int nt = min(SCAN_TB, T - t0);
-    __syncthreads();
-    for (int q = threadIdx.x; q < nt * R; q += blockDim.x)
-      s_delta[q] = ldv(drows + (size_t)t0 * R + q);
-    __syncthreads();
-    for (int tt = 0; tt < nt; ++tt) {
-      const size_t row = (size_t)b * T + t0 + tt;
-      const float* dv = s_delta + tt * R;
-      const float* Bv = dv + r;
-      const float* Cv = Bv + DS;
-      const float u = ldv(conv + row * di + c);
-      const float z = ldv(xz + row * 2 * di + di + c);
-      float acc = 0.0f;
+  const size_t row0 = (size_t)b * T;
+  float pd[ND], pu[TPT], pz[TPT];
+  auto fetch = [&](int t0) {
+    const int nt = min(TB, T - t0);
 #pragma unroll
-      for (int j = 0; j < RB; ++j)
-        if (j < r) acc = __builtin_fmaf(dv[j], wdt[j], acc);
-      const float dt = softplus<M>(acc + bdt);
-      const float dtu = dt * u;
+    for (int i = 0; i < ND; ++i) {
+      const int q = threadIdx.x + NT * i;
+      pd[i] = q < nt * R ? ldv(drows + (size_t)t0 * R + q) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TPT; ++i) {
+      const int tok = k + G * i;
+      const size_t row = row0 + t0 + tok;
+      pu[i] = tok < nt ? ldv(conv + row * di + c) : 0.0f;
+      pz[i] = tok < nt ? ldv(xz + row * 2 * di + di + c) : 0.0f;
+    }
+  };
+  fetch(0);
+  for (int t0 = 0; t0 < T; t0 += TB) {
+    const int nt = min(TB, T - t0);
+    __syncthreads();  // the previous pass no longer reads s_delta, s_tok, s_h
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const int q = threadIdx.x + NT * i;
+      if (q < nt * R) s_delta[q] = pd[i];
+    }
+    float cu[TPT], cz[TPT];
+#pragma unroll
+    for (int i = 0; i < TPT; ++i) {
+      cu[i] = pu[i];
+      cz[i] = pz[i];
+    }
+    if (t0 + TB < T) fetch(t0 + TB);
+    __syncthreads();
+    // 1. the scalars of tokens k, k + 16, ...
+#pragma unroll
+    for (int i = 0; i < TPT; ++i) {
+      const int tok = k + G * i;
+      if (tok < nt) {
+        const float* dv = s_delta + tok * R;
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RB; ++j)
+          if (j < r) acc = __builtin_fmaf(dv[j], wdt[j], acc);
+        const float dt = softplus<M>(acc + bdt);
+        const float sg = rcp_sel<M>(1.0f + exp_sel<M>(-cz[i]));
+        *reinterpret_cast<float4*>(s_tok + 4 * tok) =
+            make_float4(dt, dt * cu[i], dd * cu[i], cz[i] * sg);
+      }
+    }
+    __syncthreads();
+    // 2. states SPT k .. SPT k + SPT - 1 through the pass's tokens
+#pragma unroll 8
+    for (int tt = 0; tt < nt; ++tt) {
+      const float2 dd2 = *reinterpret_cast<const float2*>(s_tok + 4 * tt);
+      const float* Bv = s_delta + tt * R + r;
 #pragma unroll
       for (int n = 0; n < SPT; ++n) {
-        const float dA = exp2_neg_sel<M>(na[n] * dt);
-        h[n] = __builtin_fmaf(dA, h[n], Bv[SPT * sub + n] * dtu);
+        const float dA = exp2_neg_sel<M>(na[n] * dd2.x);
+        h[n] = __builtin_fmaf(dA, h[n], Bv[SPT * k + n] * dd2.y);
+        s_h[tt * HS + SPT * k + n] = h[n];
       }
-      float yv = 0.0f;
+    }
+    __syncthreads();
+    // 3. the outputs of tokens k, k + 16, ...
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        if (sub == p) {
+    for (int i = 0; i < TPT; ++i) {
+      const int tok = k + G * i;
+      if (tok < nt) {
+        const float* Cv = s_delta + tok * R + r + DS;
+        const float* hr = s_h + tok * HS;
+        float yv = 0.0f;
 #pragma unroll
-          for (int n = 0; n < SPT; ++n) yv = __builtin_fmaf(h[n], Cv[SPT * p + n], yv);
-        }
-        // thread p + 1 takes the running sum: a DPP shift by one lane within
-        // rows of 16 (P divides 16, so a group never straddles a row)
-        if (p + 1 < P)
-          yv = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                                             __builtin_bit_cast(int, yv), __builtin_bit_cast(int, yv),
-                                             0x111, 0xF, 0xF, false));
-      }
-      if (sub == P - 1) {
-        yv = yv + dd * u;
-        const float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));
-        stv(y + row * di + c, yv * (z * sg));
+        for (int n = 0; n < DS; ++n) yv = __builtin_fmaf(hr[n], Cv[n], yv);
+        const float4 tk = *reinterpret_cast<const float4*>(s_tok + 4 * tok);
+        yv = yv + tk.z;
+        stv(y + (row0 + t0 + tok) * di + c, yv * tk.w);
       }
     }
   }
@@ -569,8 +639,8 @@ static int block_for(int di) {
   return 0;
 }
 
-#ifndef BOA_SCAN_SPLIT_BELOW
-#define BOA_SCAN_SPLIT_BELOW (64 * 1024)  // threads: one wave per SIMD
+#ifndef BOA_SCAN_TBLK_BELOW
+#define BOA_SCAN_TBLK_BELOW (64 * 1024)  // threads: one wave per SIMD
 #endif
 
 template <int DS, int RB>
@@ -578,20 +648,18 @@ static hipError_t scan_chunk_go(const Dims& D, const LayerW& Lw, const void* xz,
                                 const void* delta, float* ssm_state, void* y, int lanes, int T,
                                 int bs, bool bf16, hipStream_t s) {
   const dim3 grid((lanes * D.di) / bs);
-  if ((int64_t)lanes * D.di < BOA_SCAN_SPLIT_BELOW) {
-    const size_t lds = sizeof(float) * SCAN_TB * D.R;
-    constexpr int SPT = 4, P = DS / SPT;
-    int cpb = 256 / P;  // channels per block: a power of two dividing di
-    while (cpb > 1 && D.di % cpb) cpb >>= 1;
-    const dim3 g2((lanes * D.di) / cpb);
+  if ((int64_t)lanes * D.di < BOA_SCAN_TBLK_BELOW) {
+    if (D.di % TBK_CPB) return hipErrorInvalidValue;
+    const size_t lds = sizeof(float) * TblkShape<DS>::template lds_floats<RB>();
+    const dim3 g2((lanes * D.di) / TBK_CPB);
     if (bf16)
-      BOA_LAUNCH((scan_chunk_split_kernel<DS, RB, SPT, uint16_t>), g2, dim3(cpb * P), lds, s, D,
+      BOA_LAUNCH((scan_chunk_tblk_kernel<DS, RB, uint16_t>), g2, dim3(TBK_CPB * 16), lds, s, D,
                  Lw, (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,
-                 (uint16_t*)y, lanes, T, cpb);
+                 (uint16_t*)y, lanes, T);
     else
-      BOA_LAUNCH((scan_chunk_split_kernel<DS, RB, SPT, float>), g2, dim3(cpb * P), lds, s, D, Lw,
+      BOA_LAUNCH((scan_chunk_tblk_kernel<DS, RB, float>), g2, dim3(TBK_CPB * 16), lds, s, D, Lw,
                  (const float*)xz, (const float*)conv, (const float*)delta, ssm_state, (float*)y,
-                 lanes, T, cpb);
+                 lanes, T);
   } else if (bf16 && D.r == RB)
     BOA_LAUNCH((scan_chunk_sload_kernel<DS, RB, true, uint16_t>), grid, dim3(bs), 0, s, D, Lw,
                (const uint16_t*)xz, (const uint16_t*)conv, (const uint16_t*)delta, ssm_state,

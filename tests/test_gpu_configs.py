@@ -62,17 +62,18 @@ def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
 @pytest.mark.parametrize("d,ds,prec", [(64, 16, "fp32"), (80, 16, "fp32"), (256, 16, "fp32"),
                                        (64, 16, "bf16"), (256, 16, "bf16"), (512, 32, "bf16")])
 def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
-    """The compress scan splits each channel's states over four-state thread
-    groups on small grids (under one wave per SIMD) and runs one thread per
-    channel with scalar-loaded delta rows otherwise: the same lanes' logits
-    are bit-identical between a small and a large batch, and (fp32) equal to
-    the oracle's."""
+    """The compress scan runs token-blocked (16 threads per channel, passes
+    of 32 tokens at d_state 16 and 16 at d_state 32) on small grids (under
+    one wave per SIMD) and one thread per channel with scalar-loaded delta
+    rows otherwise: the same lanes' logits are bit-identical between a small
+    and a large batch, and (fp32) equal to the oracle's.  70 tokens give
+    whole passes, a ragged last pass and a ragged 16-token block."""
     import boa_hip
     torch = torch_dev
     w = make_weights(d, 1, ds)
     di = 2 * d
     big = -(-64 * 1024 // di)  # the first lane count on the scalar-load form
-    small, T = 6, 20
+    small, T = 6, 70
     rng = np.random.default_rng(7 + d + ds)
     tok = rng.integers(0, 256, size=(big, T), dtype=np.uint8)
     out = []
