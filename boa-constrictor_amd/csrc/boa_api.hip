@@ -1014,7 +1014,7 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
     p.out = out; p.out_stride = chunk; p.states = c->dec; p.payload = d_payload;
     p.offsets = c->offsets; p.sizes = c->sizes;
     return timed(c, BOA_K_DECODE, 1024.0 * lanes * (maxlen - 1),
-                 [&] { return launch_dec_persist(p, D.d, D.ds, s); });
+                 [&] { return launch_dec_persist(p, D.d, D.ds, c->n_cus, s); });
   }
   // fp32 from 2048 lanes on: head.2 runs fused with the coder step
   // (dec_head_step_kernel), so the logits stay on chip; below that, and in

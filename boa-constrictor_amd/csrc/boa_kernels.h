@@ -257,7 +257,9 @@ struct PersistArgs {
   const int32_t* sizes;
 };
 bool dec_persist_fits(int d, int ds, int r, int L);
-hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, hipStream_t s);
+// lanes per block: the fewest (4, 8, 16) whose grid fits n_cus workgroups
+int dec_persist_lanes_per_block(int lanes, int n_cus);
+hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, int n_cus, hipStream_t s);
 
 // ---- group-synchronous decode step (decode.hip) ------------------------
 // One launch runs a whole step (every layer, the head, the CDF, the search

@@ -29,7 +29,7 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int PL = 16;  // lanes per block
+constexpr int PL = 16;  // MFMA rows of the block's tiles: the lane capacity of its LDS rows
 
 // One 16 x 16 tile of the block's 16 lanes and features n0 .. n0 + 15.  A:
 // activations in LDS, k-blocked with lane capacity 16 (feature k of lane m at
@@ -146,8 +146,16 @@ __device__ __forceinline__ void pd_ln_apply(const float* xs, float* xn, const fl
 
 }  // namespace
 
-template <int NB, int RB>
+// LP lanes per block (16, 8 or 4): rows LP .. 15 of every MFMA tile are
+// inert (an MFMA output column depends on its own row of activations only;
+// their loads read a lane of this block and nothing is stored for them), so
+// a block's matrix-core chains cost the same for any LP, while its VALU
+// phases (the scan's 16 exponentials per channel, GELU, the CDF) scale with
+// LP.  Fewer lanes per block spread those phases over more CUs.
+template <int NB, int RB, int LP>
 __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
+  static_assert(LP == 4 || LP == 8 || LP == 16, "lanes per block");
+  constexpr int LSH = LP == 4 ? 2 : LP == 8 ? 3 : 4;
   constexpr int d = NB * 16, DI = 2 * d, NBI = 2 * NB, NBF = 4 * NB, DS = 16;
   constexpr int NBX = (RB + 2 * DS + 15) / 16;  // 16-blocks of the x_proj row
   constexpr int RW = NBX * 16 + 1;              // LDS row stride of the x_proj rows
@@ -172,15 +180,15 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
   __shared__ __align__(16) float prm[PERSIST_MAX_LAYERS * PSZ];
   __shared__ float hb1[d], hb2[256];
   const int tid0 = threadIdx.x;
-  const int m0 = blockIdx.x * PL;
+  const int m0 = blockIdx.x * LP;
   // coder: half-wave h < 16 decodes lane m0 + h; its lane 0 holds the state
   const int half = tid0 >> 5, l = tid0 & 31;
   const int mh = m0 + half;
-  const bool coder_lane = half < PL && mh < a.lanes;
+  const bool coder_lane = half < LP && mh < a.lanes;
   RcDec st{};
   if (coder_lane && l == 0) st = a.states[mh];
   const int len_h = coder_lane ? a.lens[mh] : 0;
-  if (tid0 < PL) tok_s[tid0] = a.tok[min(m0 + tid0, a.lanes - 1)];
+  if (tid0 < PL) tok_s[tid0] = tid0 < LP ? a.tok[min(m0 + tid0, a.lanes - 1)] : 0;
   auto stage = [&](float* dst, const float* __restrict__ src, int n) {
     for (int k = tid0; k < n; k += 1024) dst[k] = src[k];
   };
@@ -207,8 +215,8 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
     int tid = tid0;
     asm volatile("" : "+v"(tid));
     const int wv = tid >> 6, i = tid & 15, g = (tid >> 4) & 3;
-    const int mi = min(m0 + i, a.lanes - 1);  // lane of MFMA row i (state index)
-    const bool mi_ok = m0 + i < a.lanes;
+    const int mi = min(m0 + min(i, LP - 1), a.lanes - 1);  // lane of MFMA row i (state index)
+    const bool mi_ok = i < LP && m0 + i < a.lanes;
 #pragma unroll
     for (int li = 0; li < PERSIST_MAX_LAYERS; ++li) {  // unrolled: constant kernel-argument offsets
       if (li >= a.L) break;
@@ -265,8 +273,8 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
       __syncthreads();
       // scan: item (lane lm, channel c), the operations of dec_scan_kernel
 #pragma unroll 1
-      for (int it = tid; it < PL * DI; it += 1024) {
-        const int cl = it & 15, lm = (it >> 4) & 15, cb = it >> 8;
+      for (int it = tid; it < LP * DI; it += 1024) {
+        const int cl = it & 15, lm = (it >> 4) & (LP - 1), cb = it >> (4 + LSH);
         const int c = cb * 16 + cl;
         const int m = min(m0 + lm, a.lanes - 1);
         float4* h4 = reinterpret_cast<float4*>(P.ssm);
@@ -355,7 +363,7 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
     }
     __syncthreads();
     // CDF of each lane's row on its half-wave
-    if (half < PL) {
+    if (half < LP) {
       double r[8];
       cdf_halfwave_regs(lg + half * 256, hb2, a.inv_t, l, r);
 #pragma unroll
@@ -403,10 +411,23 @@ bool dec_persist_fits(int d, int ds, int r, int L) {
   return d == 64 && ds == 16 && dec_rb(r) == 8 && L >= 1 && L <= PERSIST_MAX_LAYERS;
 }
 
-hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, hipStream_t s) {
+int dec_persist_lanes_per_block(int lanes, int n_cus) {
+  for (int lp = 4; lp < PL; lp *= 2)
+    if ((lanes + lp - 1) / lp <= n_cus) return lp;
+  return PL;
+}
+
+hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, int n_cus, hipStream_t s) {
   if (a.lanes <= 0 || a.maxlen <= 1) return hipSuccess;
   if (!dec_persist_fits(d, ds, a.r, a.L)) return hipErrorInvalidValue;
-  BOA_LAUNCH((dec_persist_kernel<4, 8>), dim3((a.lanes + PL - 1) / PL), dim3(1024), 0, s, a);
+  const int lp = dec_persist_lanes_per_block(a.lanes, n_cus);
+  const dim3 grid((a.lanes + lp - 1) / lp), block(1024);
+  if (lp == 4)
+    BOA_LAUNCH((dec_persist_kernel<4, 8, 4>), grid, block, 0, s, a);
+  else if (lp == 8)
+    BOA_LAUNCH((dec_persist_kernel<4, 8, 8>), grid, block, 0, s, a);
+  else
+    BOA_LAUNCH((dec_persist_kernel<4, 8, 16>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 

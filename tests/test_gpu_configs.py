@@ -93,6 +93,26 @@ def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
         assert np.array_equal(out[1].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("lanes", [6, 1000, 1500, 5000])
+def test_persistent_decode_lanes_per_block(torch_dev, oracle, make_weights, lanes):
+    """The d_model-64 persistent decode gives each block 4, 8 or 16 lanes,
+    the fewest whose grid fits the CUs (on 256 CUs: 4 up to 1024 lanes, 8 up
+    to 2048, then 16), and leaves the MFMA rows beyond them inert.  Every
+    block size, with a partial last block and a ragged last chunk, gives the
+    oracle's container bytes and a byte-identical round trip."""
+    w = make_weights(64, 2, 16)
+    chunk = 24
+    rng = np.random.default_rng(lanes)
+    data = rng.integers(0, 256, size=lanes * chunk - 5, dtype=np.uint8).tobytes()
+    c = _codec(64, 2, 16, lanes=lanes, w=w)
+    assert c.decode_plan(lanes)["persistent"]
+    blob = c.compress(data, chunk_size=chunk)
+    want = oracle.Model(w, 64, 2).compress(data, chunk_size=chunk)
+    assert blob == want, f"container differs ({len(blob)} vs {len(want)} bytes)"
+    assert c.decompress(blob) == data
+    c.close()
+
+
 def test_layernorm_in_gemm_epilogues(torch_dev, oracle, make_weights):
     """At d_model 256 with 16384 rows or more in a call (128 x 256 GEMM
     tiles) the fp32 pass runs LN2 in out_proj's epilogue and the next layer's
