@@ -361,8 +361,12 @@ def main() -> int:
     sc = prof["scan"]
     r_dt = -(-d // 16)
     rb = 8 if r_dt <= 8 else (16 if r_dt <= 16 else 32)
-    scan_kernel = (f"boa::scan_chunk_sload_kernel<{ds}, {rb}, {str(r_dt == rb).lower()}, "
-                   f"{'float' if prec == 'fp32' else 'unsigned short'}>")
+    ta = "float" if prec == "fp32" else "unsigned short"
+    comp_lanes = min(args.warm_start, n_chunks) if args.warm_start else n_chunks
+    if comp_lanes * 2 * d < 64 * 1024:  # under one wave per SIMD: the token-blocked form
+        scan_kernel = f"boa::scan_chunk_tblk_kernel<{ds}, {rb}, {ta}>"
+    else:
+        scan_kernel = f"boa::scan_chunk_sload_kernel<{ds}, {rb}, {str(r_dt == rb).lower()}, {ta}>"
 
     # The decode step's kernels on directly launched steps (boa_step_batch)
     # after the timed region, each launch timed by the HIP events its

@@ -100,6 +100,28 @@ __device__ __forceinline__ void dec_advance(RcDec& st, uint32_t low, uint32_t hi
   }
 }
 
+// dec_advance for a decoder that keeps running across steps in registers:
+// nw holds the word at read_idx_words (0 past the end), loaded when the
+// previous word was taken, so the load's latency overlaps the steps between
+// two renormalisations.  The state sequence is dec_advance's.
+__device__ __forceinline__ void dec_advance_ahead(RcDec& st, uint32_t low, uint32_t high,
+                                                  const uint32_t* in, int32_t n_words,
+                                                  uint32_t& nw) {
+  const uint64_t scale = st.range >> 24;
+  uint32_t prob = high - low;
+  if (prob == 0) prob = 1;
+  st.lower = st.lower + scale * (uint64_t)low;
+  st.range = scale * (uint64_t)prob;
+  for (int it = 0; it < 2 && st.range < (1ull << 32); ++it) {
+    st.lower <<= 32;
+    st.range <<= 32;
+    const uint32_t w = nw;
+    if (st.read_idx_words < n_words) ++st.read_idx_words;
+    nw = st.read_idx_words < n_words ? in[st.read_idx_words] : 0u;
+    st.point = (st.point << 32) | (uint64_t)w;
+  }
+}
+
 // ------------------------------------------------------------------- CDF
 // The cumulative probabilities of one logits row `lg` on a half-wave: lane
 // l ends with the exclusive running sums r[i] of symbols 8l + i.

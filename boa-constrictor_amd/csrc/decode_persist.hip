@@ -188,6 +188,17 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
   RcDec st{};
   if (coder_lane && l == 0) st = a.states[mh];
   const int len_h = coder_lane ? a.lens[mh] : 0;
+  // the lane's stream, read once (the byte stores of the step loop could
+  // alias these arrays, so the compiler would reload them every step) and
+  // its next word loaded ahead (dec_advance_ahead)
+  const uint32_t* pin = nullptr;
+  int32_t pn = 0;
+  uint32_t nw = 0;
+  if (coder_lane && l == 0) {
+    pin = a.payload + a.offsets[mh];
+    pn = a.sizes[mh];
+    nw = st.read_idx_words < pn ? pin[st.read_idx_words] : 0u;
+  }
   if (tid0 < PL) tok_s[tid0] = tid0 < LP ? a.tok[min(m0 + tid0, a.lanes - 1)] : 0;
   auto stage = [&](float* dst, const float* __restrict__ src, int n) {
     for (int k = tid0; k < n; k += 1024) dst[k] = src[k];
@@ -393,7 +404,7 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
         }
       }
       if (l == 0) {
-        dec_advance(st, low_s, high_s, a.payload + a.offsets[mh], a.sizes[mh]);
+        dec_advance_ahead(st, low_s, high_s, pin, pn, nw);
         a.out[(size_t)mh * a.out_stride + t] = (uint8_t)sym;
         tok_s[half] = sym;
       }
