@@ -118,6 +118,10 @@ __device__ __forceinline__ void scan_store(const ScanCtx<DS, RB>& sc, float* ssm
 // (the decay taken as 2^(na2_n dt), na2 = -exp(A_log) log2(e)),
 // out = y * (z * sigmoid(z)).  M selects the exp/log form (MATH_BF and
 // MATH_BR give the same results).
+// The update rounds every product and sum on its own, as the reference's
+// __fmul_rn / __fadd_rn lines do (mamba_kernels.cu:332-335, 453-461):
+// dB = dt B_n, h_n = (dA h_n) + (dB u), y = y + (h_n C_n); the build's
+// -ffp-contract=off keeps the compiler from fusing them.
 template <int DS, int RB, int M = MATH_BF>
 __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt_in,
                                             const float* bc, int r, float u, float z) {
@@ -128,15 +132,13 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
   const float dt = softplus<M>(acc + sc.bdt);
   const float* Bv = bc;
   const float* Cv = bc + DS;
-  // h_n = fma(dA, h_n, B_n (dt u)) and y = fma(h_n, C_n, y): the update in
-  // fused form, dt u formed once
-  const float dtu = dt * u;
   float y = 0.0f;
 #pragma unroll
   for (int n = 0; n < DS; ++n) {
     const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
-    sc.h[n] = __builtin_fmaf(dA, sc.h[n], Bv[n] * dtu);
-    y = __builtin_fmaf(sc.h[n], Cv[n], y);
+    const float dB = dt * Bv[n];
+    sc.h[n] = dA * sc.h[n] + dB * u;
+    y = y + sc.h[n] * Cv[n];
   }
   y = y + sc.dd * u;
   float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));

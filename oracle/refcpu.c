@@ -783,19 +783,42 @@ static inline float scan_row(const ref_layer* Ly, const ref_model* m, int dch, c
     const float* Bv = delta_row + r;
     const float* Cv = delta_row + r + ds;
     const float* na = Ly->na2 + (size_t)dch * ds;
-    /* h_n = dA h_n + (dt B_n) u as fmaf(dA, h_n, B_n (dt u)), y by fmaf:
-     * the contraction nvcc applies to the reference's expressions, with
-     * dt u formed once per element */
-    const float dtu = dt * u;
+    /* the reference's unfused update, every product and sum rounded on its
+     * own (__fmul_rn / __fadd_rn at mamba_kernels.cu:332-335 and :453-461):
+     * dB = dt B_n; h_n = (dA h_n) + (dB u); y = y + (h_n C_n) */
     float y = 0.0f;
     for (int n = 0; n < ds; ++n) {
         float dA = ref_exp2_neg(na[n] * dt);
-        h[n] = fmaf(dA, h[n], Bv[n] * dtu);
-        y = fmaf(h[n], Cv[n], y);
+        float dB = dt * Bv[n];
+        h[n] = dA * h[n] + dB * u;
+        y = y + h[n] * Cv[n];
     }
     y = y + Ly->dd[dch] * u;
     float sg = 1.0f / (1.0f + ref_expf(-z));
     return y * (z * sg);
+}
+
+/* scan_row over T consecutive tokens of one channel (dt_proj row w_dt[r],
+ * its bias, D, the channel's A_log[ds] and state h[ds]; delta rows of
+ * r + 2 ds floats): the chunk-mode scan of mamba_kernels.cu:414-470 with
+ * the dt_proj + softplus of boa_gpu.hpp:317-318 and the gate of
+ * mamba_kernels.cu:130-151.  A test hook for the update's rounding. */
+void ref_scan_channel(const float* w_dt, float b_dt, float dd, const float* a_log, int32_t r,
+                      int32_t ds, int32_t T, const float* delta, const float* u, const float* z,
+                      float* h, float* y) {
+    ref_layer Ly;
+    ref_model m;
+    float na2[64];
+    memset(&Ly, 0, sizeof Ly);
+    memset(&m, 0, sizeof m);
+    for (int n = 0; n < ds && n < 64; ++n) na2[n] = ref_scan_na2(a_log[n]);
+    Ly.w_dt = (float*)w_dt;  /* di = 1: w_dt[j * di + 0] = w_dt[j] */
+    Ly.b_dt = &b_dt;
+    Ly.dd = &dd;
+    Ly.na2 = na2;
+    m.r = r; m.ds = ds; m.di = 1; m.R = r + 2 * ds;
+    for (int t = 0; t < T; ++t)
+        y[t] = scan_row(&Ly, &m, 0, delta + (size_t)t * m.R, u[t], z[t], h);
 }
 
 /* One mambav1 block over `rows` rows held in sc->x.  chunk mode: the rows

@@ -110,6 +110,12 @@ void ref_cdf_from_probs(const float* probs, int32_t K, uint32_t* cdf);
 /* first k with low_k <= target < high_k (0,0,0 if none) */
 int32_t ref_cdf_search(const double* s_cdf, uint32_t target, uint32_t* low, uint32_t* high);
 
+/* one channel's chunk-mode scan over T tokens (test hook, ds <= 64):
+ * delta [T][r + 2 ds], u, z, y [T], state h [ds] updated in place */
+void ref_scan_channel(const float* w_dt, float b_dt, float dd, const float* a_log, int32_t r,
+                      int32_t ds, int32_t T, const float* delta, const float* u, const float* z,
+                      float* h, float* y);
+
 /* --------------------------------------------------------------- model */
 typedef struct ref_model ref_model;
 typedef struct ref_state ref_state;

@@ -69,6 +69,8 @@ def lib():
             "ref_gelu": (C.c_float, [C.c_float]),
             "ref_silu": (C.c_float, [C.c_float]),
             "ref_softplus": (C.c_float, [C.c_float]),
+            "ref_scan_channel": (None, [f32p, C.c_float, C.c_float, f32p, C.c_int32, C.c_int32,
+                                        C.c_int32, f32p, f32p, f32p, f32p, f32p]),
             "ref_half_to_float": (C.c_float, [C.c_uint16]),
             "ref_rc_enc_init": (None, [C.POINTER(RcEnc)]),
             "ref_rc_enc_put": (None, [C.POINTER(RcEnc), C.c_uint32, C.c_uint32, u32p]),
@@ -157,6 +159,22 @@ def decode_cdf_stream(cdf, n_sym, words):
     out = np.zeros(n_sym, np.uint8)
     lib().ref_rc_decode_cdf_stream(cdf, n_sym, w, nw, out)
     return out
+
+
+def scan_channel(w_dt, b_dt, dd, a_log, delta, u, z, h):
+    """One channel's chunk-mode scan over T tokens (ref_scan_channel):
+    returns (y [T], new state [ds])."""
+    w_dt = np.ascontiguousarray(w_dt, dtype=np.float32)
+    a_log = np.ascontiguousarray(a_log, dtype=np.float32)
+    delta = np.ascontiguousarray(delta, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    z = np.ascontiguousarray(z, dtype=np.float32)
+    hs = np.array(h, dtype=np.float32)
+    T, ds, r = len(u), len(a_log), len(w_dt)
+    assert delta.shape == (T, r + 2 * ds) and ds <= 64
+    y = np.empty(T, np.float32)
+    lib().ref_scan_channel(w_dt, float(b_dt), float(dd), a_log, r, ds, T, delta, u, z, hs, y)
+    return y, hs
 
 
 class Model:

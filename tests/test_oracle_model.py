@@ -85,6 +85,82 @@ def test_forward_matches_float64_restatement(oracle, weights_dir, d, L, ds):
         np.testing.assert_allclose(got[b], want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
 
 
+def test_long_sequence_matches_float64_restatement(oracle, weights_dir):
+    """C2's width over 2,048 tokens: with dt about 1e-3 .. 1e-1 the scan state
+    carries hundreds to thousands of steps of history, so rounding drift in
+    the recurrence would show here and not in 30-token runs."""
+    d, L, ds, T = 256, 2, 16, 2048
+    tensors = synth.random_weight_tensors(d, L, ds, seed=0)
+    path = weights_dir / f"np_long_{d}_{L}_{ds}.bin"
+    synth.write_weights(str(path), tensors)
+    rng = np.random.default_rng(11)
+    tok = rng.integers(0, 256, size=(2, T), dtype=np.uint8)
+    got = oracle.Model(path, d, L, ds).new_state(2).forward_chunk(tok)
+    for b in range(2):
+        want = np_forward(tensors, tok[b], d, L, ds)
+        np.testing.assert_allclose(got[b], want, rtol=1e-4, atol=1e-4 * np.abs(want).max())
+
+
+def _scan_float32_reference_order(oracle, w_dt, b_dt, dd, a_log, delta, u, z, h, fused=False):
+    """The reference's chunk scan (mamba_kernels.cu:414-470, every product
+    and sum rounded on its own: dB = dt B; h = (dA h) + (dB u); y = y + h C;
+    y = y + D u) followed by the gate (:130-151), in numpy float32, whose
+    scalar + and * are single IEEE roundings.  The transcendentals (softplus,
+    the base-2 decay, exp) are the oracle's own, pinned elsewhere.
+    fused=True computes the fma form h = fma(dA, h, B (dt u)),
+    y = fma(h, C, y) instead (float64 products then one rounding), the form
+    the update must not take."""
+    L = oracle.lib()
+    f = np.float32
+    r, ds = len(w_dt), len(a_log)
+    na2 = [f(L.ref_scan_na2(float(a))) for a in a_log]
+    h = [f(v) for v in h]
+    ys = []
+    for t in range(len(u)):
+        # the dt inputs and weights are dyadic, so the K-order chain is exact
+        acc = f(sum(float(delta[t, j]) * float(w_dt[j]) for j in range(r)))
+        dt = f(L.ref_softplus(float(acc + f(b_dt))))
+        ut, B, Cv = f(u[t]), delta[t, r:r + ds], delta[t, r + ds:]
+        y = f(0.0)
+        if fused:
+            dtu = f(dt * ut)
+        for n in range(ds):
+            dA = f(L.ref_exp2_neg(float(na2[n] * dt)))
+            if fused:
+                h[n] = f(float(dA) * float(h[n]) + float(f(B[n] * dtu)))
+                y = f(float(h[n]) * float(Cv[n]) + float(y))
+            else:
+                dB = dt * f(B[n])
+                h[n] = dA * h[n] + dB * ut
+                y = y + h[n] * f(Cv[n])
+        y = y + f(dd) * ut
+        sg = f(1.0) / (f(1.0) + f(L.ref_expf(float(-f(z[t])))))
+        ys.append(y * (f(z[t]) * sg))
+    return np.array(ys, np.float32), np.array(h, np.float32)
+
+
+def test_scan_update_rounds_like_the_reference(oracle):
+    """The oracle's scan rounds every product and sum of the state update on
+    its own, as the reference's __fmul_rn / __fadd_rn lines do, bit for bit
+    over 4,096 tokens; the fused (fma) form differs, so the check sees it."""
+    rng = np.random.default_rng(21)
+    r, ds, T = 16, 16, 4096
+    w_dt = (rng.integers(-8, 9, size=r) / 64).astype(np.float32)
+    a_log = np.log(np.arange(1, ds + 1)).astype(np.float32)
+    delta = rng.standard_normal((T, r + 2 * ds)).astype(np.float32)
+    delta[:, :r] = rng.integers(-8, 9, size=(T, r)) / 16
+    u = rng.standard_normal(T).astype(np.float32)
+    z = rng.standard_normal(T).astype(np.float32)
+    h0 = (0.1 * rng.standard_normal(ds)).astype(np.float32)
+    b_dt, dd = -4.5, 1.0
+    y, h = oracle.scan_channel(w_dt, b_dt, dd, a_log, delta, u, z, h0)
+    want_y, want_h = _scan_float32_reference_order(oracle, w_dt, b_dt, dd, a_log, delta, u, z, h0)
+    assert np.array_equal(y.view(np.uint32), want_y.view(np.uint32))
+    assert np.array_equal(h.view(np.uint32), want_h.view(np.uint32))
+    fy, fh = _scan_float32_reference_order(oracle, w_dt, b_dt, dd, a_log, delta, u, z, h0, fused=True)
+    assert not np.array_equal(fy.view(np.uint32), y.view(np.uint32))
+
+
 def test_chunk_step_and_tile_bit_identity(oracle, w_c1):
     m = oracle.Model(w_c1, 64, 2)
     rng = np.random.default_rng(8)
