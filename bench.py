@@ -86,6 +86,35 @@ def copy_calibration(nbytes: int, reps: int) -> int:
     return 0
 
 
+def decode_steps_only(config: str, steps: int, lanes: int = 0) -> int:
+    """Only `steps` directly launched decode steps (boa_step_batch) of the
+    config's model (random-init, seed 0) over its lane count: the workload of
+    the decode-step counter profiles (rocprofv3 --pmc)."""
+    import torch
+    import boa_hip
+    import synth
+    cfg = synth.CONFIGS[config]
+    d, L, ds, prec = cfg["d_model"], cfg["n_layers"], cfg["d_state"], cfg["precision"]
+    lanes = lanes or cfg["chunks"]
+    tmp = tempfile.mkdtemp(prefix="boa_steps_")
+    w = os.path.join(tmp, f"{config}.bin")
+    synth.write_random_weights(w, d, L, ds, seed=0)
+    c = boa_hip.Codec(d, L, ds, max_lanes=lanes, precision=prec)
+    c.set_stream(torch.cuda.current_stream().cuda_stream)
+    c.load_weights(w)
+    c.reset_state(lanes)
+    tok = torch.randint(0, 256, (lanes,), dtype=torch.uint8, device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(0))
+    logits = torch.empty(lanes * 256, dtype=torch.float32, device="cuda")
+    for _ in range(steps):
+        c.step_batch(tok.data_ptr(), lanes, logits.data_ptr())
+    torch.cuda.synchronize()
+    c.close()
+    print(json.dumps({"decode_steps": steps, "config": config, "lanes": lanes,
+                      "plan": "boa_step_batch, directly launched"}), flush=True)
+    return 0
+
+
 def uvarint_len(x: int) -> int:
     n = 1
     while x >= 0x80:
@@ -101,8 +130,15 @@ def container_bytes(stream_bytes, n_chunks) -> int:
 
 def cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, sample_len, threads, d, L, ds,
                  bf16=False):
-    """Time the CPU oracle on the first `sample_chunks` chunks x `sample_len` bytes."""
+    """Time the CPU oracle on the first `sample_chunks` chunks x `sample_len`
+    bytes, built for x86-64-v4 (AVX-512) where the host has it, else for
+    x86-64-v3 (AVX2 + FMA); both builds compute the same bits."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    if "refcpu" not in sys.modules:
+        with open("/proc/cpuinfo") as f:
+            flags = next((ln.split(":", 1)[1].split() for ln in f if ln.startswith("flags")), [])
+        if {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= set(flags):
+            os.environ["REFCPU_ISA"] = "v4"
     import refcpu
     sample = b"".join(data[c * chunk: c * chunk + sample_len] for c in range(min(sample_chunks, n_chunks)))
     m = refcpu.Model(weights, d, L, ds, bf16=bf16)
@@ -116,7 +152,7 @@ def cpu_baseline(weights, data, chunk, n_chunks, sample_chunks, sample_len, thre
     return dict(compress_mb_s=len(sample) / (t1 - t0) / 1e6,
                 decompress_mb_s=len(sample) / (t2 - t1) / 1e6,
                 bytes=len(sample), compress_s=t1 - t0, decompress_s=t2 - t1,
-                blob=blob)
+                blob=blob, isa=refcpu.ISA, lib=os.path.basename(refcpu.LIB_PATH))
 
 
 def decode_step_profile(codec, lanes: int, steps: int = 32) -> dict:
@@ -203,9 +239,14 @@ def main() -> int:
                          "--gpu-batch B); not the metric config")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
+    ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
+                    help="only run N directly launched decode steps of --config over its "
+                         "lane count (the workload of the decode counter profiles)")
     args = ap.parse_args()
     if args.copy_calibrate:
         return copy_calibration(args.copy_calibrate, 5)
+    if args.decode_steps:
+        return decode_steps_only(args.config, args.decode_steps, args.chunks)
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -487,6 +528,8 @@ def main() -> int:
                          f"({cb['bytes']} B), oracle/refcpu compress (OpenMP over chunks)",
                "decompress_value": round(cb["decompress_mb_s"], 5),
                "compress_s": round(cb["compress_s"], 2), "decompress_s": round(cb["decompress_s"], 2),
+               "isa": {"v4": "x86-64-v4 (AVX-512)", "v3": "x86-64-v3 (AVX2 + FMA)"}.get(cb["isa"], cb["isa"]),
+               "build": f"gcc -O3 -march=x86-64-{cb['isa']} -ffp-contract=off -fopenmp ({cb['lib']})",
                "host": info,
                "threads_rule": "OMP_NUM_THREADS of the GPU box (its CPU share for one GPU), "
                                "else every core in the process's affinity mask"}

@@ -22,7 +22,7 @@ BOA_OK = 0
 (K_GEMM, K_SCAN, K_CONV, K_LN, K_CDF, K_CODER, K_DECODE, K_GEMM_SMALL, K_DEC_GEMM,
  K_DEC_SCAN, K_HEAD_CDF, K_DEC_LNGEMM) = range(12)
 K_NAMES = ["gemm", "scan", "conv", "ln", "cdf", "coder", "decode", "gemm_small", "dec_gemm",
-           "dec_scan", "head_cdf", "dec_lngemm", "dec_step"]
+           "dec_scan", "head_cdf", "dec_lngemm"]
 BOA_E_ARG, BOA_E_HIP, BOA_E_IO, BOA_E_FORMAT, BOA_E_STATE, BOA_E_NOMEM = -1, -2, -3, -4, -5, -6
 
 # void (*)(void* user, int32_t phase, int64_t done_bytes, int64_t total_bytes)
@@ -77,7 +77,6 @@ def lib():
             "boa_set_progress": (C.c_int, [P, PROGRESS_FN, P]),
             "boa_decode_plan": (C.c_int, [P, i32, C.POINTER(i32), C.POINTER(i32)]),
             "boa_set_state_cache_budget": (C.c_int, [P, i64]),
-            "boa_set_decode_group": (C.c_int, [P, i32]),
             "boa_last_timings": (C.c_int, [P, C.POINTER(C.c_double), C.POINTER(C.c_double),
                                            C.POINTER(C.c_double)]),
             "boa_load_weights": (C.c_int, [P, C.c_char_p]),
@@ -227,17 +226,12 @@ class Codec:
 
     def decode_plan(self, lanes):
         """The decode step's schedule at `lanes` lanes: dict(cached_layers,
-        fused_ln, persistent, fused_xproj, fused_head, group_step)."""
+        fused_ln, persistent, fused_xproj, fused_head)."""
         a, f = C.c_int32(), C.c_int32()
         self._check(lib().boa_decode_plan(self.h, lanes, C.byref(a), C.byref(f)), "decode_plan")
         return dict(cached_layers=a.value, fused_ln=bool(f.value & 1),
                     persistent=bool(f.value & 2), fused_xproj=bool(f.value & 4),
-                    fused_head=bool(f.value & 8), group_step=bool(f.value & 16))
-
-    def set_decode_group(self, enable):
-        """Run the decode step as one group-synchronous launch where it
-        applies (True) or as its chain of launches (False, the default)."""
-        self._check(lib().boa_set_decode_group(self.h, 1 if enable else 0), "set_decode_group")
+                    fused_head=bool(f.value & 8))
 
     def last_timings(self):
         """(h2d_s, compute_s, d2h_s) of the last compress()/decompress() call."""

@@ -131,15 +131,7 @@ struct boa_ctx {
   uint8_t* tok = nullptr;
   int* t_counter = nullptr;     // decode step counter (device)
 
-  // group-synchronous decode step (dec_group_step_kernel): its plan, a host
-  // copy and a device copy, and one allocation (gaux) holding the per-group
-  // barrier counters, decoded positions and the abort flag; group_step = 0
-  // (the default) runs the launch chain instead
-  int group_step = 0;
-  int n_cus = 0;
-  GroupPlan* h_gplan = nullptr;
-  GroupPlan* d_gplan = nullptr;
-  unsigned* gaux = nullptr;
+  int n_cus = 0;  // compute units of the device (persistent decode grid)
 
   // decompress: every step is replayed from a HIP graph on dec_stream; the
   // executable graph is kept while the step's launch arguments stay the same
@@ -153,7 +145,6 @@ struct boa_ctx {
     const uint32_t* payload = nullptr;
     float inv_temp = 0.0f;
     hipStream_t stream = nullptr;
-    bool group = false;
   } dec_key;
   int32_t* h_sizes = nullptr;  // pinned
 
@@ -269,11 +260,21 @@ hipError_t timed(boa_ctx* c, int cls, double work, F&& f) {
 }
 
 // ---- model dims --------------------------------------------------------------
+// The widths the kernels are built for; a model of another d_model (at most
+// 512) runs at the next one up, its extra features zero (see Dims).  bf16
+// needs widths that are multiples of 64.
+int kernel_width(int d, bool bf16) {
+  for (int w : {64, 80, 128, 256, 512})
+    if (d <= w && !(bf16 && w % 64)) return w;
+  return 0;
+}
+
 Dims make_dims(const boa_config& cfg) {
   Dims D{};
-  D.d = cfg.d_model;
+  D.dn = cfg.d_model;
+  D.d = kernel_width(cfg.d_model, cfg.precision == 1);
   D.L = cfg.n_layers;
-  D.di = 2 * cfg.d_model;
+  D.di = 2 * D.d;
   D.r = (cfg.d_model + 15) / 16;
   D.ds = cfg.d_state;
   D.R = D.r + 2 * D.ds;
@@ -355,7 +356,7 @@ hipError_t gemm_ln(boa_ctx* c, const float* X, int ldx, const float* W, int ldw,
                    const float* bias, const float* res, int ldr, int M, int K, const float* ln_w,
                    const float* ln_b, float* out, int mode) {
   GemmArgs a{X, ldx, W, ldw, C, ldc, bias, res, ldr, M, 256, K, ACT_NONE};
-  const LnEpi ln{ln_w, ln_b, out, 256, mode};
+  const LnEpi ln{ln_w, ln_b, out, 256, mode, c->D.dn};
   return timed(c, BOA_K_GEMM, 2.0 * M * 256 * K, [&] { return gemm_f32_ln(a, ln, c->stream); });
 }
 
@@ -386,9 +387,9 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
   if (l == 0 || !fuse_ln)
     e = timed(c, BOA_K_LN, ln_bytes, [&] {
       return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
-                                 true, s)
+                                 D.dn, true, s)
                     : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn,
-                                 W.ln1_w, W.ln1_b, rows, D.d, true, s);
+                                 W.ln1_w, W.ln1_b, rows, D.d, D.dn, true, s);
     });
   if (!e) e = gemmb(c, c->xn, B.w_in, c->xz, 2 * D.di, true, nullptr, W.b_in, nullptr, 0, rows,
                     2 * D.di, D.d, ACT_NONE);
@@ -408,7 +409,7 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
                     D.di, ACT_NONE);
   if (!e && !fuse_ln)
     e = timed(c, BOA_K_LN, 2.0 * 2 * rows * D.d,
-              [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, true, s); });
+              [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, D.dn, true, s); });
   // d_model 256: FF1 + GELU + FF2 in one kernel, the hidden layer kept in
   // LDS (MI355X, C3 probe: bf16 GEMMs 131.9 -> 125.1 ms, compress 17.52 ->
   // 18.07 MB/s).  At d_model 512 the fused form, with 64-row blocks that
@@ -417,6 +418,7 @@ hipError_t block_forward_b16(boa_ctx* c, int l, int rows, int lanes, int T, cons
     if (e) return e;
     FfnB16Args f{(const uint16_t*)c->xn, B.w1, B.w2, W.b1, W.b2, c->x, c->x,
                  l == D.L - 1 ? (uint16_t*)c->y : nullptr, rows, D.d};
+    f.n = D.dn;
     if (fuse_ln) {
       f.ln2_w = W.ln2_w;
       f.ln2_b = W.ln2_b;
@@ -454,9 +456,9 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
   if (l == 0 || !fuse_ln) {
     e = timed(c, BOA_K_LN, ln_bytes, [&] {
       return l == 0 ? launch_ln1(c->emb, tok0, T, t0, c->x, c->xn, W.ln1_w, W.ln1_b, rows, D.d,
-                                 false, s)
+                                 D.dn, false, s)
                     : launch_ln1(nullptr, TokenSrc{nullptr, 0, 0, 0}, T, t0, c->x, c->xn,
-                                 W.ln1_w, W.ln1_b, rows, D.d, false, s);
+                                 W.ln1_w, W.ln1_b, rows, D.d, D.dn, false, s);
     });
     if (e) return e;
   }
@@ -488,7 +490,7 @@ hipError_t block_forward(boa_ctx* c, int l, int rows, int lanes, int T, const To
                   D.di, ACT_NONE)))
       return e;
     e = timed(c, BOA_K_LN, ln_bytes,
-              [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, false, s); });
+              [&] { return launch_ln2(c->xn, c->xn, W.ln2_w, W.ln2_b, rows, D.d, D.dn, false, s); });
     if (e) return e;
   }
   if ((e = gemm(c, c->xn, D.d, W.w1, D.ld_1, c->hid, 4 * D.d, W.b1, nullptr, 0, rows, 4 * D.d, D.d,
@@ -636,80 +638,6 @@ bool dec_fuse_xproj(const boa_ctx* c, int lanes) {
 // apart against 2.527 fused).
 bool dec_fuse_head(int lanes) { return lanes >= 2048; }
 
-// gaux words: the barrier counters of the 16 lane groups, 64 words (256
-// bytes) apart; the groups' decoded positions; their members' records of
-// the dispatch offset (16 per group); the abort flag
-constexpr int kGauxBar = 0, kGauxTGroup = 16 * 64, kGauxORec = kGauxTGroup + 64,
-              kGauxAbort = kGauxORec + 16 * 16, kGauxWords = kGauxAbort + 64;
-
-// fp32 d_model 256 up to 1024 lanes: every step in one launch of the
-// group-synchronous kernel, which runs the launch chain's fused kernels
-// (LayerNorm and x_proj fused, head.2 with the coder step) as its phases
-bool dec_use_group(const boa_ctx* c, int lanes) {
-  return c->group_step && !c->bf16 && c->d_gplan && dec_group_fits(c->D, lanes, c->n_cus) &&
-         dec_fuse_ln(c, lanes) && dec_fuse_xproj(c, lanes);
-}
-
-// model FLOPs of one decode step (the GEMMs: per layer in_proj, x_proj,
-// out_proj, FF1, FF2; then head.1 and head.2)
-double dec_step_flops(const boa_ctx* c, int lanes) {
-  const Dims& D = c->D;
-  const double layer = (double)D.d * 2 * D.di + (double)D.di * c->n_xdec + (double)D.di * D.d +
-                       2.0 * D.d * 4 * D.d;
-  return 2.0 * lanes * (D.L * layer + (double)D.d * D.d + (double)D.d * VOCAB);
-}
-
-// The group step's plan for lanes [0, lanes): the arguments step_range and
-// decode_steps give the chain's kernels (dgemm's for the plain GEMMs).
-void build_group_plan(boa_ctx* c, int lanes, uint8_t* out, int64_t chunk,
-                      const uint32_t* payload) {
-  const Dims& D = c->D;
-  const int ld = c->ld_dec;
-  GroupPlan& P = *c->h_gplan;
-  P = GroupPlan{};
-  const int n_cached = dec_cached_layers(c, lanes);
-  auto gemm = [&](const float* X, const float* W, float* C, const float* bias, const float* res,
-                  int N, int K, int act) {
-    DecGemmArgs a{};
-    a.Xt = X; a.ldx = ld; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ld;
-    a.bias = bias; a.res = res; a.ldr = ld; a.M = lanes; a.N = N; a.K = K; a.act = act;
-    return a;
-  };
-  for (int l = 0; l < D.L; ++l) {
-    const LayerW& W = c->layers[l];
-    const boa_ctx::DecW& DW = c->dlayers[l];
-    GroupLayerPlan& g = P.layer[l];
-    const bool cached = l < n_cached;
-    DecGemmArgs& a = g.in;  // LN1 + in_proj + conv
-    a.state_cached = cached ? 1 : 0;
-    a.Xt = c->dxt; a.ldx = ld; a.W = DW.w_in; a.ldw = 2 * D.di; a.C = c->dzt; a.ldc = ld;
-    a.bias = W.b_in; a.M = lanes; a.N = 2 * D.di; a.K = D.d; a.act = ACT_NONE;
-    a.conv_di = D.di; a.conv_state = dec_conv_of(c, l); a.ld_state = ld; a.conv_w = W.conv_w;
-    a.conv_b = W.conv_b; a.conv_out = c->dcvt;
-    g.out = gemm(c->dyt, DW.w_out, c->dot, W.b_out, nullptr, D.d, D.di, ACT_NONE);
-    DecGemmArgs& f = g.ff1;  // LN2 + FF1 + GELU
-    f.Xt = c->dot; f.ldx = ld; f.W = DW.w1; f.ldw = 4 * D.d; f.C = c->dhidt; f.ldc = ld;
-    f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU;
-    g.ff2 = gemm(c->dhidt, DW.w2, c->dxt, W.b2, c->dxt, D.d, 4 * D.d, ACT_NONE);
-    g.lw = W;
-    g.na = DW.na; g.wdt = DW.w_dt; g.w_x = DW.w_x; g.ssm = dec_ssm_of(c, l);
-    g.ldw_x = (int)round_up(c->n_xdec, 16); g.cached = cached ? 1 : 0;
-  }
-  P.head1 = gemm(c->dxt, c->dhw1, c->dot, c->hb1, nullptr, D.d, D.d, ACT_RELU);
-  DecGemmArgs& h = P.head2;
-  h.Xt = c->dot; h.ldx = ld; h.W = c->dhw2; h.ldw = VOCAB; h.M = lanes; h.N = VOCAB; h.K = D.d;
-  h.act = ACT_NONE; h.row_major = 1;
-  P.emb = c->emb; P.xt = c->dxt; P.zt = c->dzt; P.cvt = c->dcvt; P.yt = c->dyt;
-  P.head_b2 = c->hb2; P.tok = c->tok; P.lens = c->lens; P.out = out; P.out_stride = chunk;
-  P.states = c->dec; P.payload = payload; P.offsets = c->offsets; P.sizes = c->sizes;
-  P.bar = c->gaux + kGauxBar;
-  P.t_group = reinterpret_cast<int*>(c->gaux + kGauxTGroup);
-  P.o_rec = reinterpret_cast<int*>(c->gaux + kGauxORec);
-  P.t_counter = c->t_counter;
-  P.abort = reinterpret_cast<int*>(c->gaux + kGauxAbort);
-  P.inv_t = c->inv_temp; P.L = D.L; P.M = lanes; P.ld = ld; P.r = D.r;
-}
-
 // Grow-only device buffer: reallocated only when a call needs more.
 template <class T>
 hipError_t ensure_buf(T** p, int64_t* cap, int64_t need) {
@@ -785,7 +713,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     a.Xt = xnt; a.ldx = ld; a.W = DW.w_in; a.ldw = 2 * D.di; a.C = zt; a.ldc = ld;
     a.bias = W.b_in; a.M = lanes; a.N = 2 * D.di; a.K = D.d; a.act = ACT_NONE;
     a.conv_di = D.di; a.conv_state = conv; a.ld_state = ld; a.conv_w = W.conv_w;
-    a.conv_b = W.conv_b; a.conv_out = cvt;
+    a.conv_b = W.conv_b; a.conv_out = cvt; a.ln_n = D.dn;
     if (fuse_ln) {  // LN1 in front of in_proj, in one kernel
       a.Xt = xt;
       e = timed(c, BOA_K_DEC_LNGEMM, 2.0 * lanes * a.N * a.K, [&] {
@@ -795,7 +723,7 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     } else {
       e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
         return launch_dec_ln1(l == 0 ? c->emb : nullptr, tok, xt, xnt, W.ln1_w, W.ln1_b, lanes,
-                              D.d, ld, l == 0 ? t_counter : nullptr, s);
+                              D.d, D.dn, ld, l == 0 ? t_counter : nullptr, s);
       });
       if (!e)
         e = timed(c, BOA_K_DEC_GEMM, 2.0 * lanes * a.N * a.K, [&] { return dec_gemm(a, s); });
@@ -816,13 +744,13 @@ hipError_t step_range(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* t_co
     if (!e && fuse_ln) {  // LN2 in front of FF1, in one kernel
       DecGemmArgs f{};
       f.Xt = ot; f.ldx = ld; f.W = DW.w1; f.ldw = 4 * D.d; f.C = hidt; f.ldc = ld;
-      f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU;
+      f.bias = W.b1; f.M = lanes; f.N = 4 * D.d; f.K = D.d; f.act = ACT_GELU; f.ln_n = D.dn;
       e = timed(c, BOA_K_DEC_LNGEMM, 2.0 * lanes * f.N * f.K, [&] {
         return launch_dec_ln_gemm(2, f, nullptr, nullptr, nullptr, W.ln2_w, W.ln2_b, nullptr, s);
       });
     } else if (!e) {
       e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d,
-                [&] { return launch_dec_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
+                [&] { return launch_dec_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, D.dn, ld, s); });
       if (!e) e = dgemm(c, xnt, DW.w1, hidt, ld, W.b1, nullptr, lanes, 4 * D.d, D.d, ACT_GELU);
     }
     if (!e) e = dgemm(c, hidt, DW.w2, xt, ld, W.b2, xt, lanes, D.d, 4 * D.d, ACT_NONE);
@@ -869,7 +797,7 @@ hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* 
     const bool cached = l < n_cached;
     e = timed(c, BOA_K_LN, 3.0 * 4 * lanes * D.d, [&] {
       return launch_dec_b16_ln1(l == 0 ? c->emb : nullptr, tok, xt, xnt, W.ln1_w, W.ln1_b, lanes,
-                                D.d, ld, l == 0 ? t_counter : nullptr, s);
+                                D.d, D.dn, ld, l == 0 ? t_counter : nullptr, s);
     });
     if (!e) {
       DecB16Args a = g(xnt, B.w_in, 2 * D.di, D.d, zt, DEC_OUT_B16, W.b_in, ACT_NONE);
@@ -886,7 +814,7 @@ hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* 
     if (!e) e = run(g(yt, B.w_out, D.d, D.di, ot, DEC_OUT_B16, W.b_out, ACT_NONE));
     if (!e)
       e = timed(c, BOA_K_LN, 2.0 * 2 * lanes * D.d,
-                [&] { return launch_dec_b16_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, ld, s); });
+                [&] { return launch_dec_b16_ln2(ot, xnt, W.ln2_w, W.ln2_b, lanes, D.d, D.dn, ld, s); });
     if (!e) e = run(g(xnt, B.w1, 4 * D.d, D.d, hidt, DEC_OUT_B16, W.b1, ACT_GELU));
     if (!e) {
       DecB16Args a = g(hidt, B.w2, D.d, 4 * D.d, xt, DEC_OUT_F32, W.b2, ACT_NONE);
@@ -909,19 +837,6 @@ hipError_t step_forward(boa_ctx* c, const uint8_t* tok, int lanes, bool add_bias
   hipError_t e = ensure_state_layout(c, 1);
   if (e) return e;
   return step_range(c, 0, lanes, c->stream, c->t_counter, tok, add_bias, logits);
-}
-
-// After a batch decoded with the group step: a barrier that timed out, or a
-// workgroup outside its group's XCD, leaves the abort flag set and the
-// batch's symbols undefined.  The counters are reset for later calls.
-int check_group_abort(boa_ctx* c) {
-  int ab = 0;
-  if (hipMemcpy(&ab, c->gaux + kGauxAbort, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
-    return fail(c, BOA_E_HIP, "decode step: reading the group step's status failed");
-  if (!ab) return BOA_OK;
-  (void)hipMemset(c->gaux, 0, kGauxWords * sizeof(unsigned));
-  return fail(c, BOA_E_HIP, ab == 2 ? "decode step: workgroups were not dispatched round-robin over the XCDs"
-                                    : "decode step: a lane-group barrier timed out");
 }
 
 int check_ready(boa_ctx* c) {
@@ -1009,6 +924,7 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
                                 dec_ssm_of(c, l)};
     }
     p.L = D.L; p.r = D.r; p.lanes = lanes; p.maxlen = maxlen; p.ld_state = c->ld_dec;
+    p.ln_n = D.dn;
     p.emb = c->emb; p.hw1 = c->dhw1; p.hb1 = c->hb1; p.hw2 = c->dhw2; p.hb2 = c->hb2;
     p.inv_t = c->inv_temp; p.tok = c->tok; p.lens = c->lens; p.t_counter = c->t_counter;
     p.out = out; p.out_stride = chunk; p.states = c->dec; p.payload = d_payload;
@@ -1020,21 +936,7 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
   // (dec_head_step_kernel), so the logits stay on chip; below that, and in
   // bf16, head.2 and the coder step are separate launches
   const bool fuse_head = !c->bf16 && dec_fuse_head(lanes);
-  // fp32 d_model 256 up to 1024 lanes: one launch per step (its plan goes to
-  // the device after the previous batch's steps, and the groups' decoded
-  // positions restart at 0)
-  const bool group = dec_use_group(c, lanes);
-  if (group) {
-    build_group_plan(c, lanes, out, chunk, d_payload);
-    hipError_t e = hipMemcpyAsync(c->d_gplan, c->h_gplan, sizeof(GroupPlan),
-                                  hipMemcpyHostToDevice, s);
-    if (!e) e = launch_fill_zero(c->gaux + kGauxTGroup, 64 * sizeof(unsigned), s);
-    if (e) return e;
-  }
   auto one_step = [&](hipStream_t gs) -> hipError_t {
-    if (group)
-      return timed(c, BOA_K_DEC_STEP, dec_step_flops(c, lanes),
-                   [&] { return launch_dec_group_step(c->d_gplan, lanes, gs); });
     hipError_t e =
         step_range(c, 0, lanes, gs, c->t_counter, c->tok, false, c->dlogits, !fuse_head);
     if (e) return e;
@@ -1083,12 +985,11 @@ hipError_t decode_steps(boa_ctx* c, int lanes, int maxlen, uint8_t* out, int64_t
   // these or a buffer of the context)
   boa_ctx::GraphKey key;
   key.lanes = lanes; key.out = out; key.stride = chunk; key.payload = d_payload;
-  key.inv_temp = c->inv_temp; key.stream = c->dec_stream; key.group = group;
+  key.inv_temp = c->inv_temp; key.stream = c->dec_stream;
   const boa_ctx::GraphKey& k0 = c->dec_key;
   const bool same = c->dec_exec && k0.lanes == key.lanes && k0.out == key.out &&
                     k0.stride == key.stride && k0.payload == key.payload &&
-                    k0.inv_temp == key.inv_temp && k0.stream == key.stream &&
-                    k0.group == key.group;
+                    k0.inv_temp == key.inv_temp && k0.stream == key.stream;
   if (!same) {
     if (c->dec_exec) {
       e = hipStreamSynchronize(c->dec_stream);  // its last replay has finished
@@ -1142,13 +1043,12 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
   if (!cfg || !out) return BOA_E_ARG;
   *out = nullptr;
   const int d = cfg->d_model;
-  // d_model: the shapes the kernels are built for (80: the reference's
-  // ..._mambav1_80_1_20.pt checkpoint); bf16 needs K in multiples of 64
-  const bool d_ok = d == 64 || d == 80 || d == 128 || d == 256 || d == 512;
-  if (!d_ok || cfg->n_layers < 1 || (cfg->d_state != 16 && cfg->d_state != 32) ||
+  // any d_model up to 512 (dt_rank = ceil(d / 16) <= 32): the kernels are
+  // built for widths 64, 80 (the reference's ..._mambav1_80_1_20.pt), 128,
+  // 256 and 512, and other widths run at the next one up (make_dims)
+  if (d < 1 || d > 512 || cfg->n_layers < 1 || (cfg->d_state != 16 && cfg->d_state != 32) ||
       cfg->max_lanes < 1 || cfg->max_lanes > 65535 ||
-      (cfg->precision != 0 && cfg->precision != 1) || (cfg->precision == 1 && d % 64) ||
-      cfg->tile < 0)
+      (cfg->precision != 0 && cfg->precision != 1) || cfg->tile < 0)
     return BOA_E_ARG;
   boa_ctx* c = new boa_ctx();
   {
@@ -1201,12 +1101,6 @@ int boa_create(const boa_config* cfg, boa_ctx** out) {
         hipDeviceGetAttribute(&c->n_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       c->n_cus = 0;
   }
-  c->h_gplan = new (std::nothrow) GroupPlan{};
-  if (!c->h_gplan || dalloc(&c->d_gplan, 1) || dalloc(&c->gaux, kGauxWords) ||
-      hipMemset(c->gaux, 0, kGauxWords * sizeof(unsigned)) != hipSuccess) {
-    boa_destroy(c);
-    return BOA_E_NOMEM;
-  }
   *out = c;
   return BOA_OK;
 }
@@ -1226,8 +1120,6 @@ void boa_destroy(boa_ctx* c) {
   dfree(c->hid); dfree(c->logits); dfree(c->lowprob); dfree(c->lowprob_alt);
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
   dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
-  dfree(c->d_gplan); dfree(c->gaux);
-  delete c->h_gplan;
   if (c->h_sizes) (void)hipHostFree(c->h_sizes);
   drop_dec_graph(c);
   dfree(c->first_buf); dfree(c->reorder_words); dfree(c->reorder_off); dfree(c->reorder_sz);
@@ -1284,20 +1176,11 @@ int boa_decode_plan(const boa_ctx* c, int32_t lanes, int32_t* cached_layers, int
   const bool pers = !c->bf16 && dec_persist_fits(D.d, D.ds, D.r, D.L);
   const bool chain32 = !pers && !c->bf16;
   if (cached_layers) *cached_layers = pers ? D.L : dec_cached_layers(c, lanes);
-  const bool group = chain32 && dec_use_group(c, lanes);
   if (flags)
     *flags = (chain32 && dec_fuse_ln(c, lanes) ? BOA_PLAN_FUSED_LN : 0) |
              (pers ? BOA_PLAN_PERSISTENT : 0) |
              (chain32 && dec_fuse_xproj(c, lanes) ? BOA_PLAN_FUSED_XPROJ : 0) |
-             ((chain32 && dec_fuse_head(lanes)) || group ? BOA_PLAN_FUSED_HEAD : 0) |
-             (group ? BOA_PLAN_GROUP_STEP : 0);
-  return BOA_OK;
-}
-
-int boa_set_decode_group(boa_ctx* c, int32_t enable) {
-  if (!c) return BOA_E_ARG;
-  drop_dec_graph(c);
-  c->group_step = enable ? 1 : 0;
+             (chain32 && dec_fuse_head(lanes) ? BOA_PLAN_FUSED_HEAD : 0);
   return BOA_OK;
 }
 
@@ -1316,16 +1199,20 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
   // anything else is a headerless fp32 file.
   const bool hdr = n >= 4 && p[0] == 'B' && p[1] == 'O' && p[2] == 'A';
   if (hdr) { rd.fp16 = p[3] == 0x01; rd.pos = 4; }
-  const int64_t expect = boa_weight_file_bytes(D.d, D.L, D.ds, rd.fp16) - (hdr ? 0 : 4);
+  const int64_t expect = boa_weight_file_bytes(D.dn, D.L, D.ds, rd.fp16) - (hdr ? 0 : 4);
   if ((int64_t)n != expect) {
     char msg[256];
     snprintf(msg, sizeof msg,
              "weight file has %zu bytes, expected %lld for d_model=%d n_layers=%d d_state=%d", n,
-             (long long)expect, D.d, D.L, D.ds);
+             (long long)expect, D.dn, D.L, D.ds);
     return fail(c, BOA_E_FORMAT, msg);
   }
   // device layout: Linear weights transposed to [in][ld] with ld a multiple
-  // of 256 (zero padded) so every GEMM tile load stays in bounds.
+  // of 256 (zero padded) so every GEMM tile load stays in bounds.  A model
+  // of d_model dn below the kernel width d (Dims) is placed into the width-d
+  // layout: its features sit at 0 .. dn-1 (inner channels at 0 .. 2 dn-1 of
+  // each half of in_proj's output), every other weight and bias is zero.
+  const int dn = D.dn, din = 2 * D.dn;
   std::vector<std::pair<size_t, std::vector<float>>> parts;  // (offset floats, data)
   size_t total = 0;
   auto place = [&](std::vector<float>&& v) -> size_t {
@@ -1334,61 +1221,81 @@ int boa_load_weights_mem(boa_ctx* c, const void* data, size_t n) {
     parts.emplace_back(off, std::move(v));
     return off;
   };
-  auto linear_t = [&](int rows, int cols, int ld) -> size_t {
+  auto same = [](int i) { return i; };
+  auto xz_row = [&](int i) { return i < din ? i : i - din + D.di; };  // in_proj's two halves
+  // a [rows][cols] Linear weight of the file -> [cols_pad][ld], output feature
+  // i at column row_at(i)
+  auto linear_t = [&](int rows, int cols, int cols_pad, int ld, auto row_at) -> size_t {
     std::vector<float> w;
     rd.vec(w, (size_t)rows * cols);
-    std::vector<float> t((size_t)cols * ld, 0.0f);
+    std::vector<float> t((size_t)cols_pad * ld, 0.0f);
     if (!rd.bad)
       for (int i = 0; i < rows; ++i)
-        for (int j = 0; j < cols; ++j) t[(size_t)j * ld + i] = w[(size_t)i * cols + j];
+        for (int j = 0; j < cols; ++j) t[(size_t)j * ld + row_at(i)] = w[(size_t)i * cols + j];
     return place(std::move(t));
   };
-  auto raw = [&](size_t count) -> size_t {
+  // `count` groups of `width` floats of the file -> groups at at(i) of
+  // `count_pad` groups
+  auto raw_at = [&](int count, int count_pad, int width, auto at) -> size_t {
     std::vector<float> v;
-    rd.vec(v, count);
-    return place(std::move(v));
+    rd.vec(v, (size_t)count * width);
+    std::vector<float> t((size_t)count_pad * width, 0.0f);
+    if (!rd.bad)
+      for (int i = 0; i < count; ++i)
+        memcpy(t.data() + (size_t)at(i) * width, v.data() + (size_t)i * width, 4 * (size_t)width);
+    return place(std::move(t));
   };
+  auto raw = [&](int count, int count_pad) -> size_t { return raw_at(count, count_pad, 1, same); };
   struct LayerOff {
     size_t ln1_w, ln1_b, w_in, b_in, conv_w, conv_b, w_x, w_dt, b_dt, a_log, na2, dd, w_out, b_out,
         ln2_w, ln2_b, w1, b1, w2, b2;
   };
   std::vector<LayerOff> lo(D.L);
-  const size_t emb = raw((size_t)VOCAB * D.d);
+  size_t emb;
+  {  // embedding [256][dn] -> [256][d]
+    std::vector<float> v;
+    rd.vec(v, (size_t)VOCAB * dn);
+    std::vector<float> t((size_t)VOCAB * D.d, 0.0f);
+    if (!rd.bad)
+      for (int i = 0; i < VOCAB; ++i)
+        memcpy(t.data() + (size_t)i * D.d, v.data() + (size_t)i * dn, 4 * (size_t)dn);
+    emb = place(std::move(t));
+  }
   for (int l = 0; l < D.L; ++l) {
     LayerOff& o = lo[l];
-    o.ln1_w = raw(D.d);
-    o.ln1_b = raw(D.d);
-    o.w_in = linear_t(2 * D.di, D.d, D.ld_in);
-    o.b_in = raw(2 * D.di);
-    o.conv_w = raw((size_t)D.di * 4);
-    o.conv_b = raw(D.di);
-    o.w_x = linear_t(D.R, D.di, D.ld_x);
+    o.ln1_w = raw(dn, D.d);
+    o.ln1_b = raw(dn, D.d);
+    o.w_in = linear_t(2 * din, dn, D.d, D.ld_in, xz_row);
+    o.b_in = raw_at(2 * din, 2 * D.di, 1, xz_row);
+    o.conv_w = raw_at(din, D.di, 4, same);
+    o.conv_b = raw(din, D.di);
+    o.w_x = linear_t(D.R, din, D.di, D.ld_x, same);
     {  // dt_proj [di][r] stored as [r][di] (no padding: read per channel)
       std::vector<float> w;
-      rd.vec(w, (size_t)D.di * D.r);
+      rd.vec(w, (size_t)din * D.r);
       std::vector<float> t((size_t)D.r * D.di, 0.0f);
       if (!rd.bad)
-        for (int i = 0; i < D.di; ++i)
+        for (int i = 0; i < din; ++i)
           for (int j = 0; j < D.r; ++j) t[(size_t)j * D.di + i] = w[(size_t)i * D.r + j];
       o.w_dt = place(std::move(t));
     }
-    o.b_dt = raw(D.di);
-    o.a_log = raw((size_t)D.di * D.ds);
+    o.b_dt = raw(din, D.di);
+    o.a_log = raw_at(din, D.di, D.ds, same);
     o.na2 = place(std::vector<float>((size_t)D.di * D.ds, 0.0f));
-    o.dd = raw(D.di);
-    o.w_out = linear_t(D.d, D.di, D.ld_out);
-    o.b_out = raw(D.d);
-    o.ln2_w = raw(D.d);
-    o.ln2_b = raw(D.d);
-    o.w1 = linear_t(4 * D.d, D.d, D.ld_1);
-    o.b1 = raw(4 * D.d);
-    o.w2 = linear_t(D.d, 4 * D.d, D.ld_2);
-    o.b2 = raw(D.d);
+    o.dd = raw(din, D.di);
+    o.w_out = linear_t(dn, din, D.di, D.ld_out, same);
+    o.b_out = raw(dn, D.d);
+    o.ln2_w = raw(dn, D.d);
+    o.ln2_b = raw(dn, D.d);
+    o.w1 = linear_t(4 * dn, dn, D.d, D.ld_1, same);
+    o.b1 = raw(4 * dn, 4 * D.d);
+    o.w2 = linear_t(dn, 4 * dn, 4 * D.d, D.ld_2, same);
+    o.b2 = raw(dn, D.d);
   }
-  const size_t hw1 = linear_t(D.d, D.d, D.ld_h1);
-  const size_t hb1 = raw(D.d);
-  const size_t hw2 = linear_t(VOCAB, D.d, D.ld_h2);
-  const size_t hb2 = raw(VOCAB);
+  const size_t hw1 = linear_t(dn, dn, D.d, D.ld_h1, same);
+  const size_t hb1 = raw(dn, D.d);
+  const size_t hw2 = linear_t(VOCAB, dn, D.d, D.ld_h2, same);
+  const size_t hb2 = raw(VOCAB, VOCAB);
   if (rd.bad || rd.pos != n) return fail(c, BOA_E_FORMAT, "weight file truncated");
 
   drop_dec_graph(c);
@@ -1720,6 +1627,13 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
   // warm-start: where each chunk's stream landed in the iteration-ordered payload
   std::vector<uint64_t> stage_off(warm ? (size_t)nc : 0);
   int64_t out_words = 0;
+  // an error after coder launches were queued: let the coder stream drain
+  // (its kernels read the caller's input and write the context's words)
+  // before the caller can free or reuse those buffers
+  auto fail_coding = [&](hipError_t err, const char* where) {
+    (void)hipStreamSynchronize(c->enc_stream);
+    return hip_fail(c, err, where);
+  };
   for (int64_t u0 = 0; u0 < units; u0 += B) {
     const int G = (int)std::min<int64_t>(B, units - u0);
     for (int64_t i = 0; i < S; ++i) {
@@ -1738,7 +1652,7 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
         const int Tt = (int)std::min<int64_t>(T, chunk - t0);
         // the coder of tile k - 2 has finished reading this tile's buffer
         if (k >= 2) e = hipStreamWaitEvent(s, c->lp_free[k & 1], 0);
-        if (e) return hip_fail(c, e, "compress tile");
+        if (e) return fail_coding(e, "compress tile");
         if (c->bf16) {  // bf16: head.2 stores the logits, the CDF kernel reads them
           e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
           if (!e)
@@ -1761,14 +1675,14 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
         if (!e && c->progress)
           e = progress_mark(c, 0, std::min(processed, done + (int64_t)lanes * (t0 + Tt)), processed,
                             &pend, &slot);
-        if (e) return hip_fail(c, e, "compress tile");
+        if (e) return fail_coding(e, "compress tile");
       }
       e = hipEventRecord(c->enc_done, c->enc_stream);  // the batch's last tile is coded
       if (!e) e = hipStreamWaitEvent(s, c->enc_done, 0);
       if (!e) e = launch_rc_finish(c->enc, c->words, pitch, c->sizes, lanes, s);
       if (!e) e = hipMemcpyAsync(c->h_sizes, c->sizes, sizeof(int32_t) * lanes, hipMemcpyDeviceToHost, s);
       if (!e) e = hipStreamSynchronize(s);
-      if (e) return hip_fail(c, e, "finish");
+      if (e) return fail_coding(e, "finish");
       int64_t batch_words = 0;
       for (int b = 0; b < lanes; ++b) batch_words += c->h_sizes[b];
       if (out_words + batch_words > payload_cap_words)
@@ -1894,7 +1808,6 @@ int boa_decompress_device(boa_ctx* c, const uint32_t* d_payload, const uint64_t*
       }
       e = hipStreamSynchronize(s);
       if (e) return hip_fail(c, e, "decode sync");
-      if (dec_use_group(c, lanes) && (rc = check_group_abort(c))) return rc;
       for (int b = 0; b < lanes; ++b) c->prog_base += lens[b];
       if (c->progress) c->progress(c->progress_user, 1, c->prog_base, c->prog_total);
     }

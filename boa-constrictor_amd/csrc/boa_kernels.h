@@ -82,6 +82,7 @@ struct LnEpi {
   float* out;
   int ldo;
   int mode;  // 1 = LN1, 2 = LN2
+  int n;     // the LayerNorm's width (real features of the 256)
 };
 hipError_t gemm_f32_ln(const GemmArgs& a, const LnEpi& ln, hipStream_t s);
 // Tile configuration gemm_f32 picks: 0 = 128x256 (bulk GEMMs of a compress
@@ -118,9 +119,15 @@ struct LayerW {
       *w_out, *b_out, *ln2_w, *ln2_b, *w1, *b1, *w2, *b2;
 };
 
-// Model dimensions and padded weight strides.
+// Model dimensions and padded weight strides.  A model of d_model dn runs at
+// width d >= dn, the next width the kernels are built for: features dn .. d-1
+// (and inner channels 2 dn .. 2 d-1 of each half of in_proj's output) hold
+// zero weights, so their activations are zero, every GEMM's K-ordered chain
+// ends in exact zero terms, and the LayerNorms divide by dn.  dt_rank r is
+// dn's: ceil(dn / 16).
 struct Dims {
   int d, L, di, r, ds, R;
+  int dn;  // the model's own d_model (LayerNorm width); d = dn for the built widths
   int ld_in, ld_x, ld_out, ld_1, ld_2, ld_h1, ld_h2;
 };
 
@@ -156,6 +163,7 @@ struct FfnB16Args {
   float* C;
   uint16_t* C2;
   int M, D;
+  int n = 0;  // the LayerNorms' width (real features of the D; 0 = D)
   const float* ln2_w = nullptr;
   const float* ln2_b = nullptr;
   const float* ln1_w = nullptr;
@@ -168,11 +176,13 @@ hipError_t launch_b16_weight_nk(const float* w, int ldw_in, int N, int K, int n_
 
 // Activations other than the residual stream x are fp32, or bf16 (uint16_t)
 // when `bf16` is set; x and the recurrent state are always fp32.
+// Rows are d wide; the LayerNorms take the statistics of the first n.
 hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, void* xn,
-                      const float* w, const float* b, int rows, int d, bool bf16, hipStream_t s);
+                      const float* w, const float* b, int rows, int d, int n, bool bf16,
+                      hipStream_t s);
 // LayerNorm with sequential per-row sums (LN2 order), in place allowed.
 hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, int rows, int d,
-                      bool bf16, hipStream_t s);
+                      int n, bool bf16, hipStream_t s);
 hipError_t launch_conv_chunk(const void* xz, float* conv_state, const float* w, const float* cb,
                              void* out, int lanes, int T, int di, bool bf16, hipStream_t s);
 hipError_t launch_scan_chunk(const Dims& D, const LayerW& Lw, const void* xz, const void* conv,
@@ -197,6 +207,7 @@ struct DecGemmArgs {
   float* conv_state; int ld_state;
   const float* conv_w; const float* conv_b; float* conv_out;
   int state_cached;  // conv state through the caches (1) or streamed (0)
+  int ln_n;          // launch_dec_ln_gemm: the LayerNorm's width (real features of K)
 };
 hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s);
 // LayerNorm (mode 1: LN1, mode 2: LN2; weights lw, lb) of the K = d features
@@ -216,10 +227,10 @@ hipError_t launch_dec_scan_params(const float* w_dt, const float* na, float* wdt
 // dt_rank slots of the decode scan's row (features [0, dec_rb) hold dt_in)
 inline int dec_rb(int r) { return r <= 8 ? 8 : (r <= 16 ? 16 : 32); }
 hipError_t launch_dec_ln1(const float* emb, const uint8_t* tok, float* xt, float* xnt,
-                          const float* w, const float* b, int M, int d, int ld, int* t_counter,
-                          hipStream_t s);
+                          const float* w, const float* b, int M, int d, int n, int ld,
+                          int* t_counter, hipStream_t s);
 hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const float* b, int M, int d,
-                          int ld, hipStream_t s);
+                          int n, int ld, hipStream_t s);
 // x_proj fused with the decode scan (dec_xscan_kernel); same results as
 // dec_gemm (x_proj) + launch_dec_scan
 bool dec_xscan_fits(const Dims& D);
@@ -244,6 +255,7 @@ struct PersistLayer {
 struct PersistArgs {
   PersistLayer layer[PERSIST_MAX_LAYERS];
   int L, r, lanes, maxlen, ld_state;
+  int ln_n;  // the LayerNorms' width (real features of the 64)
   const float *emb, *hw1, *hb1, *hw2, *hb2;
   float inv_t;
   uint8_t* tok;
@@ -260,52 +272,6 @@ bool dec_persist_fits(int d, int ds, int r, int L);
 // lanes per block: the fewest (4, 8, 16) whose grid fits n_cus workgroups
 int dec_persist_lanes_per_block(int lanes, int n_cus);
 hipError_t launch_dec_persist(const PersistArgs& a, int d, int ds, int n_cus, hipStream_t s);
-
-// ---- group-synchronous decode step (decode.hip) ------------------------
-// One launch runs a whole step (every layer, the head, the CDF, the search
-// and the coder advance) for d_model 256, d_state 16, fp32, at most 1024
-// lanes.  Its grid is the launch chain's: xcd_grid(lanes, 16) workgroups of
-// 1024 threads, one per CU; a workgroup joins the 64-lane group of the XCD
-// it runs on.  The phases are the chain's kernels, in the chain's order and
-// with its bits; between phases the group's 16 workgroups meet at a barrier
-// of their own (a counter in device memory).  Every wait is bounded: a
-// timeout, or a dispatch that is not round-robin over the XCDs, sets *abort
-// and ends the launch, and the host reports an error.
-constexpr int GROUP_MAX_LAYERS = 16;
-struct GroupLayerPlan {
-  DecGemmArgs in, out, ff1, ff2;  // LN1 + in_proj + conv, out_proj, LN2 + FF1, FF2
-  LayerW lw;                       // LayerNorm weights, dt bias, D
-  const float *na, *wdt, *w_x;     // scan parameters (quad layout), x_proj (k-blocked)
-  float* ssm;                      // step-layout SSM state
-  int ldw_x, cached;
-};
-struct GroupPlan {
-  GroupLayerPlan layer[GROUP_MAX_LAYERS];
-  DecGemmArgs head1, head2;  // head.2: row-major, no bias (added with the CDF)
-  const float* emb;
-  float* xt;                 // residual stream (layer 0 stores the embedding rows)
-  const float *zt, *cvt;     // in_proj's z half and conv output
-  float* yt;                 // scan output
-  const float* head_b2;
-  uint8_t* tok;
-  const int32_t* lens;
-  uint8_t* out;
-  int64_t out_stride;
-  RcDec* states;
-  const uint32_t* payload;
-  const uint64_t* offsets;
-  const int32_t* sizes;
-  unsigned* bar;   // per 64-lane group: one barrier counter, 256 bytes apart
-  int* t_group;    // per 64-lane group: the last decoded position
-  int* o_rec;      // per 64-lane group: 16 words, each member's dispatch offset
-  int* t_counter;  // the launch chain's step counter, kept in step
-  int* abort;
-  float inv_t;
-  int L, M, ld, r;
-};
-constexpr int GROUP_MAX_LANES = 1024;
-bool dec_group_fits(const Dims& D, int lanes, int n_cus);
-hipError_t launch_dec_group_step(const GroupPlan* d_plan, int lanes, hipStream_t s);
 
 // ---- decode step, bf16 precision (decode_bf16.hip) ----------------------
 // Activations bf16 in the 32-blocked layout (feature k of lane m at
@@ -328,10 +294,10 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s);
 hipError_t launch_dec_b16_weight(const float* w, int ldw_in, int n_src, uint16_t* out, int K,
                                  int ldn, int zs, int ze, hipStream_t s);
 hipError_t launch_dec_b16_ln1(const float* emb, const uint8_t* tok, float* xt, uint16_t* xnt,
-                              const float* w, const float* b, int M, int d, int ld, int* t_counter,
-                              hipStream_t s);
+                              const float* w, const float* b, int M, int d, int n, int ld,
+                              int* t_counter, hipStream_t s);
 hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w, const float* b,
-                              int M, int d, int ld, hipStream_t s);
+                              int M, int d, int n, int ld, hipStream_t s);
 hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
                                const float* wdt_q, const uint16_t* zt, const uint16_t* cvt,
                                const uint16_t* rows, float* ssm, uint16_t* yt, int M, int ld,

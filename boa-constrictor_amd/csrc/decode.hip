@@ -27,37 +27,6 @@ namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-// ------------------------------------------ activation loads (COH = true)
-// In the group-synchronous step (dec_group_step_kernel) the 16 workgroups
-// of a 64-lane group run on one XCD and pass activations to each other
-// inside one launch: a producer's plain stores have reached the XCD's L2
-// when it arrives at the group barrier, and the consumers read them with
-// device-scope (sc1) buffer loads, which miss the CU's L1 (it may still
-// hold lines of an earlier phase) and are served by that shared L2.
-// Weights and the state a workgroup owns are read with ordinary loads.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t act_rsrc(const float* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
-}
-template <bool COH>
-__device__ __forceinline__ float4 act_ld4(const float* base, size_t i4) {
-  if constexpr (COH) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(act_rsrc(base), (int)(i4 * 16), 0, 16);
-    return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
-                       __uint_as_float(v[3]));
-  } else {
-    return reinterpret_cast<const float4*>(base)[i4];
-  }
-}
-template <bool COH>
-__device__ __forceinline__ float act_ld(const float* base, size_t i) {
-  if constexpr (COH) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(act_rsrc(base), (int)(i * 4), 0, 16));
-  } else {
-    return base[i];
-  }
-}
-
-
 // ------------------------------------------------------------------- GEMM
 // A wave computes TN x TM MFMA tiles of 16 output features x 16 lanes.  Lane
 // (i = lane & 15, g = lane >> 4) loads, per 16-k block q, the float4s at
@@ -81,7 +50,7 @@ struct EpiPre {
   float cb[CONV ? 4 : 1];
 };
 
-template <bool CONV = false, bool COH = false>
+template <bool CONV = false>
 __device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, int m, int g,
                                                  EpiPre<CONV>& p) {
   if (m >= a.M || n0 >= a.N) return;
@@ -91,7 +60,7 @@ __device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, i
     p.b[e] = a.bias ? a.bias[min(nf, a.N - 1)] : 0.0f;
   }
   if (a.res && !a.row_major && !(a.conv_di > 0))
-    p.r = act_ld4<COH>(a.res, ((size_t)(n0 >> 4) * a.ldr + m) * 4 + g);
+    p.r = reinterpret_cast<const float4*>(a.res)[((size_t)(n0 >> 4) * a.ldr + m) * 4 + g];
   if (CONV && a.conv_di > 0 && n0 < a.conv_di) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -187,7 +156,7 @@ __device__ __forceinline__ void dec_epilogue(const DecGemmArgs& a, const floatx4
 // The K loop of one wave: loads run PD groups of UQ 16-k blocks ahead of the
 // MFMAs through a ring of PD + 1 register groups (fully unrolled, so every
 // ring index is a compile-time register).
-template <int KS, int TM, int TN, int UQ, int PD, bool COH = false>
+template <int KS, int TM, int TN, int UQ, int PD>
 __device__ __forceinline__ void dec_mainloop(const DecGemmArgs& a, int n0, int m0, int i, int g,
                                              floatx4 (&acc)[TM][TN]) {
   constexpr int QB = KS / 4;  // 16-k blocks in K
@@ -196,17 +165,12 @@ __device__ __forceinline__ void dec_mainloop(const DecGemmArgs& a, int n0, int m
   static_assert(QB % UQ == 0, "K must be a multiple of 16 UQ");
   const float4* wp[TN];
   const float4* xp[TM];
-  size_t xo[TM];  // with COH: the operands as float4 offsets from a.Xt
 #pragma unroll
   for (int t = 0; t < TN; ++t)
     wp[t] = reinterpret_cast<const float4*>(a.W) + (size_t)min(n0 + 16 * t + i, a.ldw - 1) * 4 + g;
 #pragma unroll
-  for (int t = 0; t < TM; ++t) {
-    if constexpr (COH)
-      xo[t] = (size_t)min(m0 + 16 * t + i, a.M - 1) * 4 + g;
-    else
-      xp[t] = reinterpret_cast<const float4*>(a.Xt) + (size_t)min(m0 + 16 * t + i, a.M - 1) * 4 + g;
-  }
+  for (int t = 0; t < TM; ++t)
+    xp[t] = reinterpret_cast<const float4*>(a.Xt) + (size_t)min(m0 + 16 * t + i, a.M - 1) * 4 + g;
   const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // float4s per 16-k block
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm)
@@ -216,10 +180,7 @@ __device__ __forceinline__ void dec_mainloop(const DecGemmArgs& a, int n0, int m
 #define BOA_DEC_LOAD(BUF, Q0)                                                     \
   _Pragma("unroll") for (int q = 0; q < UQ; ++q) {                                \
     _Pragma("unroll") for (int t = 0; t < TN; ++t) af[BUF][q][t] = wp[t][(size_t)((Q0) + q) * wq]; \
-    _Pragma("unroll") for (int t = 0; t < TM; ++t) {                              \
-      if constexpr (COH) bf[BUF][q][t] = act_ld4<true>(a.Xt, xo[t] + (size_t)((Q0) + q) * xq); \
-      else bf[BUF][q][t] = xp[t][(size_t)((Q0) + q) * xq];                        \
-    }                                                                             \
+    _Pragma("unroll") for (int t = 0; t < TM; ++t) bf[BUF][q][t] = xp[t][(size_t)((Q0) + q) * xq]; \
   }                                                                               \
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -247,7 +208,7 @@ __device__ __forceinline__ void dec_mainloop(const DecGemmArgs& a, int n0, int m
 // One 16 x 16 tile per wave: wave w (0-3) of virtual block vb takes 16-lane
 // tile w of the 64-lane group and n tile j of xcd_slot(vb, n_tiles).  Its
 // bias and residual load ahead of the K loop.  No barriers.
-template <int KS, int UQ, int PD, bool COH>
+template <int KS, int UQ, int PD>
 __device__ __forceinline__ void dec_gemm_wave(const DecGemmArgs& a, int vb, int tid) {
   const int lane = tid & 63, w = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
@@ -255,9 +216,9 @@ __device__ __forceinline__ void dec_gemm_wave(const DecGemmArgs& a, int vb, int 
   const int m0 = q.grp * 64 + 16 * w, n0 = q.j * 16;
   if (m0 >= a.M) return;
   EpiPre<> pre;
-  dec_epi_prefetch<false, COH>(a, n0, m0 + i, g, pre);
+  dec_epi_prefetch<false>(a, n0, m0 + i, g, pre);
   floatx4 acc[1][1];
-  dec_mainloop<KS, 1, 1, UQ, PD, COH>(a, n0, m0, i, g, acc);
+  dec_mainloop<KS, 1, 1, UQ, PD>(a, n0, m0, i, g, acc);
   dec_epilogue(a, acc[0][0], n0, m0 + i, g, pre);
 }
 
@@ -270,7 +231,7 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
   if (TM == 1 && TN == 1) {
     // one tile per wave; a block's 4 waves take the 4 16-lane tiles of one
     // 64-lane group (xcd_slot) and one n tile
-    dec_gemm_wave<KS, UQ, PD, false>(a, blockIdx.x, threadIdx.x);
+    dec_gemm_wave<KS, UQ, PD>(a, blockIdx.x, threadIdx.x);
     return;
   }
   const int m_tiles = (a.M + 16 * TM - 1) / (16 * TM);
@@ -349,7 +310,7 @@ hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
 // LDS of the fused head step: 16 logits rows of HS_LS floats, then the 16
 // CDFs (doubles) and coder targets
 constexpr int HS_LS = 256 + 4;
-template <int KS, bool COH>
+template <int KS>
 __device__ __forceinline__ void dec_head_step_body(
     const DecGemmArgs& a, const float* __restrict__ head_b2, float inv_t, uint8_t* tok,
     const int32_t* __restrict__ lens, int t, uint8_t* out, int64_t out_stride, RcDec* states,
@@ -361,7 +322,7 @@ __device__ __forceinline__ void dec_head_step_body(
   const int wv = tid >> 6, lane = tid & 63, i = lane & 15, g = lane >> 4;
   {
     floatx4 acc[1][1];
-    dec_mainloop<KS, 1, 1, 1, 8, COH>(a, 16 * wv, m0, i, g, acc);
+    dec_mainloop<KS, 1, 1, 1, 8>(a, 16 * wv, m0, i, g, acc);
 #pragma unroll
     for (int v = 0; v < 4; ++v) lg[i * LS + 16 * wv + 4 * g + v] = acc[0][0][v] + 0.0f;
   }
@@ -405,7 +366,7 @@ __global__ __launch_bounds__(1024) void dec_head_step_kernel(
   __shared__ double s_cdf[16][260];
   __shared__ uint32_t s_target[16];
   const XcdSlot blk = xcd_slot(blockIdx.x, 4);  // 4 16-lane tiles per 64-lane group
-  dec_head_step_body<KS, false>(a, head_b2, inv_t, tok, lens, *t_counter, out, out_stride, states,
+  dec_head_step_body<KS>(a, head_b2, inv_t, tok, lens, *t_counter, out, out_stride, states,
                                 payload, offsets_words, sizes_words, blk.grp * 64 + blk.j * 16, lg,
                                 s_cdf, s_target, threadIdx.x);
 }
@@ -452,36 +413,16 @@ hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, floa
 // rows' round trip through memory, and the block's waves share their
 // operand loads.  Layer 0's LN1 gathers the embedding rows and the n-block
 // 0 blocks store them as x.
-// Copy of block vb's 64 weight rows into ws (global_load_lds_dwordx4: a
-// wave's 64 float4s are one contiguous 1 KB span at both ends): float4
-// r = tid % 256 of 16-k block q = 4 it + tid / 256.
-template <int NB>
-__device__ __forceinline__ void dec_ln_gemm_issue_w(const DecGemmArgs& a, int vb, float* ws,
-                                                    int tid) {
-  const XcdSlot blk = xcd_slot(vb, a.N / 64);
-  if (blk.grp * 64 >= a.M) return;
-  const int n0 = blk.j * 64, r = tid & 255;
-  const float4* W4 = reinterpret_cast<const float4*>(a.W);
-#pragma unroll
-  for (int it = 0; it < NB / 4; ++it) {
-    const int q = 4 * it + (tid >> 8);
-    __builtin_amdgcn_global_load_lds(
-        (const void*)(W4 + ((size_t)q * a.ldw + n0) * 4 + r),
-        (__attribute__((address_space(3))) void*)(reinterpret_cast<float4*>(ws) + q * 256 + (r & ~63)),
-        16, 0, 0);
-  }
-}
-
 // The block's work for virtual block vb, with its LDS passed in: xs and ws
-// of NB * 1024 floats each, lwb of 2 d, stats of 128.  With WPRE the weight
-// rows have been issued into ws already (dec_ln_gemm_issue_w).
-template <int MODE, int NB, bool EMB, bool COH, bool WPRE = false>
+// of NB * 1024 floats each, lwb of 2 d, stats of 128.
+template <int MODE, int NB, bool EMB>
 __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const float* __restrict__ emb,
                                                  const uint8_t* __restrict__ tok, float* xt,
                                                  const float* __restrict__ lw,
                                                  const float* __restrict__ lb, int vb, float* xs,
                                                  float* ws, float* lwb, float* stats, int tid) {
   constexpr int d = NB * 16;
+  const int n = a.ln_n;               // the LayerNorm's width: features n .. d-1 are zero
   constexpr int SQ = NB / 4;          // staged float4s per thread and operand
   static_assert(NB % 4 == 0, "d must be a multiple of 64");
   const XcdSlot blk = xcd_slot(vb, a.N / 64);
@@ -499,7 +440,7 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   for (int it = 0; it < SQ; ++it) {
     const int q = 4 * it + (tid >> 8);
     xr[it] = EMB ? *reinterpret_cast<const float4*>(erow + 16 * q + 4 * a4)
-                 : act_ld4<COH>(a.Xt, ((size_t)q * a.ldx + m) * 4 + a4);
+                 : reinterpret_cast<const float4*>(a.Xt)[((size_t)q * a.ldx + m) * 4 + a4];
   }
   for (int k = tid; k < d; k += 1024) { lwb[k] = lw[k]; lwb[d + k] = lb[k]; }
 #pragma unroll
@@ -520,15 +461,13 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   // barrier keeps them after the stores, whose wait would otherwise cover
   // them too): LN GEMMs 13.4 -> 13.2 us at 1000 lanes
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (!WPRE) {
 #pragma unroll
-    for (int it = 0; it < SQ; ++it) {
-      const int q = 4 * it + (tid >> 8);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(W4 + ((size_t)q * a.ldw + n0) * 4 + r),
-          (__attribute__((address_space(3))) void*)(reinterpret_cast<float4*>(ws) + q * 256 + (r & ~63)),
-          16, 0, 0);
-    }
+  for (int it = 0; it < SQ; ++it) {
+    const int q = 4 * it + (tid >> 8);
+    __builtin_amdgcn_global_load_lds(
+        (const void*)(W4 + ((size_t)q * a.ldw + n0) * 4 + r),
+        (__attribute__((address_space(3))) void*)(reinterpret_cast<float4*>(ws) + q * 256 + (r & ~63)),
+        16, 0, 0);
   }
   // LDS barrier without the fence of __syncthreads, which would wait for the
   // weight copies too: this wave's LDS stores are complete at lgkmcnt(0)
@@ -573,8 +512,8 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
       sq = sq + __shfl_down(sq, off, 16);
     }
     if (l == 0) {
-      const float mean = sum / (float)d;
-      const float var = sq / (float)d - mean * mean;
+      const float mean = sum / (float)n;
+      const float var = sq / (float)n - mean * mean;
       stats[2 * lj] = mean;
       stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
@@ -602,8 +541,8 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
       mean = stats[2 * ml];
       rstd = stats[2 * ml + 1];
     } else {  // from the two sums, as dec_ln_kernel
-      mean = stats[2 * ml] / (float)d;
-      const float var = stats[2 * ml + 1] / (float)d - mean * mean;
+      mean = stats[2 * ml] / (float)n;
+      const float var = stats[2 * ml + 1] / (float)n - mean * mean;
       rstd = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
 #pragma unroll
@@ -655,7 +594,7 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
   __shared__ float lwb[2 * NB * 16];
   __shared__ float stats[2 * 64];
   if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
-  dec_ln_gemm_body<MODE, NB, EMB, false>(a, emb, tok, xt, lw, lb, blockIdx.x, xs, ws, lwb, stats,
+  dec_ln_gemm_body<MODE, NB, EMB>(a, emb, tok, xt, lw, lb, blockIdx.x, xs, ws, lwb, stats,
                                          threadIdx.x);
 }
 
@@ -768,7 +707,7 @@ __global__ __launch_bounds__(16 * LANES) void dec_ln_kernel(const float* __restr
                                                      const float* src, float* xnt,
                                                      const float* __restrict__ w,
                                                      const float* __restrict__ b, int M, int ld,
-                                                     int* t_counter) {
+                                                     int* t_counter, int n) {
   constexpr int d = NB * 16;
   constexpr int S = d + 4;                 // LDS row stride (floats)
   constexpr int IT = (NB + 3) / 4;         // feature blocks per thread
@@ -823,8 +762,8 @@ __global__ __launch_bounds__(16 * LANES) void dec_ln_kernel(const float* __restr
       sq = sq + __shfl_down(sq, off, 16);
     }
     if (l == 0) {
-      const float mean = sum / (float)d;
-      const float var = sq / (float)d - mean * mean;
+      const float mean = sum / (float)n;
+      const float var = sq / (float)n - mean * mean;
       stats[2 * lj] = mean;
       stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
@@ -839,8 +778,8 @@ __global__ __launch_bounds__(16 * LANES) void dec_ln_kernel(const float* __restr
       sum = sum + x.z; sq = sq + x.z * x.z;
       sum = sum + x.w; sq = sq + x.w * x.w;
     }
-    const float mean = sum / (float)d;
-    const float var = sq / (float)d - mean * mean;
+    const float mean = sum / (float)n;
+    const float var = sq / (float)n - mean * mean;
     stats[2 * t] = mean;
     stats[2 * t + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
   }
@@ -869,17 +808,17 @@ __global__ __launch_bounds__(16 * LANES) void dec_ln_kernel(const float* __restr
 namespace {
 template <int MODE>
 hipError_t dec_ln_launch(const float* emb, const uint8_t* tok, float* xt, const float* src,
-                         float* xnt, const float* w, const float* b, int M, int d, int ld,
+                         float* xnt, const float* w, const float* b, int M, int d, int n, int ld,
                          int* t_counter, hipStream_t s) {
   constexpr int LN = DEC_LN_LANES;
   const dim3 grid((M + LN - 1) / LN), block(16 * LN);
 #define BOA_DEC_LN(NBv)                                                                      \
   if (emb)                                                                                   \
     BOA_LAUNCH((dec_ln_kernel<MODE, NBv, true, LN>), grid, block, 0, s, emb, tok, xt, \
-                       src, xnt, w, b, M, ld, t_counter);                                    \
+                       src, xnt, w, b, M, ld, t_counter, n);                                 \
   else                                                                                       \
     BOA_LAUNCH((dec_ln_kernel<MODE, NBv, false, LN>), grid, block, 0, s, emb, tok,   \
-                       xt, src, xnt, w, b, M, ld, t_counter);
+                       xt, src, xnt, w, b, M, ld, t_counter, n);
   switch (d) {
     case 64: BOA_DEC_LN(4) break;
     case 80: BOA_DEC_LN(5) break;
@@ -894,14 +833,14 @@ hipError_t dec_ln_launch(const float* emb, const uint8_t* tok, float* xt, const 
 }  // namespace
 
 hipError_t launch_dec_ln1(const float* emb, const uint8_t* tok, float* xt, float* xnt,
-                          const float* w, const float* b, int M, int d, int ld, int* t_counter,
-                          hipStream_t s) {
-  return dec_ln_launch<1>(emb, tok, xt, xt, xnt, w, b, M, d, ld, t_counter, s);
+                          const float* w, const float* b, int M, int d, int n, int ld,
+                          int* t_counter, hipStream_t s) {
+  return dec_ln_launch<1>(emb, tok, xt, xt, xnt, w, b, M, d, n, ld, t_counter, s);
 }
 
 hipError_t launch_dec_ln2(const float* xt, float* xnt, const float* w, const float* b, int M, int d,
-                          int ld, hipStream_t s) {
-  return dec_ln_launch<2>(nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, ld, nullptr, s);
+                          int n, int ld, hipStream_t s) {
+  return dec_ln_launch<2>(nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, n, ld, nullptr, s);
 }
 
 // ------------------------------------------------------------------- scan
@@ -1021,7 +960,7 @@ struct XscanPos {
   }
 };
 
-// The loads of the x_proj + scan that depend on no other workgroup: both
+// The loads of the x_proj + scan that depend on no other block: both
 // channels' state and the first channel's scan parameters.
 template <int DS, int RB>
 struct XscanPre {
@@ -1067,22 +1006,9 @@ __device__ __forceinline__ void xscan_load_params(XscanPre<DS, RB>& pr, const Xs
   sc0.bdt = Lw.b_dt[c];
   sc0.dd = Lw.dd[c];
 }
-// Both, for the group step to issue ahead of its barrier (lanes past M as
-// the body: a whole block past M loads nothing).
+// The block's work for virtual block vb, its x_proj rows in LDS at rown;
+// pl receives the loads that depend on no other block.
 template <int DS, int RB, int DI, bool CACHED>
-__device__ __forceinline__ void dec_xscan_pre(XscanPre<DS, RB>& pr, const LayerW& Lw,
-                                              const float* na_q, const float* wdt_q,
-                                              const float* ssm, int M, int ld_state, int vb,
-                                              int tid) {
-  const XscanPos<DI> ps(vb, tid, M);
-  if (ps.m0 >= M) return;
-  xscan_load_state<DS, RB, DI, CACHED>(pr, ps, ssm, ld_state);
-  xscan_load_params<DS, RB, DI>(pr, ps, Lw, na_q, wdt_q);
-}
-
-// The block's work for virtual block vb, its x_proj rows in LDS at rown.
-// pl holds the independent loads: made here, or with PRE by dec_xscan_pre.
-template <int DS, int RB, int DI, bool CACHED, bool COH, bool PRE = false>
 __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __restrict__ na_q,
                                                const float* __restrict__ wdt_q,
                                                const float* __restrict__ w_x, int ldw_x,
@@ -1100,7 +1026,7 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
   // 1. both channels' state (16-channel blocks 8 cb + q and 8 cb + q + 4),
   // in flight during x_proj (loading the second one only after the first
   // channel's scan measured 18.2 against 16.6 us per launch at 1000 lanes)
-  if constexpr (!PRE) xscan_load_state<DS, RB, DI, CACHED>(pl, ps, ssm, ld_state);
+  xscan_load_state<DS, RB, DI, CACHED>(pl, ps, ssm, ld_state);
   const float* h0 = pl.h0;
   const float* h1 = pl.h1;
   // the two channels' conv output and z (of lane mc) and the first channel's
@@ -1109,10 +1035,10 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const size_t cmp = dblk(16 * (8 * cb + q + 4 * p) + cl, mc, ld);
-    uz[p][0] = act_ld<COH>(cvt, cmp);
-    uz[p][1] = act_ld<COH>(zt, cmp);
+    uz[p][0] = cvt[cmp];
+    uz[p][1] = zt[cmp];
   }
-  if constexpr (!PRE) xscan_load_params<DS, RB, DI>(pl, ps, Lw, na_q, wdt_q);
+  xscan_load_params<DS, RB, DI>(pl, ps, Lw, na_q, wdt_q);
   const ScanCtx<DS, RB>& sc0 = pl.sc0;
   // 2. x_proj: wave w < NB computes feature block w for lanes m0 .. m0 + 15
   const int wv = tid >> 6;
@@ -1121,7 +1047,7 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
     DecGemmArgs a{};
     a.Xt = cvt; a.ldx = ld; a.W = w_x; a.ldw = ldw_x; a.M = M; a.N = NB * 16; a.K = DI;
     floatx4 acc[1][1];
-    dec_mainloop<DI / 4, 1, 1, 1, 4, COH>(a, 16 * wv, m0, i, g, acc);
+    dec_mainloop<DI / 4, 1, 1, 1, 4>(a, 16 * wv, m0, i, g, acc);
 #pragma unroll
     for (int v = 0; v < 4; ++v)  // the bias-free epilogue of dec_gemm_kernel: acc + 0
       rown[i * RS + 16 * wv + 4 * v + g] = acc[0][0][v] + 0.0f;
@@ -1176,7 +1102,7 @@ __global__ __launch_bounds__(1024) void dec_xscan_kernel(LayerW Lw, const float*
                                                          int ld_state, int r) {
   __shared__ __align__(16) float rown[xscan_lds_floats<DS, RB>()];
   XscanPre<DS, RB> pl;
-  dec_xscan_body<DS, RB, DI, CACHED, false>(Lw, na_q, wdt_q, w_x, ldw_x, zt, cvt, ssm, yt, M, ld,
+  dec_xscan_body<DS, RB, DI, CACHED>(Lw, na_q, wdt_q, w_x, ldw_x, zt, cvt, ssm, yt, M, ld,
                                             ld_state, r, blockIdx.x, rown, threadIdx.x, pl);
 }
 
@@ -1286,216 +1212,6 @@ hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, floa
   else
     BOA_LAUNCH(state_to_chunk_kernel, dim3((n + 255) / 256), dim3(256), 0, s, conv_in,
                        ssm_in, conv_out, ssm_out, lanes, di, ds, ld_state, conv_b16 ? 1 : 0);
-  return hipGetLastError();
-}
-
-// ------------------------------------------ group-synchronous decode step
-// Barrier of the 16 workgroups of a 64-lane group.  Every wave waits until
-// its stores of the phase are complete (in the XCD's L2) before thread 0
-// adds one to the group's counter; thread 0 then polls the counter with
-// device-scope loads until it reaches the next multiple of 16.  The counter
-// only grows, launch after launch, so it is never reset while steps run.
-// The wait is bounded: after kGroupSpin polls, or once another workgroup
-// has set *abort, it sets *abort and returns false, and the caller ends the
-// launch.
-// It comes in two halves so that loads of the next phase that depend on
-// no other workgroup can be issued between them and overlap the wait:
-// group_stores_done (every wave's stores of the phase complete), then
-// group_wait (arrive and wait).  group_wait's workgroup barriers wait for
-// LDS only, so such loads stay in flight; but thread 0's polls wait on every
-// load of wave 0, so wave 0 issues its share after group_wait returns.
-constexpr int kGroupSpin = 1 << 20;
-__device__ __forceinline__ void group_stores_done() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
-__device__ __forceinline__ bool group_wait(unsigned* ctr, int* abort, int* s_ok) {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned target = (old & ~15u) + 16u;
-    int ok = 1;
-    for (int spin = 0;; ++spin) {
-      const unsigned c = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((int)(c - target) >= 0) break;
-      if (spin >= kGroupSpin ||
-          ((spin & 255) == 255 && __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-        __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ok = 0;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    *s_ok = ok;
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  return *s_ok != 0;
-}
-__device__ __forceinline__ bool group_sync(unsigned* ctr, int* abort, int* s_ok) {
-  group_stores_done();
-  return group_wait(ctr, abort, s_ok);
-}
-
-// LDS of the step: the LayerNorm-GEMM phases' (two 64 x 256 tiles, the
-// LayerNorm weights, the statistics); the scan's x_proj rows and the head
-// step's logits and CDFs reuse its start.
-constexpr int GROUP_LDS_FLOATS = 2 * 16 * 1024 + 2 * 256 + 128;
-static_assert(16 * HS_LS + 2 * 16 * 260 + 16 <= GROUP_LDS_FLOATS, "head step LDS");
-static_assert(xscan_lds_floats<16, 16>() <= GROUP_LDS_FLOATS, "scan LDS");
-
-// Each phase of the group step takes the thread index through an opaque
-// move, so that the compiler derives the phase's addresses there instead of
-// keeping those of every phase live across the layer loop (and spilling
-// them).
-__device__ __forceinline__ int opaque_tid() {
-  int t = threadIdx.x;
-  asm volatile("" : "+v"(t));
-  return t;
-}
-
-// The boundary after LN1 + in_proj + conv, then x_proj + scan: the scan's
-// state and first scan parameters are loaded across the barrier (wave 0's
-// after it, see group_wait).
-template <bool CACHED>
-__device__ __forceinline__ bool xscan_phase(const GroupLayerPlan& lp, const GroupPlan* P, int M,
-                                            int vb, float* lds, unsigned* ctr, int* abort,
-                                            int* s_ok) {
-  XscanPre<16, 16> pl;
-  group_stores_done();
-  int tid = opaque_tid();
-  if (tid >= 64) dec_xscan_pre<16, 16, 512, CACHED>(pl, lp.lw, lp.na, lp.wdt, lp.ssm, M, P->ld, vb, tid);
-  if (!group_wait(ctr, abort, s_ok)) return false;
-  if (tid < 64) dec_xscan_pre<16, 16, 512, CACHED>(pl, lp.lw, lp.na, lp.wdt, lp.ssm, M, P->ld, vb, tid);
-  tid = opaque_tid();
-  dec_xscan_body<16, 16, 512, CACHED, true, true>(lp.lw, lp.na, lp.wdt, lp.w_x, lp.ldw_x, P->zt,
-                                                  P->cvt, lp.ssm, P->yt, M, P->ld, P->ld, P->r, vb,
-                                                  lds, tid, pl);
-  return true;
-}
-
-// One decode step of every lane (boa_gpu.hpp:1034-1053 for the model,
-// range_coder_kernels.cu:504-627 for the CDF, search and coder advance):
-// per layer LN1 + in_proj + conv, x_proj + scan, out_proj, LN2 + FF1 + GELU,
-// FF2 + residual; then head.1 and head.2 + CDF + search + coder.  Virtual
-// block vb = blockIdx.x runs, in each phase, exactly the work that block vb
-// of the chain's kernel for that phase runs (every phase maps blocks with
-// xcd_slot(vb, 16)), so results are the chain's bit for bit.
-__global__ __launch_bounds__(1024) void dec_group_step_kernel(const GroupPlan* __restrict__ P) {
-  __shared__ __align__(16) float lds[GROUP_LDS_FLOATS];
-  __shared__ int s_ok;
-  if (*P->abort) return;  // an earlier launch gave up: the batch has failed
-  // The group of a workgroup is taken from the XCD it runs on, so that the
-  // 16 workgroups of a group share that XCD's L2: workgroups go to the 8
-  // XCDs round-robin, starting where the previous dispatch left off, so
-  // block b runs on XCD (o + b) % 8 for one offset o per launch.  Octet
-  // b / 8 then holds one workgroup per XCD, and workgroup (XCD x, octet s)
-  // is member s % 16 of group x + 8 (s / 16).
-  __shared__ unsigned s_xcc;
-  if (threadIdx.x == 0) {
-    unsigned xcc;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-    s_xcc = xcc & 7u;
-  }
-  __syncthreads();
-  const int x = (int)s_xcc, oct = (int)(blockIdx.x >> 3);
-  const int grp = x + 8 * (oct >> 4), j = oct & 15;
-  const int M = P->M;
-  if (grp * 64 >= M) return;  // a group without lanes: all 16 of its workgroups
-  // the chain kernels' block index of this work (xcd_slot(vb, 16) = (grp, j))
-  const int vb = 8 * (16 * (grp >> 3) + j) + (grp & 7);
-  unsigned* ctr = P->bar + 64 * grp;
-  int* abort = P->abort;
-  // Every member records the launch's offset o as it sees it; after the
-  // first barrier each compares the group's records with its own.  A
-  // dispatch that is not round-robin puts two workgroups of one octet on
-  // one XCD (two members of one group with different o) or leaves a group
-  // short (its barrier times out): either way the launch gives up.
-  const int o = (x - (int)(blockIdx.x & 7)) & 7;
-  int* o_rec = P->o_rec + 16 * grp;
-  if (threadIdx.x == 0) o_rec[j] = o;
-  const int t = P->t_group[grp] + 1;  // written by the previous launch
-  if (!group_sync(ctr, abort, &s_ok)) return;
-  {
-    const bool bad = threadIdx.x < 16 &&
-                     (int)__builtin_amdgcn_raw_buffer_load_b32(
-                         act_rsrc(reinterpret_cast<const float*>(o_rec)), threadIdx.x * 4, 0, 16) != o;
-    if (__syncthreads_or(bad)) {
-      if (threadIdx.x == 0) __hip_atomic_store(abort, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-  }
-  const XcdSlot gs{grp, j};
-  float* xs = lds;
-  float* ws = lds + 16 * 1024;
-  float* lwb = lds + 32 * 1024;
-  float* st = lwb + 2 * 256;
-  const int L = P->L;
-  // a phase boundary with loads of the next phase issued across it
-  auto boundary = [&](auto&& issue) {
-    group_stores_done();
-    const int tid = opaque_tid();
-    if (tid >= 64) issue(tid);
-    if (!group_wait(ctr, abort, &s_ok)) return false;
-    if (tid < 64) issue(tid);
-    return true;
-  };
-  for (int l = 0; l < L; ++l) {
-    const GroupLayerPlan& lp = P->layer[l];
-    // LN1 + in_proj + conv; from layer 1 on, its weight rows were issued
-    // into ws across the last barrier
-    if (l == 0)
-      dec_ln_gemm_body<1, 16, true, true>(lp.in, P->emb, P->tok, P->xt, lp.lw.ln1_w, lp.lw.ln1_b,
-                                          vb, xs, ws, lwb, st, opaque_tid());
-    else
-      dec_ln_gemm_body<1, 16, false, true, true>(lp.in, nullptr, nullptr, nullptr, lp.lw.ln1_w,
-                                                 lp.lw.ln1_b, vb, xs, ws, lwb, st, opaque_tid());
-    // x_proj + scan, its state and first scan parameters loaded across the
-    // barrier (the cache policy of the state is a template argument, so
-    // each branch holds a whole boundary and body)
-    if (lp.cached) {
-      if (!xscan_phase<true>(lp, P, M, vb, lds, ctr, abort, &s_ok)) return;
-    } else {
-      if (!xscan_phase<false>(lp, P, M, vb, lds, ctr, abort, &s_ok)) return;
-    }
-    if (!group_sync(ctr, abort, &s_ok)) return;
-    if (threadIdx.x < 256) dec_gemm_wave<128, 1, 8, true>(lp.out, vb, opaque_tid());
-    // LN2 + FF1 + GELU, its weight rows issued into ws across the barrier
-    if (!boundary([&](int tid) { dec_ln_gemm_issue_w<16>(lp.ff1, vb, ws, tid); })) return;
-    dec_ln_gemm_body<2, 16, false, true, true>(lp.ff1, nullptr, nullptr, nullptr, lp.lw.ln2_w,
-                                               lp.lw.ln2_b, vb, xs, ws, lwb, st, opaque_tid());
-    if (!group_sync(ctr, abort, &s_ok)) return;
-    if (threadIdx.x < 256) dec_gemm_wave<256, 1, 8, true>(lp.ff2, vb, opaque_tid());
-    if (l + 1 < L) {
-      const DecGemmArgs& nin = P->layer[l + 1].in;
-      if (!boundary([&](int tid) { dec_ln_gemm_issue_w<16>(nin, vb, ws, tid); })) return;
-    } else if (!group_sync(ctr, abort, &s_ok)) {
-      return;
-    }
-  }
-  if (threadIdx.x < 256) dec_gemm_wave<64, 1, 8, true>(P->head1, vb, opaque_tid());
-  if (!group_sync(ctr, abort, &s_ok)) return;
-  if (gs.j < 4)  // 16 lanes per workgroup
-    dec_head_step_body<64, true>(P->head2, P->head_b2, P->inv_t, P->tok, P->lens, t, P->out,
-                                 P->out_stride, P->states, P->payload, P->offsets, P->sizes,
-                                 gs.grp * 64 + 16 * gs.j, lds,
-                                 reinterpret_cast<double(*)[260]>(lds + 16 * HS_LS),
-                                 reinterpret_cast<uint32_t*>(lds + 16 * HS_LS + 2 * 16 * 260),
-                                 opaque_tid());
-  // every member has read t_group (before the first barrier)
-  if (gs.j == 0 && threadIdx.x == 0) {
-    P->t_group[gs.grp] = t;
-    if (gs.grp == 0) *P->t_counter = t;
-  }
-}
-
-bool dec_group_fits(const Dims& D, int lanes, int n_cus) {
-  return D.d == 256 && D.di == 512 && D.ds == 16 && dec_rb(D.r) == 16 &&
-         D.L <= GROUP_MAX_LAYERS && lanes >= 1 && lanes <= GROUP_MAX_LANES &&
-         (int)xcd_grid(lanes, 16) <= n_cus;
-}
-
-hipError_t launch_dec_group_step(const GroupPlan* d_plan, int lanes, hipStream_t s) {
-  if (lanes < 1 || lanes > GROUP_MAX_LANES) return hipErrorInvalidValue;
-  BOA_LAUNCH(dec_group_step_kernel, dim3(xcd_grid(lanes, 16)), dim3(1024), 0, s, d_plan);
   return hipGetLastError();
 }
 

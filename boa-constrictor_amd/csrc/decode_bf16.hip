@@ -417,7 +417,7 @@ __global__ __launch_bounds__(256) void dec_b16_ln_kernel(const float* __restrict
                                                          const void* src, uint16_t* xnt,
                                                          const float* __restrict__ w,
                                                          const float* __restrict__ b, int M,
-                                                         int ld, int* t_counter) {
+                                                         int ld, int* t_counter, int n) {
   constexpr int d = NB * 16;
   constexpr int S = d + 4;
   __shared__ __align__(16) float tile[16 * S];
@@ -470,8 +470,8 @@ __global__ __launch_bounds__(256) void dec_b16_ln_kernel(const float* __restrict
       sq = sq + __shfl_down(sq, off, 16);
     }
     if (l == 0) {
-      const float mean = sum / (float)d;
-      const float var = sq / (float)d - mean * mean;
+      const float mean = sum / (float)n;
+      const float var = sq / (float)n - mean * mean;
       stats[2 * lj] = mean;
       stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
@@ -485,8 +485,8 @@ __global__ __launch_bounds__(256) void dec_b16_ln_kernel(const float* __restrict
       sum = sum + x.z; sq = sq + x.z * x.z;
       sum = sum + x.w; sq = sq + x.w * x.w;
     }
-    const float mean = sum / (float)d;
-    const float var = sq / (float)d - mean * mean;
+    const float mean = sum / (float)n;
+    const float var = sq / (float)n - mean * mean;
     stats[2 * t] = mean;
     stats[2 * t + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
   }
@@ -519,14 +519,14 @@ __global__ __launch_bounds__(256) void dec_b16_ln_kernel(const float* __restrict
 
 template <int MODE, int IN>
 static hipError_t dec_b16_ln_go(const float* emb, const uint8_t* tok, float* xt, const void* src,
-                                uint16_t* xnt, const float* w, const float* b, int M, int d, int ld,
-                                int* t_counter, hipStream_t s) {
+                                uint16_t* xnt, const float* w, const float* b, int M, int d, int n,
+                                int ld, int* t_counter, hipStream_t s) {
   const dim3 grid((M + 15) / 16), block(256);
   switch (d) {
-    case 64: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 4, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
-    case 128: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 8, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
-    case 256: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 16, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
-    case 512: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 32, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter); break;
+    case 64: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 4, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter, n); break;
+    case 128: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 8, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter, n); break;
+    case 256: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 16, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter, n); break;
+    case 512: BOA_LAUNCH((dec_b16_ln_kernel<MODE, 32, IN>), grid, block, 0, s, emb, tok, xt, src, xnt, w, b, M, ld, t_counter, n); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -534,17 +534,18 @@ static hipError_t dec_b16_ln_go(const float* emb, const uint8_t* tok, float* xt,
 
 // LN1: from the embedding (emb != null; also stores x) or from fp32 x.
 hipError_t launch_dec_b16_ln1(const float* emb, const uint8_t* tok, float* xt, uint16_t* xnt,
-                              const float* w, const float* b, int M, int d, int ld, int* t_counter,
-                              hipStream_t s) {
-  return emb ? dec_b16_ln_go<1, LN_IN_EMB>(emb, tok, xt, nullptr, xnt, w, b, M, d, ld, t_counter, s)
-             : dec_b16_ln_go<1, LN_IN_F32>(nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, ld,
+                              const float* w, const float* b, int M, int d, int n, int ld,
+                              int* t_counter, hipStream_t s) {
+  return emb ? dec_b16_ln_go<1, LN_IN_EMB>(emb, tok, xt, nullptr, xnt, w, b, M, d, n, ld,
+                                           t_counter, s)
+             : dec_b16_ln_go<1, LN_IN_F32>(nullptr, nullptr, nullptr, xt, xnt, w, b, M, d, n, ld,
                                            t_counter, s);
 }
 
 hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w, const float* b,
-                              int M, int d, int ld, hipStream_t s) {
-  return dec_b16_ln_go<2, LN_IN_B16>(nullptr, nullptr, nullptr, src, xnt, w, b, M, d, ld, nullptr,
-                                     s);
+                              int M, int d, int n, int ld, hipStream_t s) {
+  return dec_b16_ln_go<2, LN_IN_B16>(nullptr, nullptr, nullptr, src, xnt, w, b, M, d, n, ld,
+                                     nullptr, s);
 }
 
 // ------------------------------------------------------------------- scan

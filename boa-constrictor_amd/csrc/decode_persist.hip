@@ -71,9 +71,9 @@ __device__ __forceinline__ float4* pd_out(float* base, int n0, int i, int g) {
 // MODE 1 (LN1): 16 threads per lane, the reference's warp-tree order, stats =
 // (mean, rstd).  MODE 2 (LN2): sequential sums (one thread for the sum, one
 // for the squares), stats = (sum, sum of squares).  The orders of
-// dec_ln_gemm_kernel.
+// dec_ln_gemm_kernel.  n: the LayerNorm's width (features n .. d-1 are zero).
 template <int MODE, int NB>
-__device__ __forceinline__ void pd_ln_stats(const float* xs, float* stats, int tid) {
+__device__ __forceinline__ void pd_ln_stats(const float* xs, float* stats, int tid, int n) {
   constexpr int d = NB * 16;
   if (MODE == 1) {
     if (tid >= 16 * PL) return;
@@ -99,8 +99,8 @@ __device__ __forceinline__ void pd_ln_stats(const float* xs, float* stats, int t
       sq = sq + __shfl_down(sq, off, 16);
     }
     if (l == 0) {
-      const float mean = sum / (float)d;
-      const float var = sq / (float)d - mean * mean;
+      const float mean = sum / (float)n;
+      const float var = sq / (float)n - mean * mean;
       stats[2 * lj] = mean;
       stats[2 * lj + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
@@ -127,8 +127,7 @@ __device__ __forceinline__ void pd_ln_stats(const float* xs, float* stats, int t
 template <int MODE, int NB>
 __device__ __forceinline__ void pd_ln_apply(const float* xs, float* xn, const float* stats,
                                             const float* __restrict__ w,
-                                            const float* __restrict__ b, int tid) {
-  constexpr int d = NB * 16;
+                                            const float* __restrict__ b, int tid, int n) {
   for (int p = tid; p < NB * 256; p += 1024) {
     const int q = p >> 8, m = (p >> 4) & 15, f = 16 * q + dperm(p & 15);
     float mean, rstd;
@@ -136,8 +135,8 @@ __device__ __forceinline__ void pd_ln_apply(const float* xs, float* xn, const fl
       mean = stats[2 * m];
       rstd = stats[2 * m + 1];
     } else {
-      mean = stats[2 * m] / (float)d;
-      const float var = stats[2 * m + 1] / (float)d - mean * mean;
+      mean = stats[2 * m] / (float)n;
+      const float var = stats[2 * m + 1] / (float)n - mean * mean;
       rstd = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
     xn[p] = ((xs[p] - mean) * rstd) * w[f] + b[f];
@@ -240,9 +239,9 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
         }
         __syncthreads();
       }
-      pd_ln_stats<1, NB>(xs, stats, tid);
+      pd_ln_stats<1, NB>(xs, stats, tid, a.ln_n);
       __syncthreads();
-      pd_ln_apply<1, NB>(xs, xn, stats, q + O_LN1W, q + O_LN1B, tid);
+      pd_ln_apply<1, NB>(xs, xn, stats, q + O_LN1W, q + O_LN1B, tid, a.ln_n);
       __syncthreads();
       // in_proj: features < DI run the conv step (state float4 [c][lane]),
       // features >= DI are z
@@ -327,9 +326,9 @@ __global__ __launch_bounds__(1024) void dec_persist_kernel(PersistArgs a) {
         *pd_out(os, n0, i, g) = make_float4(v[0], v[1], v[2], v[3]);
       }
       __syncthreads();
-      pd_ln_stats<2, NB>(os, stats, tid);
+      pd_ln_stats<2, NB>(os, stats, tid, a.ln_n);
       __syncthreads();
-      pd_ln_apply<2, NB>(os, xn, stats, q + O_LN2W, q + O_LN2B, tid);
+      pd_ln_apply<2, NB>(os, xn, stats, q + O_LN2W, q + O_LN2B, tid, a.ln_n);
       __syncthreads();
       // FF1 + bias + GELU
       for (int tile = wv; tile < NBF; tile += 16) {

@@ -350,8 +350,8 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
           sq = sq + hi * hi;
         }
       }
-      const float mean = sm / (float)D;
-      const float var = sq / (float)D - mean * mean;
+      const float mean = sm / (float)a.n;
+      const float var = sq / (float)a.n - mean * mean;
       lnst[2 * tid] = mean;
       lnst[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
     }
@@ -491,8 +491,8 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
       }
       sm = __shfl(sm, 0, 32);
       sq = __shfl(sq, 0, 32);
-      const float mean = sm / (float)D;
-      const float var = sq / (float)D - mean * mean;
+      const float mean = sm / (float)a.n;
+      const float var = sq / (float)a.n - mean * mean;
       const float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
 #pragma unroll
       for (int e = 0; e < D / 32; ++e) {
@@ -521,7 +521,9 @@ __global__ __launch_bounds__(1024) void ffn_bf16_kernel(FfnB16Args a) {
   }
 }
 
-hipError_t ffn_bf16(const FfnB16Args& a, hipStream_t s) {
+hipError_t ffn_bf16(const FfnB16Args& args, hipStream_t s) {
+  FfnB16Args a = args;
+  if (a.n <= 0) a.n = a.D;  // the LayerNorms' width defaults to the row width
   if (a.M <= 0) return hipSuccess;
   const unsigned blocks = (unsigned)((a.M + 127) / 128);
   switch (a.D) {

@@ -236,8 +236,8 @@ void gemm_f32_kernel(
             sq = sq + __shfl_down(sq, off, 32);
           }
           if (l == 0) {
-            const float mean = sm / (float)D;
-            const float var = sq / (float)D - mean * mean;
+            const float mean = sm / (float)ln.n;
+            const float var = sq / (float)ln.n - mean * mean;
             stat[2 * row_i] = mean;
             stat[2 * row_i + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
           }
@@ -250,8 +250,8 @@ void gemm_f32_kernel(
           sm = sm + e;
           sq = sq + e * e;
         }
-        const float mean = sm / (float)D;
-        const float var = sq / (float)D - mean * mean;
+        const float mean = sm / (float)ln.n;
+        const float var = sq / (float)ln.n - mean * mean;
         stat[2 * tid] = mean;
         stat[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
       }

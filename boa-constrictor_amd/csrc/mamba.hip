@@ -47,11 +47,16 @@ __device__ __forceinline__ void st4(uint16_t* p, const float* v) {
 // 2, 1, lane 0's
 // totals broadcast.  Layer 0 gathers the embedding rows of the tile's
 // tokens and also stores them as x.
+// Rows are D wide, of which the model's n <= D features are real: a model
+// of d_model n is run at the next width D the kernels are built for, its
+// features n .. D-1 zero (weights and activations).  Those zeros add +0 to
+// the sums, which leaves them unchanged, and the mean and variance divide
+// by n, so the statistics are the n-feature row's.
 template <typename TO, int D>
 __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb, TokenSrc tok,
                                                   int use_tok, int T, int t0, float* x, TO* xn,
                                                   const float* __restrict__ w,
-                                                  const float* __restrict__ b, int rows) {
+                                                  const float* __restrict__ b, int rows, int n) {
   constexpr int RPB = 8, S = D + 4, DQ = D / 4;
   constexpr int NQ = (RPB * DQ + 255) / 256;
   __shared__ __align__(16) float tile[RPB * S];
@@ -99,8 +104,8 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
   }
   sum = __shfl(sum, 0, 32);
   sq = __shfl(sq, 0, 32);
-  const float mean = sum / (float)D;
-  const float var = sq / (float)D - mean * mean;
+  const float mean = sum / (float)n;
+  const float var = sq / (float)n - mean * mean;
   const float inv_std = 1.0f / __builtin_sqrtf(var + 1e-5f);
 #pragma unroll
   for (int e = 0; e < (D + 31) / 32; ++e) {
@@ -116,16 +121,17 @@ __global__ __launch_bounds__(256) void ln1_kernel(const float* __restrict__ emb,
 }
 
 hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, void* xn,
-                      const float* w, const float* b, int rows, int d, bool bf16, hipStream_t s) {
+                      const float* w, const float* b, int rows, int d, int n, bool bf16,
+                      hipStream_t s) {
   const dim3 grid((rows + 7) / 8), block(256);
   const int ut = emb ? 1 : 0;
 #define BOA_LN1(Dv)                                                                          \
   if (bf16)                                                                                  \
     BOA_LAUNCH((ln1_kernel<uint16_t, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x, \
-                       (uint16_t*)xn, w, b, rows);                                           \
+                       (uint16_t*)xn, w, b, rows, n);                                        \
   else                                                                                       \
     BOA_LAUNCH((ln1_kernel<float, Dv>), grid, block, 0, s, emb, tok, ut, T, t0, x,    \
-                       (float*)xn, w, b, rows);
+                       (float*)xn, w, b, rows, n);
   switch (d) {
     case 64: BOA_LN1(64) break;
     case 80: BOA_LN1(80) break;
@@ -141,10 +147,10 @@ hipError_t launch_ln1(const float* emb, TokenSrc tok, int T, int t0, float* x, v
 // LN2: per-row sums in element order (the reference's thread-per-row order).
 // RPB rows per 256-thread block; thread t < RPB runs row t's sequential
 // sums over the LDS copy (row stride D + 1 keeps those reads conflict-free).
-// In place is allowed.
+// In place is allowed.  n <= D real features, as ln1_kernel.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void ln2_kernel(const T* x, T* out, const float* __restrict__ w,
-                                                  const float* __restrict__ b, int rows) {
+                                                  const float* __restrict__ b, int rows, int n) {
   constexpr int RPB = D <= 256 ? 32 : 16, S = D + 1, DQ = D / 4;
   constexpr int NQ = (RPB * DQ + 255) / 256;
   __shared__ float tile[RPB * S];
@@ -173,8 +179,8 @@ __global__ __launch_bounds__(256) void ln2_kernel(const T* x, T* out, const floa
       s = s + e;
       q = q + e * e;
     }
-    const float mean = s / (float)D;
-    const float var = q / (float)D - mean * mean;
+    const float mean = s / (float)n;
+    const float var = q / (float)n - mean * mean;
     stats[2 * tid] = mean;
     stats[2 * tid + 1] = 1.0f / __builtin_sqrtf(var + 1e-5f);
   }
@@ -198,17 +204,17 @@ __global__ __launch_bounds__(256) void ln2_kernel(const T* x, T* out, const floa
 }
 
 hipError_t launch_ln2(const void* x, void* out, const float* w, const float* b, int rows, int d,
-                      bool bf16, hipStream_t s) {
+                      int n, bool bf16, hipStream_t s) {
 #define BOA_LN2(Dv)                                                                             \
   {                                                                                             \
     constexpr int RPB = Dv <= 256 ? 32 : 16;                                                    \
     const dim3 grid((rows + RPB - 1) / RPB), block(256);                                        \
     if (bf16)                                                                                   \
       BOA_LAUNCH((ln2_kernel<uint16_t, Dv>), grid, block, 0, s, (const uint16_t*)x,     \
-                         (uint16_t*)out, w, b, rows);                                           \
+                         (uint16_t*)out, w, b, rows, n);                                        \
     else                                                                                        \
       BOA_LAUNCH((ln2_kernel<float, Dv>), grid, block, 0, s, (const float*)x,           \
-                         (float*)out, w, b, rows);                                              \
+                         (float*)out, w, b, rows, n);                                              \
   }
   switch (d) {
     case 64: BOA_LN2(64) break;

@@ -42,7 +42,10 @@ typedef struct boa_ctx boa_ctx;
  * --temperature CLI state of boa.cpp:838-897.  d_conv = 4 and expand = 2 are
  * fixed as in the reference; dt_rank = ceil(d_model / 16). */
 typedef struct {
-    int32_t d_model;     /* 64, 80, 128, 256 or 512 (bf16: not 80) */
+    int32_t d_model;     /* 1 .. 512.  The kernels are built for widths 64, 80,
+                            128, 256 and 512 (bf16: 64, 128, 256, 512); another
+                            d_model runs at the next built width with its extra
+                            features zero, giving the d_model's own results */
     int32_t n_layers;
     int32_t d_state;     /* 16 or 32 (the reference supports 16 only) */
     int32_t max_lanes;   /* chunks processed in parallel (--gpu-batch) */
@@ -91,21 +94,16 @@ int boa_set_progress(boa_ctx* ctx, boa_progress_fn fn, void* user);
  * schedule for `lanes` lanes): how many layers keep their recurrent state in
  * the caches (the rest stream it past them), and BOA_PLAN_* flags: LayerNorm
  * fused into in_proj and FF1, one persistent kernel for the whole batch,
- * x_proj fused into the scan, head.2 fused with the coder step, the whole
- * step in one group-synchronous launch (fp32 d_model 256 up to 1024 lanes).
+ * x_proj fused into the scan, head.2 fused with the coder step.
  * boa_set_state_cache_budget sets the bytes of decode state kept in the
  * caches (< 0 restores the default, 160 MiB), which changes only the cache
- * policy of the state accesses, never the results.  boa_set_decode_group(ctx,
- * 1) runs the step as one group-synchronous launch where it applies, 0 (the
- * default) as its chain of launches; both give the same bytes. */
+ * policy of the state accesses, never the results. */
 #define BOA_PLAN_FUSED_LN 1
 #define BOA_PLAN_PERSISTENT 2
 #define BOA_PLAN_FUSED_XPROJ 4
 #define BOA_PLAN_FUSED_HEAD 8
-#define BOA_PLAN_GROUP_STEP 16
 int boa_decode_plan(const boa_ctx* ctx, int32_t lanes, int32_t* cached_layers, int32_t* flags);
 int boa_set_state_cache_budget(boa_ctx* ctx, int64_t bytes);
-int boa_set_decode_group(boa_ctx* ctx, int32_t enable);
 
 /* Weights in the convert_boa_weights.py layout: "BOA\0" fp32, "BOA\1" fp16 or
  * headerless fp32.  Replaces BoaPredictorGPU::load_weights
@@ -136,8 +134,9 @@ int boa_forward_chunk(boa_ctx* ctx, const uint8_t* d_tokens, int32_t lanes, int3
  * boa_forward_chunk, but the activations live in a fixed 64 MiB scratch
  * array per GPU (held until the process ends) instead of buffers the
  * context grows on demand; the call makes no hipMalloc, hipFree or other
- * allocating call.  Limit: lanes x T <= (64 MiB - 1792) / (4 (14 d_model +
- * ceil(d_model/16) + 2 d_state)) rows (4619 at d_model 256, d_state 16);
+ * allocating call.  Limit: lanes x T <= (64 MiB - 1792) / (4 (14 w +
+ * ceil(d_model/16) + 2 d_state)) rows, w the built width d_model runs at
+ * (4619 at d_model 256, d_state 16);
  * larger requests fail with BOA_E_ARG.  Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (two host threads, or
  * two streams) race, so serialise them.  HIP-event profiling is off during
@@ -234,8 +233,7 @@ uint32_t boa_crc32(const uint8_t* data, int64_t n);
 #define BOA_K_DEC_SCAN 9   /* decode-step scan (x_proj fused in where it runs so) */
 #define BOA_K_HEAD_CDF 10  /* compress head.2 fused with the CDF (fp32) */
 #define BOA_K_DEC_LNGEMM 11 /* decode-step LayerNorm + in_proj / FF1 GEMMs */
-#define BOA_K_DEC_STEP 12  /* group-synchronous decode step: a whole step in one launch */
-#define BOA_K_COUNT 13
+#define BOA_K_COUNT 12
 /* When enabled, every kernel launch is bracketed by HIP events recorded on
  * the launch stream; boa_profile_read synchronises and returns, for a
  * kernel class, the summed kernel time (ms), the launch count and the

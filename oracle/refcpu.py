@@ -13,7 +13,26 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librefcpu.so")
+# Two builds of the same source: x86-64-v3 (AVX2 + FMA; the tests' default)
+# and x86-64-v4 (AVX-512), chosen with REFCPU_ISA=v4 before the first load.
+# Neither reassociates nor contracts floating-point operations
+# (-ffp-contract=off, no -ffast-math), so both compute the same bits.
+ISA_LIBS = {"v3": "librefcpu.so", "v4": "librefcpu_v4.so"}
+ISA = os.environ.get("REFCPU_ISA", "v3")
+LIB_PATH = os.path.join(HERE, ISA_LIBS.get(ISA, ISA_LIBS["v3"]))
+
+
+def host_has_avx512() -> bool:
+    """AVX-512 F/BW/CD/DQ/VL, the x86-64-v4 level, on this host."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    fl = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= fl
+    except OSError:
+        pass
+    return False
 
 
 def build() -> str:

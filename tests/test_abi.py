@@ -27,9 +27,9 @@ def test_host_only_entry_points():
 
 def test_create_rejects_bad_configs():
     h = ctypes.c_void_p()
-    for bad in [boa_hip.Config(250, 8, 16, 10, 0, 0, 1.0),   # d_model % 16
-                boa_hip.Config(96, 8, 16, 10, 0, 0, 1.0),    # d_model without kernels
-                boa_hip.Config(80, 8, 16, 10, 0, 1, 1.0),    # bf16 needs d_model % 64 == 0
+    for bad in [boa_hip.Config(513, 8, 16, 10, 0, 0, 1.0),   # d_model above 512 (dt_rank 33)
+                boa_hip.Config(0, 8, 16, 10, 0, 0, 1.0),     # d_model
+                boa_hip.Config(256, 0, 16, 10, 0, 0, 1.0),   # layers
                 boa_hip.Config(256, 8, 24, 10, 0, 0, 1.0),   # d_state
                 boa_hip.Config(256, 8, 16, 0, 0, 0, 1.0),    # lanes
                 boa_hip.Config(256, 8, 16, 10, 0, 2, 1.0)]:  # precision

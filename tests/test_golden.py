@@ -45,3 +45,31 @@ def test_oracle_reproduces_cdf_and_coder_vector(oracle):
     words = oracle.encode_cdf_stream(cdfs, syms)
     assert words.tolist() == v["words"]
     assert np.array_equal(oracle.decode_cdf_stream(cdfs, len(syms), words), syms)
+
+
+@pytest.mark.skipif(not __import__("refcpu").host_has_avx512(), reason="host has no AVX-512")
+def test_avx512_build_reproduces_the_fixtures(w_c1, weights_dir):
+    """The x86-64-v4 (AVX-512) build of the oracle, the timed CPU baseline on
+    hosts that have it, writes the same containers as the default build."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    names = sorted(MANIFEST["containers"])
+    code = (
+        "import hashlib, json, sys\n"
+        f"sys.path[:0] = [{os.path.join(root, 'oracle')!r}, {os.path.join(root, 'boa-constrictor_amd')!r}]\n"
+        "import refcpu, synth\n"
+        "assert refcpu.LIB_PATH.endswith('librefcpu_v4.so')\n"
+        f"man = json.load(open({os.path.join(GOLDEN, 'manifest.json')!r}))['containers']\n"
+        "out = {}\n"
+        f"for name in {names!r}:\n"
+        "    spec = man[name]\n"
+        f"    m = refcpu.Model({str(w_c1)!r}, 64, 2, bf16=spec['bf16'])\n"
+        "    blob = m.compress(synth.gen_c1()[:spec['n']], chunk_size=spec['chunk'], **spec['options'])\n"
+        "    out[name] = hashlib.sha256(blob).hexdigest()\n"
+        "print(json.dumps(out))\n")
+    env = dict(os.environ, REFCPU_ISA="v4")
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       timeout=300, check=True)
+    got = json.loads(r.stdout.strip().splitlines()[-1])
+    assert got == {n: MANIFEST["containers"][n]["sha256"] for n in names}

@@ -95,6 +95,8 @@ def test_cli_auto_batch(oracle, w_c1, tmp_path):
     assert "Auto-sizing: Selected Batch=" in r.stdout and "Timing (s): H2D=" in r.stdout
     assert out.read_bytes() == oracle.Model(w_c1, 64, 2).compress(data, chunk_size=1000)
     r = subprocess.run([exe, "decompress", str(w_c1), str(out), str(back), "64", "2",
-                        "--gpu-batch", "0"], check=True, timeout=120, capture_output=True, text=True)
+                        "--gpu-batch", "0", "--kernel-timings"], check=True, timeout=120,
+                       capture_output=True, text=True)
     assert "Auto-sizing: Selected Batch=" in r.stdout
+    assert "(profiled run" in r.stdout and "Kernel time (s): Forward=" in r.stdout
     assert back.read_bytes() == data

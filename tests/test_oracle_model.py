@@ -69,10 +69,12 @@ def np_forward(tensors, tokens, d, L, ds):
 
 
 @pytest.mark.parametrize("d,L,ds", [(64, 2, 16), (32, 1, 32), (80, 1, 16), (256, 2, 16),
-                                    (512, 1, 32)])
+                                    (512, 1, 32), (100, 1, 16), (37, 1, 16), (200, 1, 32)])
 def test_forward_matches_float64_restatement(oracle, weights_dir, d, L, ds):
     """Up to C2's width (K = 1024 in FF2) and C5's (d_model 512, d_state 32,
-    K = 2048), and d_model 80 (dt_rank 5, rows not a multiple of 32)."""
+    K = 2048), d_model 80 (dt_rank 5, rows not a multiple of 32), and widths
+    between the GPU kernels' built widths (100, 37 and 200, which the GPU runs
+    zero-padded to 128, 64 and 256)."""
     tensors = synth.random_weight_tensors(d, L, ds, seed=1)
     path = weights_dir / f"np_{d}_{L}_{ds}.bin"
     synth.write_weights(str(path), tensors)

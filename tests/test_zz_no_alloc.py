@@ -2,7 +2,10 @@
 the library's fixed per-GPU scratch array) gives the bits of
 boa_forward_chunk, through the C ABI, on two calls in a row -- the second
 smaller, so it runs on what the first left in the array -- and rejects a
-request beyond the array's limit with BOA_E_ARG."""
+request beyond the array's limit with BOA_E_ARG.  On a fresh context (no
+activation buffers allocated yet) it is captured into a HIP graph in global
+capture mode, where any device allocation would fail the capture, and the
+graph's replays give boa_forward_chunk's bits."""
 import ctypes
 
 import numpy as np
@@ -73,3 +76,72 @@ def test_noalloc_rejects_rows_beyond_the_scratch(make_weights):
         assert b"exceeds" in lib.boa_last_error(h)
     finally:
         lib.boa_destroy(h)
+
+
+def _hip():
+    h = ctypes.CDLL("libamdhip64.so")
+    vp, P = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+    for name, args in [("hipStreamCreateWithFlags", [P, ctypes.c_uint]),
+                       ("hipStreamBeginCapture", [vp, ctypes.c_int]),
+                       ("hipStreamEndCapture", [vp, P]),
+                       ("hipGraphInstantiate", [P, vp, vp, vp, ctypes.c_size_t]),
+                       ("hipGraphLaunch", [vp, vp]), ("hipStreamSynchronize", [vp]),
+                       ("hipGraphExecDestroy", [vp]), ("hipGraphDestroy", [vp]),
+                       ("hipStreamDestroy", [vp])]:
+        getattr(h, name).argtypes = args
+        getattr(h, name).restype = ctypes.c_int
+    return h
+
+
+def test_noalloc_captured_in_a_graph_on_a_fresh_context(make_weights):
+    import torch
+    assert torch.cuda.is_available()
+    lib, hip = boa_hip.lib(), _hip()
+    w = make_weights(256, 2)
+    cfg = boa_hip.Config(256, 2, 16, 64, 0, 0, 1.0)
+    h = ctypes.c_void_p()
+    assert lib.boa_create(ctypes.byref(cfg), ctypes.byref(h)) == 0
+    stream, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    try:
+        assert hip.hipStreamCreateWithFlags(ctypes.byref(stream), 1) == 0  # non-blocking
+        assert lib.boa_set_stream(h, stream) == 0
+        assert lib.boa_load_weights(h, str(w).encode()) == 0
+        lanes, T = 12, 70
+        tok = np.random.default_rng(5).integers(0, 256, size=(lanes, T), dtype=np.uint8)
+        d_tok = torch.from_numpy(tok).cuda()
+        d_log = torch.full((lanes * T * 256,), float("nan"), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        assert lib.boa_reset_state(h, lanes) == 0
+        assert hip.hipStreamSynchronize(stream) == 0
+        # capture the first forward this context runs: it must neither
+        # allocate nor synchronise
+        assert hip.hipStreamBeginCapture(stream, 0) == 0  # hipStreamCaptureModeGlobal
+        rc = lib.boa_forward_chunk_noalloc(h, ctypes.c_void_p(d_tok.data_ptr()), lanes, T,
+                                           ctypes.c_void_p(d_log.data_ptr()))
+        ec = hip.hipStreamEndCapture(stream, ctypes.byref(graph))
+        assert rc == 0, lib.boa_last_error(h)
+        assert ec == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        # the eager reference afterwards, on the same context
+        d_want = torch.empty_like(d_log)
+        assert lib.boa_reset_state(h, lanes) == 0
+        assert lib.boa_forward_chunk(h, ctypes.c_void_p(d_tok.data_ptr()), lanes, T,
+                                     ctypes.c_void_p(d_want.data_ptr())) == 0
+        assert hip.hipStreamSynchronize(stream) == 0
+        want = d_want.cpu().numpy()
+        for _ in range(3):  # replays, with eager work and synchronisations between
+            d_log.fill_(float("nan"))
+            torch.cuda.synchronize()
+            assert lib.boa_reset_state(h, lanes) == 0
+            assert hip.hipGraphLaunch(exe, stream) == 0
+            assert hip.hipStreamSynchronize(stream) == 0
+            got = d_log.cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    finally:
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        lib.boa_destroy(h)
+        if stream.value:
+            hip.hipStreamDestroy(stream)
