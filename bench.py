@@ -180,6 +180,36 @@ def decode_step_profile(codec, lanes: int, steps: int = 32) -> dict:
                     work_per_step=v["work"] / steps) for k, v in p.items() if v["launches"]}
 
 
+def decode_coder_profile(codec, torch, data: bytes, chunk: int, n_chunks: int, steps: int = 64):
+    """Per-launch time of the decode coder step (the CDF, the symbol search
+    and the coder advance; head.2 fused in where the plan fuses it) from a
+    profiled decompress of the first `steps` + 1 bytes of every chunk, at the
+    config's lane count: one launch per step, HIP events in each dispatch."""
+    probe = b"".join(data[c * chunk: c * chunk + steps + 1] for c in range(n_chunks))
+    blob = codec.compress(probe, chunk_size=steps + 1)
+    torch.cuda.synchronize()
+    codec.profile(True)
+    codec.profile_reset()
+    back = codec.decompress(blob)
+    torch.cuda.synchronize()
+    p = codec.profile_read()
+    codec.profile(False)
+    assert back == probe, "decode coder probe round trip failed"
+    return p["decode"]
+
+
+# Compiled VALU instructions per element (token x channel) of the compress
+# scan's token loop (scan_chunk_sload_kernel, the large-grid form), counted
+# from this build's gfx950 assembly (hipcc --cuda-device-only -S of mamba.hip;
+# instructions between the loop header and its back branch, one token per
+# iteration): fp32 d_state 16 (the reference's rounding, software exp2) and
+# bf16 (hardware exp; the fused update at d_state 16).
+SCAN_VALU_PER_ELEMENT = {("fp32", 16): 409, ("fp32", 32): 713, ("bf16", 16): 134, ("bf16", 32): 323}
+# MI355X's published fp32 vector peak, 157.3 TFLOP/s, as wave64 FMA
+# instructions per second (64 lanes x 2 FLOP): 1,228.8 G/s
+VALU_ISSUE_PEAK = 157.3e12 / 128
+
+
 def gpu_hold(torch, ms: float = 60.0):
     """Queue a GPU-side busy wait of about `ms` on the current stream."""
     torch.cuda._sleep(int(ms * 1e-3 * 2.4e9))
@@ -431,6 +461,14 @@ def main() -> int:
                 n_l = v["launches_per_step"]
                 dec_cls[k] = dict(avg_us=v["us_per_step"] / n_l, launches_per_step=n_l,
                                   work_per_launch=v["work_per_step"] / n_l)
+            log("decode coder-step profile (64 profiled decompress steps)")
+            dc = decode_coder_profile(codec, torch, data, chunk, n_chunks)
+            # the unfused coder step reads each lane's 1 KB logits row; with
+            # head.2 fused in (from 2048 lanes) its work is counted in FLOP
+            if dc["launches"] and not plan["fused_head"]:
+                dec_cls["decode"] = dict(avg_us=dc["ms"] * 1e3 / dc["launches"], launches_per_step=1,
+                                         work_per_launch=dc["work"] / dc["launches"])
+                dec["kernel_us_per_step"]["decode"] = round(dec_cls["decode"]["avg_us"], 2)
 
     # Rooflines of the kernels that take most of a round trip; `roofline`
     # is the one with the largest total time per step (compress: its
@@ -458,22 +496,43 @@ def main() -> int:
     add("compress GEMM", GEMM_KERNEL[prec], "mfma", g["work"] / max(g["launches"], 1),
         gemm_launch_us, g["launches"], peak_mm,
         traffic=gemm_traffic_bytes() if workload == "c2" else None)
-    add("compress scan", scan_kernel, "hbm", sc["work"] / max(sc["launches"], 1),
-        sc["ms"] * 1e3 / max(sc["launches"], 1), sc["launches"], None)
-    hc, cd_ = prof["head_cdf"], prof["cdf"]
+    scan_us = sc["ms"] * 1e3 / max(sc["launches"], 1)
+    scan_extra = {}
+    vpe = SCAN_VALU_PER_ELEMENT.get((prec, ds), 0)
+    if vpe and sc["launches"] and "sload" in scan_kernel:
+        # the scan's other bound: VALU issue.  Elements per launch from the
+        # algorithmic bytes (4 (3 di + R) per row in fp32, 2 (3 di) + 2 R in bf16)
+        rows = sc["work"] / sc["launches"] / ((4 if prec == "fp32" else 2) * (3 * 2 * d + r_dt + 2 * ds))
+        wi = rows * 2 * d * vpe / 64 / (scan_us * 1e-6)
+        scan_extra["valu"] = {"bound": "valu issue", "instr_per_element": vpe,
+                              "achieved_g_wave_instr_s": round(wi / 1e9, 1),
+                              "peak_g_wave_instr_s": round(VALU_ISSUE_PEAK / 1e9, 1),
+                              "frac": round(wi / VALU_ISSUE_PEAK, 3),
+                              "note": "instr_per_element counted from the compiled loop; peak "
+                                      "= the published fp32 vector peak (157.3 TFLOP/s) in wave64 "
+                                      "FMA instructions"}
+    add("compress scan", scan_kernel, "hbm", sc["work"] / max(sc["launches"], 1), scan_us,
+        sc["launches"], None, **scan_extra)
+    hc = prof["head_cdf"]
     if hc["launches"]:
-        add("compress head.2 + CDF", "boa::gemm_f32_kernel<64, 256, 4, 4, 16, 3> (head.2 with the "
-            "CDF epilogue)", "mfma", hc["work"] / hc["launches"], hc["ms"] * 1e3 / hc["launches"],
-            hc["launches"], peak_mm)
-    if cd_["launches"]:
-        add("compress CDF", "boa::cdf_targets_kernel", "hbm", cd_["work"] / cd_["launches"],
-            cd_["ms"] * 1e3 / cd_["launches"], cd_["launches"], None)
+        hk = ("boa::gemm_f32_kernel<64, 256, 4, 4, 16, 3>" if prec == "fp32" else
+              "boa::gemm_bf16_kernel<256, 256, 4, 4, 64, 1|2, 3>")
+        add("compress head.2 + CDF", hk + " (head.2 with the CDF epilogue)", "mfma",
+            hc["work"] / hc["launches"], hc["ms"] * 1e3 / hc["launches"], hc["launches"], peak_mm)
+    co = prof["coder"]
+    if co["launches"]:
+        # range encoder (8 B of (low, prob) per symbol read, compressed words
+        # written) and the payload compaction (words read and written)
+        add("compress coder", "boa::rc_encode_tile_kernel + boa::compact_kernel", "hbm",
+            co["work"] / co["launches"], co["ms"] * 1e3 / co["launches"], co["launches"], None)
     kn = {"dec_lngemm": ("decode LayerNorm GEMMs", "boa::dec_ln_gemm_kernel<1|2, d/16, *> "
                          "(LN1 + in_proj + conv, LN2 + FF1 + GELU)", "mfma"),
           "dec_gemm": ("decode GEMMs", "boa::dec_gemm_kernel / dec_b16_gemm* (x_proj, out_proj, "
                        "FF2, heads)", "mfma"),
           "dec_scan": ("decode scan", "boa::dec_xscan_kernel / dec_scan_kernel / dec_b16_scan_kernel",
-                       "hbm")}
+                       "hbm"),
+          "decode": ("decode coder step", "boa::decode_step_kernel (CDF, search, coder advance) / "
+                     "dec_head_step_kernel (head.2 fused in)", "hbm")}
     c2_lanes = args.config == "c2" and not args.warm_start and n_chunks == 1000
     for k, (name, kernel, bound) in kn.items():
         if k in dec_cls:

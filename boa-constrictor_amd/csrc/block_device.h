@@ -121,7 +121,23 @@ __device__ __forceinline__ void scan_store(const ScanCtx<DS, RB>& sc, float* ssm
 // The update rounds every product and sum on its own, as the reference's
 // __fmul_rn / __fadd_rn lines do (mamba_kernels.cu:332-335, 453-461):
 // dB = dt B_n, h_n = (dA h_n) + (dB u), y = y + (h_n C_n); the build's
-// -ffp-contract=off keeps the compiler from fusing them.
+// -ffp-contract=off keeps the compiler from fusing them.  The bf16 precision
+// (M = MATH_HW, hardware transcendentals, results within the bf16
+// tolerance of the oracle rather than bit-equal) takes the fused form
+// h_n = fma(dA, h_n, B_n (dt u)), y = fma(h_n, C_n, y): three VALU
+// operations fewer per state; compress and decode both run this function,
+// so their bits still agree.
+// The fused form at d_state 16 only: at d_state 32 its compress scan needs
+// 140 VGPRs (three waves per SIMD) against 127 unfused (four), and measured
+// slower on the C5 probe (compress scan 937 against 836 ms; capped at four
+// waves it spills, 1126 ms), while its decode scan was 4 % faster.
+#ifndef BOA_SCAN_B16_FUSED_DS32
+#define BOA_SCAN_B16_FUSED_DS32 0
+#endif
+template <int DS, int M>
+constexpr bool scan_fused_update() {
+  return M == MATH_HW && (DS == 16 || BOA_SCAN_B16_FUSED_DS32);
+}
 template <int DS, int RB, int M = MATH_BF>
 __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt_in,
                                             const float* bc, int r, float u, float z) {
@@ -133,12 +149,22 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
   const float* Bv = bc;
   const float* Cv = bc + DS;
   float y = 0.0f;
+  if constexpr (scan_fused_update<DS, M>()) {
+    const float dtu = dt * u;
 #pragma unroll
-  for (int n = 0; n < DS; ++n) {
-    const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
-    const float dB = dt * Bv[n];
-    sc.h[n] = dA * sc.h[n] + dB * u;
-    y = y + sc.h[n] * Cv[n];
+    for (int n = 0; n < DS; ++n) {
+      const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
+      sc.h[n] = __builtin_fmaf(dA, sc.h[n], Bv[n] * dtu);
+      y = __builtin_fmaf(sc.h[n], Cv[n], y);
+    }
+  } else {
+#pragma unroll
+    for (int n = 0; n < DS; ++n) {
+      const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
+      const float dB = dt * Bv[n];
+      sc.h[n] = dA * sc.h[n] + dB * u;
+      y = y + sc.h[n] * Cv[n];
+    }
   }
   y = y + sc.dd * u;
   float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));

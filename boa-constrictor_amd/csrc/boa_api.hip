@@ -110,7 +110,7 @@ struct boa_ctx {
   // activations
   int64_t rows_cap = 0;
   float *x = nullptr, *xn = nullptr, *xz = nullptr, *cv = nullptr, *delta = nullptr, *y = nullptr,
-        *hid = nullptr, *logits = nullptr;
+        *hid = nullptr;
   uint2* lowprob = nullptr;
   // compress: tile k's (low, prob) pairs are coded on enc_stream while tile
   // k + 1's forward pass runs on the caller's stream; the two buffers
@@ -288,8 +288,10 @@ Dims make_dims(const boa_config& cfg) {
   return D;
 }
 
+// compress activation bytes per row: x, xn, xz, conv, delta, y, hidden
+// (floats) and the two (low, prob) buffers
 int64_t row_bytes(const Dims& D) {
-  return 4 * (int64_t)(D.d + D.d + 2 * D.di + D.di + D.R + D.di + 4 * D.d + VOCAB) + 8;
+  return 4 * (int64_t)(D.d + D.d + 2 * D.di + D.di + D.R + D.di + 4 * D.d) + 16;
 }
 
 int64_t pitch_words_for(int64_t chunk) { return (chunk * 10 + 4096 + 3) / 4; }
@@ -298,12 +300,12 @@ int ensure_rows(boa_ctx* c, int64_t rows) {
   if (rows <= c->rows_cap) return BOA_OK;
   const Dims& D = c->D;
   dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
-  dfree(c->hid); dfree(c->logits); dfree(c->lowprob); dfree(c->lowprob_alt);
+  dfree(c->hid); dfree(c->lowprob); dfree(c->lowprob_alt);
   c->rows_cap = 0;
   size_t r = (size_t)rows;
   if (dalloc(&c->x, r * D.d) || dalloc(&c->xn, r * D.d) || dalloc(&c->xz, r * 2 * D.di) ||
       dalloc(&c->cv, r * D.di) || dalloc(&c->delta, r * D.R) || dalloc(&c->y, r * D.di) ||
-      dalloc(&c->hid, r * 4 * D.d) || dalloc(&c->logits, r * VOCAB) || dalloc(&c->lowprob, r) ||
+      dalloc(&c->hid, r * 4 * D.d) || dalloc(&c->lowprob, r) ||
       dalloc(&c->lowprob_alt, r))
     return fail(c, BOA_E_NOMEM, "device allocation of activation buffers failed");
   c->rows_cap = rows;
@@ -540,13 +542,24 @@ hipError_t forward_tile(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t
   return e ? e : head_forward(c, lanes * T, true, logits);
 }
 
-// A compress tile up to the coder's input (fp32): the blocks, head.1, then
-// head.2 fused with the CDF, which writes each row's (low, prob) of the next
-// byte to c->lowprob without storing the logits.
+// A compress tile up to the coder's input: the blocks, head.1, then head.2
+// fused with the CDF, which writes each row's (low, prob) of the next byte to
+// c->lowprob without storing the logits.
 hipError_t forward_tile_cdf(boa_ctx* c, const TokenSrc& tok, int lanes, int T, int t0) {
   const Dims& D = c->D;
   const int rows = lanes * T;
   hipError_t e = blocks_forward(c, tok, lanes, T, t0);
+  if (c->bf16) {  // head1 reads the bf16 copy of x stored in y's buffer
+    if (!e)
+      e = gemmb(c, c->y, c->b16c_h1, c->xn, D.d, true, nullptr, c->hb1, nullptr, 0, rows, D.d,
+                D.d, ACT_RELU);
+    if (e) return e;
+    GemmB16Args a{(const uint16_t*)c->xn, D.d, c->b16c_h2, D.d, nullptr, 0, 0, nullptr, c->hb2,
+                  nullptr, 0, rows, VOCAB, D.d, ACT_NONE};
+    CdfEpi ce{tok.base, tok.stride, tok.total, tok.len, T, t0, c->inv_temp, c->lowprob};
+    return timed(c, BOA_K_HEAD_CDF, 2.0 * rows * VOCAB * D.d,
+                 [&] { return gemm_bf16_head_cdf(a, ce, c->stream); });
+  }
   if (!e)
     e = gemm(c, c->x, D.d, c->hw1, D.ld_h1, c->xn, D.d, c->hb1, nullptr, 0, rows, D.d, D.d,
              ACT_RELU);
@@ -1117,7 +1130,7 @@ void boa_destroy(boa_ctx* c) {
   dfree(c->dyt); dfree(c->dhidt); dfree(c->dlogits);
   dfree(c->x); dfree(c->xn); dfree(c->xz); dfree(c->cv); dfree(c->delta); dfree(c->y);
   if (c->enc_stream) (void)hipStreamSynchronize(c->enc_stream);
-  dfree(c->hid); dfree(c->logits); dfree(c->lowprob); dfree(c->lowprob_alt);
+  dfree(c->hid); dfree(c->lowprob); dfree(c->lowprob_alt);
   dfree(c->words); dfree(c->enc); dfree(c->dec); dfree(c->sizes); dfree(c->offsets);
   dfree(c->lens); dfree(c->tok); dfree(c->t_counter);
   if (c->h_sizes) (void)hipHostFree(c->h_sizes);
@@ -1653,16 +1666,7 @@ int boa_compress_device(boa_ctx* c, const uint8_t* d_data, int64_t n, int64_t ch
         // the coder of tile k - 2 has finished reading this tile's buffer
         if (k >= 2) e = hipStreamWaitEvent(s, c->lp_free[k & 1], 0);
         if (e) return fail_coding(e, "compress tile");
-        if (c->bf16) {  // bf16: head.2 stores the logits, the CDF kernel reads them
-          e = forward_tile(c, tok, lanes, Tt, (int)t0, c->logits);
-          if (!e)
-            e = timed(c, BOA_K_CDF, 1032.0 * lanes * Tt, [&] {
-              return launch_cdf_encode_targets(c->logits, tok, Tt, (int)t0, lanes, c->inv_temp,
-                                               c->lowprob, s);
-            });
-        } else {
-          e = forward_tile_cdf(c, tok, lanes, Tt, (int)t0);
-        }
+        e = forward_tile_cdf(c, tok, lanes, Tt, (int)t0);
         if (!e) e = hipEventRecord(c->lp_ready[k & 1], s);
         if (!e) e = hipStreamWaitEvent(c->enc_stream, c->lp_ready[k & 1], 0);
         if (!e)

@@ -147,6 +147,10 @@ struct GemmB16Args {
   int M, N, K, act;
 };
 hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s);
+// head.2 of the bf16 compress pass (N = 256, act none, bias = head.2's)
+// fused with the CDF: each row's (low, prob) of the next byte goes to
+// cdf.lowprob and the logits are not stored (C unused)
+hipError_t gemm_bf16_head_cdf(const GemmB16Args& a, const CdfEpi& cdf, hipStream_t s);
 // FF1 + GELU + FF2 (+ b2 + residual) of the bf16 compress pass in one kernel:
 // X bf16 [M][D] (LN2's output), W1 bf16 [4D][D], W2 bf16 [D][4D] (the
 // gemm_bf16 layouts), res and C fp32 [M][D] (may alias), C2 an optional bf16
@@ -312,8 +316,6 @@ hipError_t launch_state_relayout(const float* conv_in, const float* ssm_in, floa
                                  bool to_step, bool conv_b16, hipStream_t s);
 
 // CDF + coder kernels.
-hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,
-                                     float inv_temp, uint2* lowprob, hipStream_t s);
 hipError_t launch_rc_enc_init(RcEnc* st, int lanes, hipStream_t s);
 hipError_t launch_rc_encode_tile(const uint2* lowprob, TokenSrc tok, int T, int t0, int lanes,
                                  RcEnc* st, uint32_t* out, int64_t pitch_words, hipStream_t s);

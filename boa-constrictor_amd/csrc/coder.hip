@@ -20,41 +20,6 @@
 
 namespace boa {
 
-__device__ __forceinline__ uint32_t token_at(const TokenSrc& tok, int lane, int64_t pos_in_chunk) {
-  const int64_t pos = (int64_t)lane * tok.stride + pos_in_chunk;
-  return (pos_in_chunk < tok.len && pos < tok.total) ? tok.base[pos] : 0u;
-}
-
-// (low, prob) of the next byte for every row (lane b, position t0+t) of a
-// tile.  8 rows per 256-thread block; the two entries a row needs are
-// shuffled out of the registers that hold its cumulative sums.
-__global__ __launch_bounds__(256) void cdf_targets_kernel(const float* __restrict__ logits,
-                                                          TokenSrc tok, int T, int t0, int rows,
-                                                          float inv_t, uint2* lowprob) {
-  const int half = threadIdx.x >> 5, l = threadIdx.x & 31;
-  const int row = blockIdx.x * 8 + half;
-  const int rr = row < rows ? row : rows - 1;
-  double r[8];
-  cdf_halfwave_regs(logits + (size_t)rr * 256, nullptr, inv_t, l, r);
-  const int b = rr / T, t = rr % T;
-  const int sym = (int)token_at(tok, b, (int64_t)t0 + t + 1);
-  const double c_lo = cdf_entry(r, sym);
-  const double c_hi = cdf_entry(r, sym + 1 > 255 ? 255 : sym + 1);
-  if (row < rows && l == 0) {
-    const uint32_t lo = (uint32_t)(c_lo * CDF_SCALE) + (uint32_t)sym;
-    const uint32_t hi = sym == 255 ? TOTAL : (uint32_t)(c_hi * CDF_SCALE) + (uint32_t)(sym + 1);
-    lowprob[row] = make_uint2(lo, hi - lo);
-  }
-}
-
-hipError_t launch_cdf_encode_targets(const float* logits, TokenSrc tok, int T, int t0, int lanes,
-                                     float inv_temp, uint2* lowprob, hipStream_t s) {
-  const int rows = lanes * T;
-  BOA_LAUNCH(cdf_targets_kernel, dim3((rows + 7) / 8), dim3(256), 0, s, logits, tok, T, t0,
-                     rows, inv_temp, lowprob);
-  return hipGetLastError();
-}
-
 __global__ __launch_bounds__(256) void cdf_rows_kernel(const float* __restrict__ logits,
                                                        const float* __restrict__ bias, float inv_t,
                                                        int rows, uint32_t* qcdf) {

@@ -208,6 +208,29 @@ __device__ __forceinline__ double cdf_entry(const double (&r)[8], int k) {
   return __shfl(mine, k >> 3, 32);
 }
 
+// The coder's (low, prob) of the byte that follows row `row` of a compress
+// tile (row = lane b x T + t, position t0 + t of lane b's chunk; past the
+// chunk's end the byte is 0), from the row's logits lg (bias already added),
+// run by the row's half-wave (lane l) in the fused head.2 + CDF GEMM
+// epilogues.  Rows at or past M store nothing.
+__device__ __forceinline__ void cdf_row_lowprob(const float* lg, const CdfEpi& c, int row, int M,
+                                                int l) {
+  const int rr = row < M ? row : M - 1;
+  double cr[8];
+  cdf_halfwave_regs(lg, nullptr, c.inv_t, l, cr);
+  const int b = rr / c.T, t = rr % c.T;
+  const int64_t pic = (int64_t)c.t0 + t + 1;
+  const int64_t pos = (int64_t)b * c.tok_stride + pic;
+  const int sym = (pic < c.tok_len && pos < c.tok_total) ? c.tok_base[pos] : 0;
+  const double c_lo = cdf_entry(cr, sym);
+  const double c_hi = cdf_entry(cr, sym + 1 > 255 ? 255 : sym + 1);
+  if (row < M && l == 0) {
+    const uint32_t lo = (uint32_t)(c_lo * CDF_SCALE) + (uint32_t)sym;
+    const uint32_t hi = sym == 255 ? TOTAL : (uint32_t)(c_hi * CDF_SCALE) + (uint32_t)(sym + 1);
+    c.lowprob[row] = make_uint2(lo, hi - lo);
+  }
+}
+
 __device__ __forceinline__ uint32_t q_low(const double* s_cdf, int k) {
   return (uint32_t)(s_cdf[k] * CDF_SCALE) + (uint32_t)k;
 }

@@ -17,10 +17,17 @@
 // consecutive n of one row m.  LDS: [rows][BK + 8] u16 per operand (the pad
 // staggers 16-byte row reads across banks), double-buffered.
 #include "boa_kernels.h"
+#include "coder_device.h"
 
 namespace boa {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Epilogue mode of head.2 fused with the CDF (not a user activation): the
+// block's logits rows pass through LDS 64 at a time and each row's (low,
+// prob) pair of the next input byte is computed there (cdf_row_lowprob); the
+// logits never reach memory.
+constexpr int ACT_CDF = 3;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -84,7 +91,8 @@ __device__ __forceinline__ void b16_epilogue(const GemmB16Args& a, const floatx4
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int BK, int NBUF, int ACT>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB16Args a,
-                                                                           int swizzle) {
+                                                                           int swizzle,
+                                                                           CdfEpi cdf) {
   constexpr int NT = 64 * WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -94,9 +102,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
   static_assert(BK % 32 == 0, "BK must be a multiple of the MFMA k-step");
   // NBUF = 1 keeps one LDS stage (the next k-tile waits in registers), so
   // two workgroups fit in a CU's LDS and one's epilogue overlaps the
-  // other's main loop.
-  __shared__ __attribute__((aligned(16))) uint16_t xs[NBUF][BM * S];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[NBUF][BN * S];
+  // other's main loop.  The CDF epilogue reuses the words for 64 logits
+  // rows of LS floats.
+  constexpr int LS = BN + 4;
+  constexpr int MAIN_B = NBUF * (BM + BN) * S * 2;
+  constexpr int EPI_B = ACT == ACT_CDF ? 64 * LS * 4 : 0;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[(MAIN_B > EPI_B ? MAIN_B : EPI_B) / 2];
+  uint16_t(*xs)[BM * S] = reinterpret_cast<uint16_t(*)[BM * S]>(smem);
+  uint16_t(*ws)[BN * S] = reinterpret_cast<uint16_t(*)[BN * S]>(smem + NBUF * BM * S);
   __shared__ float sbias[BN];  // the block's bias values, for the epilogue
 
   const int tid = threadIdx.x;
@@ -180,17 +193,54 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_bf16_kernel(GemmB
 #undef BOA_B16_LOAD
 #undef BOA_B16_STORE
 
+  if constexpr (ACT == ACT_CDF) {
+    // the logits rows, acc + bias as the unfused epilogue stores them,
+    // 64 rows (one wave row of the block) at a time; the K loop ended with
+    // a barrier, so its buffers are free
+    static_assert(BN == 256 && WM == 64, "whole logits rows, 64 per wave row");
+    float* lg = reinterpret_cast<float*>(smem);
+    const int hw = tid >> 5, l = tid & 31;
+    for (int h = 0; h < BM / 64; ++h) {
+      if (wm0 == 64 * h) {
+#pragma unroll
+        for (int p = 0; p < TM; ++p)
+#pragma unroll
+          for (int q = 0; q < TN; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int col = wn0 + 16 * q + 4 * g + e;
+              lg[(16 * p + j) * LS + col] = acc[p][q][e] + sbias[col];
+            }
+      }
+      __syncthreads();
+      for (int r = hw; r < 64; r += NT / 32)
+        cdf_row_lowprob(lg + r * LS, cdf, m_blk + 64 * h + r, a.M, l);
+      __syncthreads();  // the next 64 rows reuse the buffer
+    }
+    return;
+  }
   b16_epilogue<TM, TN, ACT>(a, acc, m_blk, n_blk, wm0, wn0, j, g, sbias);
 }
 
 template <int BM, int BN, int WM_, int WN_, int BK, int NBUF = 2>
-static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 1) {
+static hipError_t launch_b16(const GemmB16Args& a, hipStream_t s, int swizzle = 1,
+                             const CdfEpi* cdf = nullptr) {
   if (a.K % BK || a.ldx % 8 || a.ldw % 8 || a.ldw < a.K) return hipErrorInvalidValue;
   const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
   if (tiles >= (1ll << 31)) return hipErrorInvalidValue;
+  const CdfEpi ce = cdf ? *cdf : CdfEpi{};
 #define BOA_B16_GO(ACTv)                                                                  \
   BOA_LAUNCH((gemm_bf16_kernel<BM, BN, WM_, WN_, BK, NBUF, ACTv>), dim3((unsigned)tiles), \
-                     dim3(64 * WM_ * WN_), 0, s, a, swizzle)
+                     dim3(64 * WM_ * WN_), 0, s, a, swizzle, ce)
+  if (cdf) {
+    if constexpr (BN == 256 && BM / WM_ == 64) {
+      if (a.N != 256 || a.act != ACT_NONE) return hipErrorInvalidValue;
+      BOA_B16_GO(ACT_CDF);
+      return hipGetLastError();
+    } else {
+      return hipErrorInvalidValue;
+    }
+  }
   switch (a.act) {
     case ACT_NONE: BOA_B16_GO(ACT_NONE); break;
     case ACT_GELU: BOA_B16_GO(ACT_GELU); break;
@@ -213,6 +263,14 @@ hipError_t gemm_bf16(const GemmB16Args& a, hipStream_t s) {
   if (a.N >= 256 && (a.N >= 512 || a.K >= 512)) return launch_b16<256, 256, 4, 4, 64, 1>(a, s);
   if (a.N >= 256) return launch_b16<256, 256, 4, 4, 64>(a, s);
   return launch_b16<128, 64, 4, 2, 64>(a, s);
+}
+
+// head.2 (N = 256) fused with the CDF: the head GEMM's tile and stages, the
+// epilogue of ACT_CDF; writes cdf.lowprob instead of the logits
+hipError_t gemm_bf16_head_cdf(const GemmB16Args& a, const CdfEpi& cdf, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.K >= 512) return launch_b16<256, 256, 4, 4, 64, 1>(a, s, 1, &cdf);
+  return launch_b16<256, 256, 4, 4, 64>(a, s, 1, &cdf);
 }
 
 // ------------------------------------------------------ FF1 + GELU + FF2

@@ -27,7 +27,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Epilogue mode of head.2 fused with the CDF (not a user activation): the
 // block's logits rows go to LDS, and each row's (low, prob) pair of the
-// next input byte is computed there (cdf_targets_kernel's work).
+// next input byte is computed there (cdf_row_lowprob).
 constexpr int ACT_CDF = 3;
 // Epilogue modes of a 256-wide GEMM followed by a LayerNorm (see gemm_f32_ln).
 constexpr int ACT_LN1 = 4, ACT_LN2 = 5;
@@ -146,7 +146,7 @@ void gemm_f32_kernel(
 
   if constexpr (ACT == ACT_CDF) {
     // head.2 + bias into LDS (the K loop ended with a barrier, so the tile
-    // buffers are free), then per row the CDF of cdf_targets_kernel
+    // buffers are free), then per row the CDF (cdf_row_lowprob)
     static_assert(BN == 256, "one block holds whole logits rows");
 #pragma unroll
     for (int a = 0; a < TM; ++a)
@@ -159,24 +159,7 @@ void gemm_f32_kernel(
         }
     __syncthreads();
     const int hw = tid >> 5, l = tid & 31;
-    for (int r = hw; r < BM; r += NT / 32) {
-      const int row = m_blk + r;
-      const int rr = row < M ? row : M - 1;
-      double cr[8];
-      cdf_halfwave_regs(smem + r * LS, nullptr, cdf.inv_t, l, cr);
-      // the byte after position t0 + t of lane b (0 past the chunk's end)
-      const int b = rr / cdf.T, t = rr % cdf.T;
-      const int64_t pic = (int64_t)cdf.t0 + t + 1;
-      const int64_t pos = (int64_t)b * cdf.tok_stride + pic;
-      const int sym = (pic < cdf.tok_len && pos < cdf.tok_total) ? cdf.tok_base[pos] : 0;
-      const double c_lo = cdf_entry(cr, sym);
-      const double c_hi = cdf_entry(cr, sym + 1 > 255 ? 255 : sym + 1);
-      if (row < M && l == 0) {
-        const uint32_t lo = (uint32_t)(c_lo * CDF_SCALE) + (uint32_t)sym;
-        const uint32_t hi = sym == 255 ? TOTAL : (uint32_t)(c_hi * CDF_SCALE) + (uint32_t)(sym + 1);
-        cdf.lowprob[row] = make_uint2(lo, hi - lo);
-      }
-    }
+    for (int r = hw; r < BM; r += NT / 32) cdf_row_lowprob(smem + r * LS, cdf, m_blk + r, M, l);
     return;
   }
 

@@ -488,6 +488,8 @@ void scan_chunk_sload_kernel(Dims D, LayerW Lw, const TA* __restrict__ xz,
 //      h = (2^(na dt) h) + ((dt B) u), and leaves each token's h in LDS;
 //   3. thread (c, k) sums y = y + h_n C_n over n = 0 .. DS-1 in order for
 //      tokens k, k + 16, ..., adds D u, gates and stores.
+// (bf16 at d_state 16: the fused update of scan_token,
+// h = fma(2^(na dt), h, B (dt u)), y = fma(h_n, C_n, y).)
 // Every element sees scan_token's operations in scan_token's order, so the
 // bits are scan_chunk_sload_kernel's.  The per-token scalars are computed
 // once per channel and the recurrence's critical path per token is its fma.
@@ -602,7 +604,7 @@ __global__ __launch_bounds__(256) void scan_chunk_tblk_kernel(Dims D, LayerW Lw,
         const float dt = softplus<M>(acc + bdt);
         const float sg = rcp_sel<M>(1.0f + exp_sel<M>(-cz[i]));
         *reinterpret_cast<float4*>(s_tok + 4 * tok) =
-            make_float4(dt, cu[i], dd * cu[i], cz[i] * sg);
+            make_float4(dt, scan_fused_update<DS, M>() ? dt * cu[i] : cu[i], dd * cu[i], cz[i] * sg);
       }
     }
     __syncthreads();
@@ -614,8 +616,12 @@ __global__ __launch_bounds__(256) void scan_chunk_tblk_kernel(Dims D, LayerW Lw,
 #pragma unroll
       for (int n = 0; n < SPT; ++n) {
         const float dA = exp2_neg_sel<M>(na[n] * dd2.x);
-        const float dB = dd2.x * Bv[SPT * k + n];
-        h[n] = dA * h[n] + dB * dd2.y;
+        if constexpr (scan_fused_update<DS, M>()) {  // dd2.y = dt u
+          h[n] = __builtin_fmaf(dA, h[n], Bv[SPT * k + n] * dd2.y);
+        } else {  // dd2.y = u
+          const float dB = dd2.x * Bv[SPT * k + n];
+          h[n] = dA * h[n] + dB * dd2.y;
+        }
         s_h[tt * HS + SPT * k + n] = h[n];
       }
     }
@@ -629,7 +635,8 @@ __global__ __launch_bounds__(256) void scan_chunk_tblk_kernel(Dims D, LayerW Lw,
         const float* hr = s_h + tok * HS;
         float yv = 0.0f;
 #pragma unroll
-        for (int n = 0; n < DS; ++n) yv = yv + hr[n] * Cv[n];
+        for (int n = 0; n < DS; ++n)
+          yv = scan_fused_update<DS, M>() ? __builtin_fmaf(hr[n], Cv[n], yv) : yv + hr[n] * Cv[n];
         const float4 tk = *reinterpret_cast<const float4*>(s_tok + 4 * tok);
         yv = yv + tk.z;
         stv(y + (row0 + t0 + tok) * di + c, yv * tk.w);
