@@ -269,6 +269,10 @@ def main() -> int:
                          "--gpu-batch B); not the metric config")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (counter calibration)")
+    ap.add_argument("--part", default="", metavar="I/N",
+                    help="round-trip only part I of N (0-based) of the config's chunks, a "
+                         "contiguous share at the config's chunk size; the timed step also "
+                         "carries the kernel profile (no second compress pass)")
     ap.add_argument("--decode-steps", type=int, default=0, metavar="N",
                     help="only run N directly launched decode steps of --config over its "
                          "lane count (the workload of the decode counter profiles)")
@@ -308,6 +312,17 @@ def main() -> int:
         chunk = args.chunk_len
         data = b"".join(data[c * full: c * full + chunk] for c in range(n_chunks))
         workload = f"{args.config}-probe-{chunk}B-chunks"
+    part = None
+    if args.part:
+        pi, pn = (int(v) for v in args.part.split("/"))
+        total = math.ceil(len(data) / chunk)
+        if not 0 <= pi < pn <= total:
+            print(f"bench.py: bad --part {args.part} for {total} chunks", file=sys.stderr)
+            return 2
+        c0, c1 = pi * total // pn, (pi + 1) * total // pn
+        data = data[c0 * chunk: c1 * chunk]
+        part = {"index": pi, "of": pn, "chunks": [c0, c1], "chunks_total": total}
+        workload += f"-part{pi}of{pn}"
     if args.warm_start:
         workload += f"-warm{args.warm_start}"
     n = len(data)
@@ -402,7 +417,10 @@ def main() -> int:
         left = args.budget_s - (time.perf_counter() - t_start) - reserve()
         if K > 0 and step_s and left < step_s * 1.05:
             break
-        tc, td, lens, ok, _ = step(profile=False)
+        # a part run profiles its one timed step instead of a second pass
+        tc, td, lens, ok, p_step = step(profile=part is not None and prof is None)
+        if p_step is not None:
+            prof = p_step
         K += 1
         step_s = tc + (0 if args.no_decompress else td)
         log(f"timed step {K}: compress {tc:.3f} s, decompress {td:.3f} s, round trip {ok}")
@@ -612,7 +630,8 @@ def main() -> int:
                    "chunks": n_chunks, "chunk_len": chunk, "input_bytes": n,
                    "precision": prec, "warm_start": args.warm_start,
                    "weights": "random-init seed 0",
-                   "input": f"synth.gen_{args.config}"},
+                   "input": f"synth.gen_{args.config}",
+                   **({"part": part} if part else {})},
         "compress_mb_s": round(comp_mb_s, 4),
         "decompress_mb_s": round(dec_mb_s, 4) if dec_mb_s else None,
         "value_span": "device-resident: input in HBM -> compacted payload in HBM (and back)",

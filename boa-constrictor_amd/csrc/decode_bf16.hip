@@ -168,7 +168,12 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_kernel(DecB16Args a) {
 // lanes x 16 TN features), so each operand fragment it loads feeds TN (or
 // TM) MFMAs; the k-steps of every tile run in the order of
 // dec_b16_gemm_kernel (the same bits).  Loads run two k-steps ahead.
-template <int KS, int TM, int TN>
+// CONV (in_proj): the conv state of the wave's tiles is loaded with the
+// first operands, so that its latency hides behind the K loop (C3 decode
+// GEMMs 841 -> 811 us per step; a deeper operand ring, 4 k-steps ahead,
+// measured the same, 2 x 4 tiles per wave slower).  The other GEMMs keep
+// the registers it takes.
+template <int KS, int TM, int TN, bool CONV>
 __global__ __launch_bounds__(256) void dec_b16_gemm_blk_kernel(DecB16Args a) {
   constexpr int R = (2 < KS ? 2 : KS - 1) + 1;  // ring size
   const int lane = threadIdx.x & 63;
@@ -200,6 +205,29 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_blk_kernel(DecB16Args a) {
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 0; p < R - 1; ++p) { BOA_B16_BLOAD(p, p) }
+  // in_proj's conv state of the wave's tiles, loaded with the first
+  // operands so that its latency hides behind the K loop
+  ushort4 csp[TM][TN][4];
+  const bool conv_w = CONV && n0 < a.conv_di;
+  if (conv_w) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int mm = min(m0 + 16 * tm + i, a.M - 1);
+        const int nb = n0 + 16 * tn + 4 * g;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const ushort4* st = reinterpret_cast<const ushort4*>(a.conv_state) + (size_t)(nb + e) * a.ld_state + mm;
+          if (a.state_cached) {
+            csp[tm][tn][e] = *st;
+          } else {
+            const stream_h4 h = __builtin_nontemporal_load(reinterpret_cast<const stream_h4*>(st));
+            csp[tm][tn][e] = make_ushort4(h[0], h[1], h[2], h[3]);
+          }
+        }
+      }
+  }
 #pragma unroll
   for (int st = 0; st < KS; ++st) {
     if (st + R - 1 < KS) { BOA_B16_BLOAD((st + R - 1) % R, st + R - 1) }
@@ -219,7 +247,8 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_blk_kernel(DecB16Args a) {
     for (int tn = 0; tn < TN; ++tn) {
       B16Pre pre;
       dec_b16_prefetch(a, n0 + 16 * tn, m0 + 16 * tm + i, g, pre);
-      dec_b16_epilogue(a, acc[tm][tn], n0 + 16 * tn, m0 + 16 * tm + i, g, pre);
+      dec_b16_epilogue(a, acc[tm][tn], n0 + 16 * tn, m0 + 16 * tm + i, g, pre,
+                       conv_w ? csp[tm][tn] : nullptr);
     }
 }
 
@@ -340,17 +369,17 @@ hipError_t dec_b16_lds_launch(const DecB16Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int TM, int TN>
+template <int TM, int TN, bool CONV>
 hipError_t dec_b16_blk_launch(const DecB16Args& a, hipStream_t s) {
   const int tiles = ((a.N + 16 * TN - 1) / (16 * TN)) * ((a.M + 16 * TM - 1) / (16 * TM));
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {
-    case 64: BOA_LAUNCH((dec_b16_gemm_blk_kernel<2, TM, TN>), grid, block, 0, s, a); break;
-    case 128: BOA_LAUNCH((dec_b16_gemm_blk_kernel<4, TM, TN>), grid, block, 0, s, a); break;
-    case 256: BOA_LAUNCH((dec_b16_gemm_blk_kernel<8, TM, TN>), grid, block, 0, s, a); break;
-    case 512: BOA_LAUNCH((dec_b16_gemm_blk_kernel<16, TM, TN>), grid, block, 0, s, a); break;
-    case 1024: BOA_LAUNCH((dec_b16_gemm_blk_kernel<32, TM, TN>), grid, block, 0, s, a); break;
-    case 2048: BOA_LAUNCH((dec_b16_gemm_blk_kernel<64, TM, TN>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_b16_gemm_blk_kernel<2, TM, TN, CONV>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_b16_gemm_blk_kernel<4, TM, TN, CONV>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_b16_gemm_blk_kernel<8, TM, TN, CONV>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_b16_gemm_blk_kernel<16, TM, TN, CONV>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_b16_gemm_blk_kernel<32, TM, TN, CONV>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_b16_gemm_blk_kernel<64, TM, TN, CONV>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -367,7 +396,10 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   // LDS-tiled blocks for K >= 512 (4.40 -> 4.54 MB/s at C3, 0.95 -> 0.98 at
   // C5; LDS tiles for in_proj and FF1 too were slower, the block's two
   // waves per SIMD exposing their conv and epilogue latency)
-  if (a.M >= 2048) return a.K >= 512 ? dec_b16_lds_launch(a, s) : dec_b16_blk_launch<2, 2>(a, s);
+  if (a.M >= 2048) {
+    if (a.K >= 512) return dec_b16_lds_launch(a, s);
+    return a.conv_di > 0 ? dec_b16_blk_launch<2, 2, true>(a, s) : dec_b16_blk_launch<2, 2, false>(a, s);
+  }
   const int tiles = ((a.N + 15) / 16) * ((a.M + 15) / 16);
   const dim3 grid((tiles + 3) / 4), block(256);
   switch (a.K) {
