@@ -77,10 +77,12 @@ def test_bf16_round_trip_and_ratio(torch_dev, oracle, make_weights, d, L, ds, ge
     assert abs(len(blob) / len(ref) - 1.0) < 5e-3, f"{len(blob)} vs oracle {len(ref)} bytes"
 
 
-@pytest.mark.parametrize("d,L,ds", [(64, 2, 16), (256, 1, 16)])
+@pytest.mark.parametrize("d,L,ds", [(64, 2, 16), (256, 1, 16), (512, 1, 32)])
 def test_bf16_many_lanes_step_equals_chunk_and_round_trip(torch_dev, make_weights, d, L, ds):
-    """From 2048 lanes on the bf16 decode GEMMs run 2 x 2 tiles per wave:
-    step logits stay bit-identical to chunk logits, and a container of 2101
+    """From 2048 lanes on the bf16 decode GEMMs run the many-lane forms (2 x 2
+    tiles per wave, 64 x 64 LDS blocks, and 128 x 128 LDS blocks for in_proj
+    and FF1 from d_model 128, a partial last block at 2100 lanes): step
+    logits stay bit-identical to chunk logits, and a container of 2101
     chunks (one decode batch) round-trips byte for byte."""
     torch = torch_dev
     w = make_weights(d, L, ds)
