@@ -80,6 +80,51 @@ __device__ __forceinline__ size_t dblk32(int k, int m, int ld) {
   return ((size_t)(k >> 5) * ld + m) * 32 + (k & 31);
 }
 
+// Staged-operand pipelines fed by direct-to-LDS copies (global_load_lds):
+// the compiler counts such a copy as an LDS write and waits for every copy
+// in flight (vmcnt(0)) before any LDS read it emits, and __syncthreads()
+// waits for them too; both would drain the pipeline every stage.  These
+// reads and this barrier are outside its view: the caller waits for the
+// copies it needs (s_waitcnt vmcnt(n)) before lds_barrier, and for its reads
+// with lds_wait4 before using them.
+typedef uint32_t lds_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ lds_u32x4 lds_read128(const void* p) {
+  lds_u32x4 v;
+  const uint32_t a = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// the reads' values are the asm's outputs, so nothing uses them before it
+__device__ __forceinline__ void lds_wait8(lds_u32x4& a, lds_u32x4& b, lds_u32x4& c, lds_u32x4& d,
+                                          lds_u32x4& e, lds_u32x4& f, lds_u32x4& g, lds_u32x4& h) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g), "+v"(h)::"memory");
+}
+// s_waitcnt vmcnt(n) for the n a staged loop allows (its immediates)
+__device__ __forceinline__ void vm_wait(int n) {
+  switch (n) {
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+}
+
+// (lane block, feature block) of 128 x 128 GEMM block b.  Workgroups go to
+// the eight XCDs round-robin (b % 8); when the lane blocks divide by eight,
+// XCD x takes lane blocks x, x + 8, ... with every feature block, so that
+// each XCD's L2 holds an eighth of the activations and in_proj's conv
+// blocks (the first feature blocks) spread over every XCD instead of
+// landing on XCDs 0-3.
+__device__ __forceinline__ int2 t128_block(int b, int m_blocks, int n_blocks) {
+  if (m_blocks % 8) return make_int2(b / n_blocks, b % n_blocks);
+  const int x = b & 7, k = b >> 3;
+  return make_int2(8 * (k / n_blocks) + x, k % n_blocks);
+}
+
 constexpr int RMAX = 32;  // dt_rank <= 32 (d_model <= 512)
 
 template <int DS, int RB>

@@ -364,11 +364,13 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_lds_kernel(DecB16Args a) {
 // keeps its texture-address units busy half its time).  A stage's 8 KB tile
 // of one operand holds row r's 16-byte quarter q at position
 // q ^ ((r >> 2) & 3), so that the 16 lanes of a ds_read_b128 pass read 16
-// distinct bank groups.  Every tile's k-steps run in the order of
-// dec_b16_gemm_kernel (the same bits).  The epilogue walks the tiles a
-// feature column at a time, loading the column's bias (and in_proj's conv
-// taps) once; in_proj loads column tn + 1's conv state while column tn is
-// computed.
+// distinct bank groups.  The stage's reads and barrier bypass the
+// compiler's waits (lds_read128, lds_barrier: its own would wait for every
+// copy in flight).  Blocks map to XCDs by t128_block.  Every tile's k-steps
+// run in the order of dec_b16_gemm_kernel (the same bits).  The epilogue
+// walks the tiles a feature column at a time, loading the column's bias
+// (and in_proj's conv taps) once; in_proj loads column tn + 1's conv state
+// while column tn is computed.
 constexpr int T128_RING = 4;  // LDS stages; T128_RING - 1 in flight
 
 template <int KS, bool CONV>
@@ -379,8 +381,8 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
   __shared__ __align__(16) u32x4 sm[NR][2][128 * 4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
-  const int n_blocks = (a.N + 127) / 128;
-  const int m0 = (blockIdx.x / n_blocks) * 128, n0 = (blockIdx.x % n_blocks) * 128;
+  const int2 mn = t128_block(blockIdx.x, (a.M + 127) / 128, (a.N + 127) / 128);
+  const int m0 = mn.x * 128, n0 = mn.y * 128;
   const u32x4* X4 = reinterpret_cast<const u32x4*>(a.X);
   const u32x4* W4 = reinterpret_cast<const u32x4*>(a.W);
   // DMA of k-step s: wave wv issues instructions 4 wv .. 4 wv + 3 of the
@@ -414,20 +416,18 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
     // this wave's copies of stage st have landed (the younger in-flight
     // stages, four instructions each, may still run); after the barrier
     // every wave's have, and every wave is done with stage st - 1's buffer
-    const int younger = min(PF - 1, KS - 1 - st);
-    if (younger >= 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (younger == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    vm_wait(4 * min(PF - 1, KS - 1 - st));
+    lds_barrier();
     if (st + PF < KS) issue(st + PF);
     const int buf = st % NR;
     u32x4 xf[4], wf[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int rx = 64 * wm + 16 * t + i, rw = 64 * wn + 16 * t + i;
-      xf[t] = sm[buf][0][rx * 4 + (g ^ ((rx >> 2) & 3))];
-      wf[t] = sm[buf][1][rw * 4 + (g ^ ((rw >> 2) & 3))];
+      xf[t] = lds_read128(&sm[buf][0][rx * 4 + (g ^ ((rx >> 2) & 3))]);
+      wf[t] = lds_read128(&sm[buf][1][rw * 4 + (g ^ ((rw >> 2) & 3))]);
     }
+    lds_wait8(xf[0], xf[1], xf[2], xf[3], wf[0], wf[1], wf[2], wf[3]);
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm)
 #pragma unroll

@@ -59,6 +59,34 @@ def test_forward_and_step_bit_exact(torch_dev, oracle, make_weights, d, L, ds):
         assert np.array_equal(st.view(np.uint32), want[:, t].view(np.uint32)), f"step {t}"
 
 
+@pytest.mark.parametrize("d,L,ds", [(128, 1, 16), (256, 1, 16), (512, 1, 32)])
+def test_fp32_many_lanes_step_equals_chunk_and_round_trip(torch_dev, make_weights, d, L, ds):
+    """From 2048 lanes on, the fp32 decode step's GEMMs run their many-lane
+    tile forms (32 x 32 and 64-lane wave tiles, a partial last tile at 2100
+    lanes): step logits stay bit-identical to chunk logits, and a container
+    of 2101 chunks (one decode batch) round-trips byte for byte."""
+    torch = torch_dev
+    w = make_weights(d, L, ds)
+    lanes, T = 2100, 5
+    rng = np.random.default_rng(11 + d)
+    tok = rng.integers(0, 256, size=(lanes, T), dtype=np.uint8)
+    c = _codec(d, L, ds, lanes=2200, w=w)
+    c.reset_state(lanes)
+    d_log = torch.zeros(lanes * T * 256, dtype=torch.float32, device="cuda")
+    c.forward_chunk(torch.from_numpy(tok).cuda(), lanes, T, d_log)
+    torch.cuda.synchronize()
+    got = d_log.cpu().numpy().reshape(lanes, T, 256)
+    c.reset_state(lanes)
+    d_s = torch.zeros(lanes * 256, dtype=torch.float32, device="cuda")
+    for t in range(T):
+        c.step_batch(torch.from_numpy(np.ascontiguousarray(tok[:, t])).cuda(), lanes, d_s, True)
+        st = d_s.cpu().numpy().reshape(lanes, 256)
+        assert np.array_equal(st.view(np.uint32), got[:, t].view(np.uint32)), f"step {t}"
+    data = synth.gen_c2(2700)[:2100 * 40 + 7]
+    blob = c.compress(data, chunk_size=40)
+    assert c.decompress(blob) == data
+
+
 @pytest.mark.parametrize("d,ds,prec", [(64, 16, "fp32"), (80, 16, "fp32"), (256, 16, "fp32"),
                                        (64, 16, "bf16"), (256, 16, "bf16"), (512, 32, "bf16")])
 def test_scan_forms_agree(torch_dev, oracle, make_weights, d, ds, prec):
