@@ -354,59 +354,66 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_lds_kernel(DecB16Args a) {
     }
 }
 
-// Block-tiled form for many lanes and wide bf16 outputs (in_proj, FF1): a
-// block of four waves owns 128 lanes x 128 features, wave w the 4 x 4 tiles
-// of lanes 64 (w / 2) .. + 63 and features 64 (w % 2) .. + 63.  The operands
-// go straight from global memory to LDS (global_load_lds, 16 bytes a lane),
-// one 32-k step a stage, three stages in flight in a ring of four, so each
-// operand byte passes the vector memory path once per 128 x 128 tile (the
-// register-blocked form re-reads each fragment per 32 x 32 tile, which
-// keeps its texture-address units busy half its time).  A stage's 8 KB tile
-// of one operand holds row r's 16-byte quarter q at position
+// Block-tiled form for many lanes and outputs 512 wide or more: a block of
+// four waves owns 128 lanes x 128 features, wave w the 4 x 4 tiles of lanes
+// 64 (w / 2) .. + 63 and features 64 (w % 2) .. + 63.  The
+// operands go straight from global memory to LDS (global_load_lds, 16 bytes
+// a lane), one 32-k step a stage, three stages in flight in a ring of four,
+// so each operand byte passes the vector memory path once per block tile
+// (the register-blocked form re-read each fragment per 32 x 32 tile, which
+// kept its texture-address units busy half its time; the 64 x 64 LDS form
+// stages through registers one group ahead, which its MFMAs cannot cover).
+// A stage's tile of one operand holds row r's 16-byte quarter q at position
 // q ^ ((r >> 2) & 3), so that the 16 lanes of a ds_read_b128 pass read 16
 // distinct bank groups.  The stage's reads and barrier bypass the
 // compiler's waits (lds_read128, lds_barrier: its own would wait for every
 // copy in flight).  Blocks map to XCDs by t128_block.  Every tile's k-steps
 // run in the order of dec_b16_gemm_kernel (the same bits).  The epilogue
-// walks the tiles a feature column at a time, loading the column's bias
-// (and in_proj's conv taps) once; in_proj loads column tn + 1's conv state
-// while column tn is computed.
+// (dec_b16_epilogue's, for bf16 or fp32 + residual outputs) walks the tiles
+// a feature column at a time, loading the column's bias (and in_proj's conv
+// taps) once; in_proj loads column tn + 1's conv state while column tn is
+// computed.
 constexpr int T128_RING = 4;  // LDS stages; T128_RING - 1 in flight
 
-template <int KS, bool CONV>
+template <int KS, bool CONV, bool F32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_b16_gemm_t128_kernel(DecB16Args a) {
   constexpr int NR = T128_RING, PF = (NR - 1 < KS ? NR - 1 : KS);  // stages issued ahead
-  // [ring stage][operand: X, W][row * 4 + quarter]
-  __shared__ __align__(16) u32x4 sm[NR][2][128 * 4];
+  constexpr int BM = 128, TMW = 4;             // lanes per block, lane tiles per wave
+  constexpr int NQ = (BM + 128) / 16;          // 1 KB copies per stage
+  constexpr int IPW = NQ / 4;                  // of them per wave
+  // [ring stage][X rows 0 .. BM-1, then W rows 0 .. 127][row * 4 + quarter]
+  __shared__ __align__(16) u32x4 sm[NR][(BM + 128) * 4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
-  const int2 mn = t128_block(blockIdx.x, (a.M + 127) / 128, (a.N + 127) / 128);
-  const int m0 = mn.x * 128, n0 = mn.y * 128;
+  const int2 mn = t128_block(blockIdx.x, (a.M + BM - 1) / BM, (a.N + 127) / 128);
+  const int m0 = mn.x * BM, n0 = mn.y * 128;
   const u32x4* X4 = reinterpret_cast<const u32x4*>(a.X);
   const u32x4* W4 = reinterpret_cast<const u32x4*>(a.W);
-  // DMA of k-step s: wave wv issues instructions 4 wv .. 4 wv + 3 of the
-  // stage's 16 (operand q / 8, 1 KB part j = q % 8); lane L of part j fills
-  // position 64 j + L of the 8 KB tile: row (64 j + L) / 4, quarter L % 4
+  // DMA of k-step st: wave wv issues copies IPW wv .. IPW wv + IPW - 1 of
+  // the stage's NQ (the first BM / 16 fill X, the rest W); lane L of copy j
+  // of an operand fills position 64 j + L: row (64 j + L) / 4, quarter L % 4
   auto issue = [&](int st) {
     const int buf = st % NR;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int q = 4 * wv + u;
-      const int op = q >> 3, j = q & 7;
+    for (int u = 0; u < IPW; ++u) {
+      const int q = IPW * wv + u;
+      const bool xop = q < BM / 16;
+      const int j = xop ? q : q - BM / 16;
       const int pos = 64 * j + lane, row = pos >> 2, qd = pos & 3;
       const int gq = qd ^ ((row >> 2) & 3);
-      const u32x4* src = op == 0 ? X4 + ((size_t)st * a.ldx + min(m0 + row, a.M - 1)) * 4 + gq
-                                 : W4 + ((size_t)st * a.ldw + min(n0 + row, a.ldw - 1)) * 4 + gq;
+      const u32x4* src = xop ? X4 + ((size_t)st * a.ldx + min(m0 + row, a.M - 1)) * 4 + gq
+                             : W4 + ((size_t)st * a.ldw + min(n0 + row, a.ldw - 1)) * 4 + gq;
       __builtin_amdgcn_global_load_lds(
-          (const void*)src, (__attribute__((address_space(3))) void*)(&sm[buf][op][64 * j]), 16,
-          0, 0);
+          (const void*)src,
+          (__attribute__((address_space(3))) void*)(&sm[buf][(xop ? 0 : BM * 4) + 64 * j]), 16, 0,
+          0);
     }
   };
   const int wm = wv >> 1, wn = wv & 1;
-  floatx4 acc[4][4];
+  floatx4 acc[TMW][4];
 #pragma unroll
-  for (int tm = 0; tm < 4; ++tm)
+  for (int tm = 0; tm < TMW; ++tm)
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) acc[tm][tn] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -414,37 +421,37 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
 #pragma unroll 1
   for (int st = 0; st < KS; ++st) {
     // this wave's copies of stage st have landed (the younger in-flight
-    // stages, four instructions each, may still run); after the barrier
-    // every wave's have, and every wave is done with stage st - 1's buffer
-    vm_wait(4 * min(PF - 1, KS - 1 - st));
+    // stages, IPW copies each, may still run); after the barrier every
+    // wave's have, and every wave is done with stage st - 1's buffer
+    vm_wait(IPW * min(PF - 1, KS - 1 - st));
     lds_barrier();
     if (st + PF < KS) issue(st + PF);
     const int buf = st % NR;
     u32x4 xf[4], wf[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int rx = 64 * wm + 16 * t + i, rw = 64 * wn + 16 * t + i;
-      xf[t] = lds_read128(&sm[buf][0][rx * 4 + (g ^ ((rx >> 2) & 3))]);
-      wf[t] = lds_read128(&sm[buf][1][rw * 4 + (g ^ ((rw >> 2) & 3))]);
+      const int rx = (BM / 2) * wm + 16 * t + i, rw = 64 * wn + 16 * t + i;
+      xf[t] = lds_read128(&sm[buf][rx * 4 + (g ^ ((rx >> 2) & 3))]);
+      wf[t] = lds_read128(&sm[buf][BM * 4 + rw * 4 + (g ^ ((rw >> 2) & 3))]);
     }
     lds_wait8(xf[0], xf[1], xf[2], xf[3], wf[0], wf[1], wf[2], wf[3]);
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm)
+    for (int tm = 0; tm < TMW; ++tm)
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn)
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8, wf[tn]), __builtin_bit_cast(bf16x8, xf[tm]), acc[tm][tn], 0,
             0, 0);
   }
-  // epilogue (bf16 output): bias and activation; in_proj's x half runs the
-  // conv step as dec_b16_epilogue does
+  // epilogue: bias and activation; bf16 outputs (in_proj's x half runs the
+  // conv step) or fp32 + residual (and the bf16 copy), as dec_b16_epilogue
   const bool conv_b = CONV && n0 < a.conv_di;
-  ushort4 cs[2][4][4];  // conv state of a tile column: [buffer][tile row][channel]
-  auto load_cs = [&](int tn, ushort4 (&dst)[4][4]) {
+  ushort4 cs[2][TMW][4];  // conv state of a tile column: [buffer][tile row][channel]
+  auto load_cs = [&](int tn, ushort4 (&dst)[TMW][4]) {
     const int nb = n0 + 64 * wn + 16 * tn + 4 * g;
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-      const int mm = min(m0 + 64 * wm + 16 * tm + i, a.M - 1);
+    for (int tm = 0; tm < TMW; ++tm) {
+      const int mm = min(m0 + (BM / 2) * wm + 16 * tm + i, a.M - 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const ushort4* sp = reinterpret_cast<const ushort4*>(a.conv_state) + (size_t)(nb + e) * a.ld_state + mm;
@@ -457,26 +464,25 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
       }
     }
   };
-  if (conv_b) load_cs(0, cs[0]);
-  uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+  if (CONV && conv_b) load_cs(0, cs[0]);
 #pragma unroll
   for (int tn = 0; tn < 4; ++tn) {
     const int nb = n0 + 64 * wn + 16 * tn + 4 * g;
-    if (conv_b && tn + 1 < 4) load_cs(tn + 1, cs[(tn + 1) & 1]);
+    if (CONV && conv_b && tn + 1 < 4) load_cs(tn + 1, cs[(tn + 1) & 1]);
     if (nb < a.N) {
       const float4 bv = a.bias ? *reinterpret_cast<const float4*>(a.bias + nb) : make_float4(0.f, 0.f, 0.f, 0.f);
       const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
       float4 cw[4];
       float4 cbv = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (conv_b) {
+      if (CONV && conv_b) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) cw[e] = reinterpret_cast<const float4*>(a.conv_w)[nb + e];
         cbv = *reinterpret_cast<const float4*>(a.conv_b + nb);
       }
       const float cbb[4] = {cbv.x, cbv.y, cbv.z, cbv.w};
 #pragma unroll
-      for (int tm = 0; tm < 4; ++tm) {
-        const int m = m0 + 64 * wm + 16 * tm + i;
+      for (int tm = 0; tm < TMW; ++tm) {
+        const int m = m0 + (BM / 2) * wm + 16 * tm + i;
         if (m >= a.M) continue;
         float v[4];
 #pragma unroll
@@ -486,7 +492,19 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
           else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
           v[e] = r;
         }
-        if (conv_b) {
+        if constexpr (F32) {  // residual stream: fp32 k-blocked, + res
+          float* C = reinterpret_cast<float*>(a.C);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float r = v[e];
+            if (a.res) r = r + a.res[dblk(nb + e, m, a.ldr)];
+            v[e] = r;
+            C[dblk(nb + e, m, a.ldc)] = r;
+          }
+          if (a.C2)
+            *reinterpret_cast<ushort4*>(a.C2 + dblk32(nb, m, a.ldc)) =
+                make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
+        } else if (CONV && conv_b) {
           uint16_t o[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -501,6 +519,7 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
           *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) =
               make_ushort4(o[0], o[1], o[2], o[3]);
         } else {
+          uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
           const int row = a.conv_di > 0 ? nb - a.conv_di : nb;
           *reinterpret_cast<ushort4*>(C + dblk32(row, m, a.ldc)) =
               make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
@@ -526,16 +545,16 @@ hipError_t dec_b16_lds_launch(const DecB16Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <bool CONV>
+template <bool CONV, bool F32>
 hipError_t dec_b16_t128_launch(const DecB16Args& a, hipStream_t s) {
   const dim3 grid(((a.M + 127) / 128) * ((a.N + 127) / 128)), block(256);
   switch (a.K) {
-    case 64: BOA_LAUNCH((dec_b16_gemm_t128_kernel<2, CONV>), grid, block, 0, s, a); break;
-    case 128: BOA_LAUNCH((dec_b16_gemm_t128_kernel<4, CONV>), grid, block, 0, s, a); break;
-    case 256: BOA_LAUNCH((dec_b16_gemm_t128_kernel<8, CONV>), grid, block, 0, s, a); break;
-    case 512: BOA_LAUNCH((dec_b16_gemm_t128_kernel<16, CONV>), grid, block, 0, s, a); break;
-    case 1024: BOA_LAUNCH((dec_b16_gemm_t128_kernel<32, CONV>), grid, block, 0, s, a); break;
-    case 2048: BOA_LAUNCH((dec_b16_gemm_t128_kernel<64, CONV>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_b16_gemm_t128_kernel<2, CONV, F32>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_b16_gemm_t128_kernel<4, CONV, F32>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_b16_gemm_t128_kernel<8, CONV, F32>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_b16_gemm_t128_kernel<16, CONV, F32>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_b16_gemm_t128_kernel<32, CONV, F32>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_b16_gemm_t128_kernel<64, CONV, F32>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -564,16 +583,23 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
       (a.out_mode != DEC_OUT_ROWMAJOR && a.ldc < a.M) || (a.res && a.ldr < a.M))
     return hipErrorInvalidValue;
   // From 2048 lanes on:
-  // - in_proj and FF1 (bf16 output, N >= 512): the 128 x 128 blocks (C3
-  //   decode GEMMs 809 -> 716 us per step, decompress 4.88 -> 5.15 MB/s;
-  //   C5 probe 5.58 -> 4.73 ms, 1.05 -> 1.11 MB/s);
+  // - outputs 512 wide or more (in_proj and FF1; at d_model 512 also
+  //   out_proj and FF2): the 128 x 128 blocks (C3 decode GEMMs 809 -> 716
+  //   us per step, decompress 4.88 -> 5.15 MB/s; C5 probe 5.58 -> 4.73 ms,
+  //   1.05 -> 1.11 MB/s, then out_proj and FF2 4.24 -> 3.84 ms, 1.153 ->
+  //   1.187 MB/s; 64-lane blocks for the 256-wide out_proj and FF2 of C3
+  //   were slower, 708 -> 774 us);
   // - the other GEMMs: 2 x 2 tiles per wave for K <= 256 (C3 decode 3.76 ->
   //   4.40 MB/s against one tile per wave; 4 x 4, 2 x 1 and 1 x 2 were
   //   slower) and the 64 x 64 LDS-tiled blocks for K >= 512 (4.40 -> 4.54
   //   MB/s at C3, 0.95 -> 0.98 at C5)
   if (a.M >= 2048) {
-    if (a.out_mode == DEC_OUT_B16 && a.N >= 512 && a.conv_di % 128 == 0)
-      return a.conv_di > 0 ? dec_b16_t128_launch<true>(a, s) : dec_b16_t128_launch<false>(a, s);
+    if ((a.out_mode == DEC_OUT_B16 || a.out_mode == DEC_OUT_F32) && a.N >= 512 &&
+        a.conv_di % 128 == 0) {
+      if (a.out_mode == DEC_OUT_F32) return dec_b16_t128_launch<false, true>(a, s);
+      return a.conv_di > 0 ? dec_b16_t128_launch<true, false>(a, s)
+                           : dec_b16_t128_launch<false, false>(a, s);
+    }
     if (a.K >= 512) return dec_b16_lds_launch(a, s);
     return a.conv_di > 0 ? dec_b16_blk_launch<2, 2, true>(a, s) : dec_b16_blk_launch<2, 2, false>(a, s);
   }
