@@ -96,6 +96,9 @@ __device__ __forceinline__ lds_u32x4 lds_read128(const void* p) {
 }
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 // the reads' values are the asm's outputs, so nothing uses them before it
+__device__ __forceinline__ void lds_wait4(lds_u32x4& a, lds_u32x4& b, lds_u32x4& c, lds_u32x4& d) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d)::"memory");
+}
 __device__ __forceinline__ void lds_wait8(lds_u32x4& a, lds_u32x4& b, lds_u32x4& c, lds_u32x4& d,
                                           lds_u32x4& e, lds_u32x4& f, lds_u32x4& g, lds_u32x4& h) {
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -107,7 +110,9 @@ __device__ __forceinline__ void vm_wait(int n) {
     case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
     case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
     case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
     case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
     case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
   }

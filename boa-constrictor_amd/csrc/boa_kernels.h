@@ -222,7 +222,7 @@ bool dec_ln_gemm_fits(int d, int N);
 hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, const uint8_t* tok,
                               float* xt, const float* lw, const float* lb, int* t_counter,
                               hipStream_t s);
-// decode GEMM with an explicit wave-tile configuration (4, 9, 10 or 13; all give the same bits)
+// decode GEMM with an explicit wave-tile configuration (4, 9, 10, 13 or 15; all give the same bits)
 hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s);
 hipError_t launch_dec_weight_blk(const float* w, int ldw_in, int n_src, float* out, int K, int ldn,
                                  int permute, int zs, int ze, hipStream_t s);

@@ -246,6 +246,78 @@ __global__ __launch_bounds__(256) void dec_gemm_kernel(DecGemmArgs a) {
     for (int tn = 0; tn < TN; ++tn) dec_epilogue(a, acc[tm][tn], n0 + 16 * tn, m0 + 16 * tm + i, g);
 }
 
+// One 16 x 16 tile per wave with the weight fragments shared in LDS.  The
+// block's four waves take the four 16-lane tiles of a 64-lane group and one
+// 16-feature n tile, as in dec_gemm_wave, so they need the same weight
+// fragment at every 16-k block.  Per stage of four 16-k blocks, wave w
+// copies weight block 4 s + w (1 KB: lane i + 16 g gets the float4 of
+// feature n0 + i, k quad g) straight into LDS (global_load_lds), and its own
+// four activation blocks likewise; every wave then reads its operands from
+// LDS, one 16-byte read per lane and block.  A CU issues 20 vector-memory
+// loads per stage instead of 32: a 16-byte-per-lane load occupies the
+// texture-address unit for about 32 cycles, which bounded dec_gemm_wave on
+// the 1000-lane K >= 512 shapes (FF2 9.5 us against a 256-MFMA chain of
+// about 6 us).  The activations go through LDS too so that every operand
+// wait is this kernel's own (vm_wait): the compiler waits for all copies in
+// flight (vmcnt(0)) before a register load's use once a copy to LDS is
+// pending.  Same K-ordered chain, same bits.
+template <int KS, int P>
+__global__ __launch_bounds__(256) void dec_gemm_sw_kernel(DecGemmArgs a) {
+  constexpr int QB = KS / 4, ST = QB / 4, R = P + 1;  // 16-k blocks, stages, ring slots
+  static_assert(QB % 4 == 0 && ST > P, "whole stages of four 16-k blocks");
+  // slot: 4 weight blocks, then 4 activation blocks of each wave
+  __shared__ __align__(16) lds_u32x4 sm[R][4 + 16][64];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const XcdSlot sl = xcd_slot(blockIdx.x, (a.N + 15) / 16);
+  const int m0 = sl.grp * 64 + 16 * w, n0 = sl.j * 16;
+  if (sl.grp * 64 >= a.M) return;  // the whole block; waves past M take part in the barriers
+  EpiPre<> pre;
+  dec_epi_prefetch<false>(a, n0, m0 + i, g, pre);
+  const size_t wq = (size_t)a.ldw * 4, xq = (size_t)a.ldx * 4;  // float4s per 16-k block
+  const lds_u32x4* wsrc = reinterpret_cast<const lds_u32x4*>(a.W) + (size_t)(n0 + i) * 4 + g + w * wq;
+  const lds_u32x4* xsrc =
+      reinterpret_cast<const lds_u32x4*>(a.Xt) + (size_t)min(m0 + i, a.M - 1) * 4 + g;
+  auto issue = [&](int s) {  // stage s: one weight copy and four activation copies
+    __builtin_amdgcn_global_load_lds((const void*)(wsrc + (size_t)(4 * s) * wq),
+                                     (__attribute__((address_space(3))) void*)&sm[s % R][w][0],
+                                     16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(xsrc + (size_t)(4 * s + u) * xq),
+          (__attribute__((address_space(3))) void*)&sm[s % R][4 + 4 * w + u][0], 16, 0, 0);
+  };
+  floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < P; ++s) issue(s);
+#pragma unroll
+  for (int s = 0; s < ST; ++s) {
+    // this wave's copies of stage s are done (the younger stages' five
+    // copies each may still run); after the barrier every wave's are in LDS
+    // and every wave is done reading slot (s - 1) % R, which the copies of
+    // stage s + P overwrite
+    vm_wait(5 * min(P - 1, ST - 1 - s));
+    lds_barrier();
+    if (s + P < ST) issue(s + P);
+    lds_u32x4 wf[4], xf[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      wf[u] = lds_read128(&sm[s % R][u][lane]);
+      xf[u] = lds_read128(&sm[s % R][4 + 4 * w + u][lane]);
+    }
+    lds_wait8(wf[0], wf[1], wf[2], wf[3], xf[0], xf[1], xf[2], xf[3]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const floatx4 wv = __builtin_bit_cast(floatx4, wf[u]);
+      const floatx4 xv = __builtin_bit_cast(floatx4, xf[u]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[e], xv[e], acc, 0, 0, 0);
+    }
+  }
+  dec_epilogue(a, acc, n0, m0 + i, g, pre);
+}
+
 namespace {
 template <int TM, int TN, int UQ, int PD>
 hipError_t dec_launch(const DecGemmArgs& a, hipStream_t s) {
@@ -272,12 +344,26 @@ hipError_t dec_check(const DecGemmArgs& a) {
     return hipErrorInvalidValue;
   return hipSuccess;
 }
+
+template <int P>
+hipError_t dec_launch_sw(const DecGemmArgs& a, hipStream_t s) {
+  const dim3 grid(xcd_grid(a.M, (a.N + 15) / 16)), block(256);
+  switch (a.K) {
+    case 256: BOA_LAUNCH((dec_gemm_sw_kernel<64, P>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_gemm_sw_kernel<128, P>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_gemm_sw_kernel<256, P>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_gemm_sw_kernel<512, P>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 }  // namespace
 
 hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0) return hipSuccess;
   if (hipError_t e = dec_check(a)) return e;
   switch (cfg) {
+    case 15: return dec_launch_sw<3>(a, s);
     case 4: return dec_launch<1, 1, 1, 8>(a, s);
     case 9: return dec_launch<2, 2, 1, 6>(a, s);
     case 10: return dec_launch<1, 1, 1, 2>(a, s);
@@ -289,11 +375,15 @@ hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s) {
 // Wave tiles by shape, from a sweep on MI355X (all configurations give the
 // same bits): K = 256 x N >= 1024 (in_proj, FF1) runs fastest on the smallest
 // register ring; from 2048 lanes on, 32 x 32 tiles halve the operand loads of
-// the K >= 512 projections and 64-lane tiles those of the heads.
+// the K >= 512 projections and 64-lane tiles those of the heads; below 2048
+// lanes the other K >= 256 shapes (out_proj, FF2, the heads) share their
+// weight fragments through LDS (at 1000 lanes 127 -> 110 us of these GEMMs
+// per decode step, three stages in flight; two measured 0.5 us slower).
 hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
   int cfg = 4;
   if (a.K <= 256 && a.N >= 1024) cfg = 10;
   else if (a.M >= 2048 && a.N >= 256) cfg = a.K >= 512 ? 9 : 13;
+  else if (a.M < 2048 && (a.K == 256 || a.K == 512 || a.K == 1024 || a.K == 2048)) cfg = 15;
   return dec_gemm_cfg(a, cfg, s);
 }
 
