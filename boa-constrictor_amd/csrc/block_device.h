@@ -54,6 +54,17 @@ __device__ __forceinline__ void state_st4(float4* p, float4 v, bool cached) {
   if (cached) *p = v;
   else st_stream(p, v);
 }
+// The conv step reads the last three of a channel's four state values (the
+// oldest drops out): loading only those keeps the compiler from reusing the
+// fourth one's register while its load is in flight, which it guards with a
+// wait for that load and every load before it.  x is left 0.
+typedef float stream_f3 __attribute__((ext_vector_type(3)));
+template <bool CACHED>
+__device__ __forceinline__ float4 state_ld3(const float4* p) {
+  const stream_f3* q = reinterpret_cast<const stream_f3*>(reinterpret_cast<const float*>(p) + 1);
+  const stream_f3 v = CACHED ? *q : __builtin_nontemporal_load(q);
+  return make_float4(0.0f, v[0], v[1], v[2]);
+}
 // bf16 precision keeps the step-layout conv state as four bf16 (8 bytes) per
 // channel and lane: its values are the bf16-rounded in_proj outputs, so the
 // narrow form is exact and halves the state's traffic.

@@ -50,14 +50,19 @@ struct EpiPre {
   float cb[CONV ? 4 : 1];
 };
 
-template <bool CONV = false>
+// SC: the conv state's cache policy at compile time (1 cached, 0 streamed)
+// or -1 for a.state_cached; BIAS: a.bias is known to be set.  A runtime
+// choice between two loads, or a load and a constant, joins in a register
+// copy that the compiler guards with s_waitcnt vmcnt(0), which also waits
+// for every load and copy issued before (the LayerNorm GEMM's weight rows).
+template <bool CONV = false, int SC = -1, bool BIAS = false>
 __device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, int m, int g,
                                                  EpiPre<CONV>& p) {
   if (m >= a.M || n0 >= a.N) return;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int nf = a.row_major ? n0 + 4 * g + e : n0 + 4 * e + g;
-    p.b[e] = a.bias ? a.bias[min(nf, a.N - 1)] : 0.0f;
+    p.b[e] = (BIAS || a.bias) ? a.bias[min(nf, a.N - 1)] : 0.0f;
   }
   if (a.res && !a.row_major && !(a.conv_di > 0))
     p.r = reinterpret_cast<const float4*>(a.res)[((size_t)(n0 >> 4) * a.ldr + m) * 4 + g];
@@ -65,8 +70,8 @@ __device__ __forceinline__ void dec_epi_prefetch(const DecGemmArgs& a, int n0, i
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int n = n0 + 4 * e + g;
-      p.cs[e] = state_ld4(reinterpret_cast<const float4*>(a.conv_state) + (size_t)n * a.ld_state + m,
-                          a.state_cached);
+      const float4* sp = reinterpret_cast<const float4*>(a.conv_state) + (size_t)n * a.ld_state + m;
+      p.cs[e] = SC < 0 ? state_ld4(sp, a.state_cached) : state_ld3<SC == 1>(sp);
       p.cw[e] = reinterpret_cast<const float4*>(a.conv_w)[n];
       p.cb[e] = a.conv_b[n];
     }
@@ -491,8 +496,7 @@ hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, floa
 // features:
 //   1. it copies the 64 lanes' k-blocked rows (through registers) and the
 //      64 weight rows (straight from global memory) into LDS, per 16-k block
-//      one contiguous 4 KB span each; the weight copies complete during
-//      step 2 and are waited for before step 3;
+//      one contiguous 4 KB span each, and loads the epilogue's operands;
 //   2. it computes each lane's mean and rstd in the LayerNorm's reduction
 //      order (dec_ln_kernel) and normalises the rows in LDS with the same
 //      operations, so the operands are the bits the LayerNorm would store;
@@ -505,7 +509,7 @@ hipError_t launch_dec_head_step(const DecGemmArgs& a, const float* head_b2, floa
 // 0 blocks store them as x.
 // The block's work for virtual block vb, with its LDS passed in: xs and ws
 // of NB * 1024 floats each, lwb of 2 d, stats of 128.
-template <int MODE, int NB, bool EMB>
+template <int MODE, int NB, bool EMB, int SC>
 __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const float* __restrict__ emb,
                                                  const uint8_t* __restrict__ tok, float* xt,
                                                  const float* __restrict__ lw,
@@ -546,10 +550,13 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
     }
   }
   // the weight rows go straight to LDS (global_load_lds_dwordx4: a wave's 64
-  // float4s are one contiguous 1 KB span at both ends); issued after the
-  // rows' LDS stores, they complete behind the LayerNorm (the scheduling
-  // barrier keeps them after the stores, whose wait would otherwise cover
-  // them too): LN GEMMs 13.4 -> 13.2 us at 1000 lanes
+  // float4s are one contiguous 1 KB span at both ends), issued after the
+  // rows' LDS stores (the scheduling barrier keeps them there): 13.4 ->
+  // 13.2 us at 1000 lanes against register staging.  The compiler waits for
+  // every copy before the LayerNorm's first LDS read, so they and the
+  // epilogue loads below complete before step 2; staging the weights through
+  // registers instead, which lets the LayerNorm run under the loads,
+  // measured slower (LN GEMMs 206 -> 209.5 us per step at 1000 lanes).
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int it = 0; it < SQ; ++it) {
@@ -568,7 +575,7 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   const int lane_ = tid & 63, wv_ = tid >> 6;
   const int lr_ = 16 * (wv_ >> 2) + (lane_ & 15), fn0 = n0 + 16 * (wv_ & 3);
   EpiPre<MODE == 1> pre;
-  dec_epi_prefetch<MODE == 1>(a, fn0, m0 + lr_, lane_ >> 4, pre);
+  dec_epi_prefetch<MODE == 1, SC, true>(a, fn0, m0 + lr_, lane_ >> 4, pre);
   if (EMB && n0 == 0 && m0 + ml < a.M) {  // layer 0: x = embedding rows
 #pragma unroll
     for (int it = 0; it < SQ; ++it) {
@@ -581,7 +588,7 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   // 2. statistics (the orders of dec_ln_kernel) and normalisation
   if (MODE == 1) {
     const int lj = tid >> 4, l = tid & 15;
-    auto xat = [&](int f) { return xs[((f >> 4) * 64 + lj) * 16 + dperm(f & 15)]; };
+    auto xat = [xs, lj](int f) { return xs[((f >> 4) * 64 + lj) * 16 + dperm(f & 15)]; };
     float s0 = 0.0f, q0 = 0.0f, s1 = 0.0f, q1 = 0.0f;
 #pragma unroll
     for (int f = l; f < d; f += 32) {
@@ -672,7 +679,8 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   dec_epilogue<MODE == 1>(a, acc, n0 + 16 * (wv & 3), m0 + lr, g, pre);
 }
 
-template <int MODE, int NB, bool EMB>
+// SC: the conv state's cache policy (in_proj; 0 for FF1)
+template <int MODE, int NB, bool EMB, int SC>
 __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const float* __restrict__ emb,
                                                            const uint8_t* __restrict__ tok, float* xt,
                                                            const float* __restrict__ lw,
@@ -684,8 +692,8 @@ __global__ __launch_bounds__(1024) void dec_ln_gemm_kernel(DecGemmArgs a, const 
   __shared__ float lwb[2 * NB * 16];
   __shared__ float stats[2 * 64];
   if (t_counter && blockIdx.x == 0 && threadIdx.x == 0) *t_counter += 1;
-  dec_ln_gemm_body<MODE, NB, EMB>(a, emb, tok, xt, lw, lb, blockIdx.x, xs, ws, lwb, stats,
-                                         threadIdx.x);
+  dec_ln_gemm_body<MODE, NB, EMB, SC>(a, emb, tok, xt, lw, lb, blockIdx.x, xs, ws, lwb, stats,
+                                      threadIdx.x);
 }
 
 bool dec_ln_gemm_fits(int d, int N) { return (d == 64 || d == 128 || d == 256) && N % 64 == 0; }
@@ -694,21 +702,27 @@ hipError_t launch_dec_ln_gemm(int mode, const DecGemmArgs& a, const float* emb, 
                               float* xt, const float* lw, const float* lb, int* t_counter,
                               hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  if (!dec_ln_gemm_fits(a.K, a.N) || (mode != 1 && mode != 2) || (emb && mode != 1) ||
+  if (!dec_ln_gemm_fits(a.K, a.N) || (mode != 1 && mode != 2) || (emb && mode != 1) || !a.bias ||
       a.ldw < a.N || a.ldx < a.M || a.ldc < (a.row_major ? a.N : a.M) ||
       (a.res && a.ldr < a.M) || (a.conv_di % 16))
     return hipErrorInvalidValue;
   const dim3 grid(xcd_grid(a.M, a.N / 64)), block(1024);
 #define BOA_LNG(NBv)                                                                          \
-  if (emb)                                                                                    \
-    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, true>), grid, block, 0, s, a, emb, tok, xt,  \
-                       lw, lb, t_counter);                                                    \
+  if (emb && a.state_cached)                                                                  \
+    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, true, 1>), grid, block, 0, s, a, emb, tok, xt, \
+               lw, lb, t_counter);                                                            \
+  else if (emb)                                                                               \
+    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, true, 0>), grid, block, 0, s, a, emb, tok, xt, \
+               lw, lb, t_counter);                                                            \
+  else if (mode == 1 && a.state_cached)                                                       \
+    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, false, 1>), grid, block, 0, s, a, emb, tok, xt, \
+               lw, lb, t_counter);                                                            \
   else if (mode == 1)                                                                         \
-    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
-                       lw, lb, t_counter);                                                    \
+    BOA_LAUNCH((dec_ln_gemm_kernel<1, NBv, false, 0>), grid, block, 0, s, a, emb, tok, xt, \
+               lw, lb, t_counter);                                                            \
   else                                                                                        \
-    BOA_LAUNCH((dec_ln_gemm_kernel<2, NBv, false>), grid, block, 0, s, a, emb, tok, xt, \
-                       lw, lb, t_counter);
+    BOA_LAUNCH((dec_ln_gemm_kernel<2, NBv, false, 0>), grid, block, 0, s, a, emb, tok, xt, \
+               lw, lb, t_counter);
   switch (a.K) {
     case 64: BOA_LNG(4) break;
     case 128: BOA_LNG(8) break;

@@ -375,7 +375,84 @@ __global__ __launch_bounds__(256) void dec_b16_gemm_lds_kernel(DecB16Args a) {
 // computed.
 constexpr int T128_RING = 4;  // LDS stages; T128_RING - 1 in flight
 
-template <int KS, bool CONV, bool F32>
+// in_proj's conv blocks: per feature column tn of the wave (features nw +
+// 16 tn + 4 g + e), the conv state of its tiles' lanes and the column's bias,
+// taps and conv biases, loaded one column ahead (the column being computed
+// waits only for its own loads).  SC: the state's cache policy (1 cached, 0
+// streamed) at compile time; a runtime choice joins two loads in a register
+// copy that the compiler guards with a wait for every load in flight.
+template <int TMW, int SC>
+__device__ __forceinline__ void t128_conv_epilogue(const DecB16Args& a, const floatx4 (&acc)[TMW][4],
+                                                   int nw, int mw, int g) {
+  struct ColOps {
+    ushort4 cs[TMW][4];
+    float4 bias, cw[4], cb;
+  };
+  ColOps col[2];
+  auto load_col = [&](int tn, ColOps& o) {
+    const int nb = nw + 16 * tn + 4 * g;  // < conv_di <= N: in bounds
+#pragma unroll
+    for (int tm = 0; tm < TMW; ++tm) {
+      const int mm = min(mw + 16 * tm, a.M - 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const ushort4* sp = reinterpret_cast<const ushort4*>(a.conv_state) + (size_t)(nb + e) * a.ld_state + mm;
+        if constexpr (SC) {
+          o.cs[tm][e] = *sp;
+        } else {
+          const stream_h4 h = __builtin_nontemporal_load(reinterpret_cast<const stream_h4*>(sp));
+          o.cs[tm][e] = make_ushort4(h[0], h[1], h[2], h[3]);
+        }
+      }
+    }
+    o.bias = *reinterpret_cast<const float4*>(a.bias + nb);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o.cw[e] = reinterpret_cast<const float4*>(a.conv_w)[nb + e];
+    o.cb = *reinterpret_cast<const float4*>(a.conv_b + nb);
+  };
+  load_col(0, col[0]);
+#pragma unroll
+  for (int tn = 0; tn < 4; ++tn) {
+    if (tn + 1 < 4) load_col(tn + 1, col[(tn + 1) & 1]);
+    const ColOps& c = col[tn & 1];
+    const int nb = nw + 16 * tn + 4 * g;
+    const float bb[4] = {c.bias.x, c.bias.y, c.bias.z, c.bias.w};
+    const float cbb[4] = {c.cb.x, c.cb.y, c.cb.z, c.cb.w};
+    // every use of a loaded value is unconditional; only the stores test
+    // m < M (a use under the test would be waited for again, with every
+    // load and store in flight, after each tile row)
+#pragma unroll
+    for (int tm = 0; tm < TMW; ++tm) {
+      const int m = mw + 16 * tm;
+      uint16_t o[4];
+      float4 ns[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float r = acc[tm][tn][e] + bb[e];
+        if (a.act == ACT_GELU) r = gelu<MATH_HW>(r);
+        else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
+        const ushort4 h = c.cs[tm][e];
+        const float4 s0 = make_float4(bf16_to_f32(h.x), bf16_to_f32(h.y), bf16_to_f32(h.z),
+                                      bf16_to_f32(h.w));
+        const float x0 = bf16r(r);  // the compress pass reads xz in bf16
+        o[e] = f32_to_bf16(conv_step_value<MATH_HW>(cbb[e], s0, x0, c.cw[e]));
+        ns[e] = make_float4(s0.y, s0.z, s0.w, x0);
+      }
+      if (m < a.M) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          state_st4h(reinterpret_cast<ushort4*>(a.conv_state) + (size_t)(nb + e) * a.ld_state + m,
+                     ns[e], SC != 0);
+        *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) =
+            make_ushort4(o[0], o[1], o[2], o[3]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// SC: in_proj's conv state cache policy (t128_conv_epilogue; 0 otherwise)
+template <int KS, bool CONV, bool F32, int SC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_b16_gemm_t128_kernel(DecB16Args a) {
   constexpr int NR = T128_RING, PF = (NR - 1 < KS ? NR - 1 : KS);  // stages issued ahead
@@ -445,85 +522,70 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
   }
   // epilogue: bias and activation; bf16 outputs (in_proj's x half runs the
   // conv step) or fp32 + residual (and the bf16 copy), as dec_b16_epilogue
-  const bool conv_b = CONV && n0 < a.conv_di;
-  ushort4 cs[2][TMW][4];  // conv state of a tile column: [buffer][tile row][channel]
-  auto load_cs = [&](int tn, ushort4 (&dst)[TMW][4]) {
-    const int nb = n0 + 64 * wn + 16 * tn + 4 * g;
+  if constexpr (CONV) {
+    if (n0 < a.conv_di) {
+      t128_conv_epilogue<TMW, SC>(a, acc, n0 + 64 * wn, m0 + (BM / 2) * wm + i, g);
+      return;
+    }
+  }
+  // column tn + 1's bias (and residual, fp32 outputs) load while column tn
+  // is computed; the loaded values are used unconditionally and only the
+  // stores test m < M (as in t128_conv_epilogue)
+  struct ColOps {
+    float4 bias;
+    float res[F32 ? TMW : 1][4];
+  };
+  ColOps col[2];
+  auto load_col = [&](int tn, ColOps& o) {
+    const int nb = min(n0 + 64 * wn + 16 * tn + 4 * g, a.N - 4);  // N % 4 == 0
+    o.bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + nb) : make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (F32) {
+      if (a.res) {
 #pragma unroll
-    for (int tm = 0; tm < TMW; ++tm) {
-      const int mm = min(m0 + (BM / 2) * wm + 16 * tm + i, a.M - 1);
+        for (int tm = 0; tm < TMW; ++tm) {
+          const int mc = min(m0 + (BM / 2) * wm + 16 * tm + i, a.M - 1);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const ushort4* sp = reinterpret_cast<const ushort4*>(a.conv_state) + (size_t)(nb + e) * a.ld_state + mm;
-        if (a.state_cached) {
-          dst[tm][e] = *sp;
-        } else {
-          const stream_h4 h = __builtin_nontemporal_load(reinterpret_cast<const stream_h4*>(sp));
-          dst[tm][e] = make_ushort4(h[0], h[1], h[2], h[3]);
+          for (int e = 0; e < 4; ++e) o.res[tm][e] = a.res[dblk(nb + e, mc, a.ldr)];
         }
       }
     }
   };
-  if (CONV && conv_b) load_cs(0, cs[0]);
+  load_col(0, col[0]);
 #pragma unroll
   for (int tn = 0; tn < 4; ++tn) {
+    if (tn + 1 < 4) load_col(tn + 1, col[(tn + 1) & 1]);
+    const ColOps& c = col[tn & 1];
     const int nb = n0 + 64 * wn + 16 * tn + 4 * g;
-    if (CONV && conv_b && tn + 1 < 4) load_cs(tn + 1, cs[(tn + 1) & 1]);
-    if (nb < a.N) {
-      const float4 bv = a.bias ? *reinterpret_cast<const float4*>(a.bias + nb) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
-      float4 cw[4];
-      float4 cbv = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (CONV && conv_b) {
+    const float bb[4] = {c.bias.x, c.bias.y, c.bias.z, c.bias.w};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) cw[e] = reinterpret_cast<const float4*>(a.conv_w)[nb + e];
-        cbv = *reinterpret_cast<const float4*>(a.conv_b + nb);
+    for (int tm = 0; tm < TMW; ++tm) {
+      const int m = m0 + (BM / 2) * wm + 16 * tm + i;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float r = acc[tm][tn][e] + bb[e];
+        if (a.act == ACT_GELU) r = gelu<MATH_HW>(r);
+        else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
+        v[e] = r;
       }
-      const float cbb[4] = {cbv.x, cbv.y, cbv.z, cbv.w};
+      if constexpr (F32) {  // residual stream: fp32 k-blocked, + res
+        if (a.res) {
 #pragma unroll
-      for (int tm = 0; tm < TMW; ++tm) {
-        const int m = m0 + (BM / 2) * wm + 16 * tm + i;
-        if (m >= a.M) continue;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float r = acc[tm][tn][e] + bb[e];
-          if (a.act == ACT_GELU) r = gelu<MATH_HW>(r);
-          else if (a.act == ACT_RELU) r = fmaxf(0.0f, r);
-          v[e] = r;
+          for (int e = 0; e < 4; ++e) v[e] = v[e] + c.res[tm][e];
         }
-        if constexpr (F32) {  // residual stream: fp32 k-blocked, + res
+        if (m < a.M && nb < a.N) {
           float* C = reinterpret_cast<float*>(a.C);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float r = v[e];
-            if (a.res) r = r + a.res[dblk(nb + e, m, a.ldr)];
-            v[e] = r;
-            C[dblk(nb + e, m, a.ldc)] = r;
-          }
+          for (int e = 0; e < 4; ++e) C[dblk(nb + e, m, a.ldc)] = v[e];
           if (a.C2)
             *reinterpret_cast<ushort4*>(a.C2 + dblk32(nb, m, a.ldc)) =
                 make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
-        } else if (CONV && conv_b) {
-          uint16_t o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const ushort4 h = cs[tn & 1][tm][e];
-            const float4 s0 = make_float4(bf16_to_f32(h.x), bf16_to_f32(h.y), bf16_to_f32(h.z),
-                                          bf16_to_f32(h.w));
-            const float x0 = bf16r(v[e]);  // the compress pass reads xz in bf16
-            o[e] = f32_to_bf16(conv_step_value<MATH_HW>(cbb[e], s0, x0, cw[e]));
-            state_st4h(reinterpret_cast<ushort4*>(a.conv_state) + (size_t)(nb + e) * a.ld_state + m,
-                       make_float4(s0.y, s0.z, s0.w, x0), a.state_cached);
-          }
-          *reinterpret_cast<ushort4*>(a.conv_out + dblk32(nb, m, a.ldc)) =
-              make_ushort4(o[0], o[1], o[2], o[3]);
-        } else {
-          uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
-          const int row = a.conv_di > 0 ? nb - a.conv_di : nb;
-          *reinterpret_cast<ushort4*>(C + dblk32(row, m, a.ldc)) =
-              make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
         }
+      } else if (m < a.M && nb < a.N) {
+        uint16_t* C = reinterpret_cast<uint16_t*>(a.C);
+        const int row = a.conv_di > 0 ? nb - a.conv_di : nb;
+        *reinterpret_cast<ushort4*>(C + dblk32(row, m, a.ldc)) =
+            make_ushort4(f32_to_bf16(v[0]), f32_to_bf16(v[1]), f32_to_bf16(v[2]), f32_to_bf16(v[3]));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -545,16 +607,16 @@ hipError_t dec_b16_lds_launch(const DecB16Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <bool CONV, bool F32>
+template <bool CONV, bool F32, int SC = 0>
 hipError_t dec_b16_t128_launch(const DecB16Args& a, hipStream_t s) {
   const dim3 grid(((a.M + 127) / 128) * ((a.N + 127) / 128)), block(256);
   switch (a.K) {
-    case 64: BOA_LAUNCH((dec_b16_gemm_t128_kernel<2, CONV, F32>), grid, block, 0, s, a); break;
-    case 128: BOA_LAUNCH((dec_b16_gemm_t128_kernel<4, CONV, F32>), grid, block, 0, s, a); break;
-    case 256: BOA_LAUNCH((dec_b16_gemm_t128_kernel<8, CONV, F32>), grid, block, 0, s, a); break;
-    case 512: BOA_LAUNCH((dec_b16_gemm_t128_kernel<16, CONV, F32>), grid, block, 0, s, a); break;
-    case 1024: BOA_LAUNCH((dec_b16_gemm_t128_kernel<32, CONV, F32>), grid, block, 0, s, a); break;
-    case 2048: BOA_LAUNCH((dec_b16_gemm_t128_kernel<64, CONV, F32>), grid, block, 0, s, a); break;
+    case 64: BOA_LAUNCH((dec_b16_gemm_t128_kernel<2, CONV, F32, SC>), grid, block, 0, s, a); break;
+    case 128: BOA_LAUNCH((dec_b16_gemm_t128_kernel<4, CONV, F32, SC>), grid, block, 0, s, a); break;
+    case 256: BOA_LAUNCH((dec_b16_gemm_t128_kernel<8, CONV, F32, SC>), grid, block, 0, s, a); break;
+    case 512: BOA_LAUNCH((dec_b16_gemm_t128_kernel<16, CONV, F32, SC>), grid, block, 0, s, a); break;
+    case 1024: BOA_LAUNCH((dec_b16_gemm_t128_kernel<32, CONV, F32, SC>), grid, block, 0, s, a); break;
+    case 2048: BOA_LAUNCH((dec_b16_gemm_t128_kernel<64, CONV, F32, SC>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -595,10 +657,11 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   //   MB/s at C3, 0.95 -> 0.98 at C5)
   if (a.M >= 2048) {
     if ((a.out_mode == DEC_OUT_B16 || a.out_mode == DEC_OUT_F32) && a.N >= 512 &&
-        a.conv_di % 128 == 0) {
+        a.conv_di % 128 == 0 && (a.conv_di == 0 || a.bias)) {
       if (a.out_mode == DEC_OUT_F32) return dec_b16_t128_launch<false, true>(a, s);
-      return a.conv_di > 0 ? dec_b16_t128_launch<true, false>(a, s)
-                           : dec_b16_t128_launch<false, false>(a, s);
+      if (a.conv_di == 0) return dec_b16_t128_launch<false, false>(a, s);
+      return a.state_cached ? dec_b16_t128_launch<true, false, 1>(a, s)
+                            : dec_b16_t128_launch<true, false, 0>(a, s);
     }
     if (a.K >= 512) return dec_b16_lds_launch(a, s);
     return a.conv_di > 0 ? dec_b16_blk_launch<2, 2, true>(a, s) : dec_b16_blk_launch<2, 2, false>(a, s);

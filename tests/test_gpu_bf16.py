@@ -82,8 +82,9 @@ def test_bf16_many_lanes_step_equals_chunk_and_round_trip(torch_dev, make_weight
     """From 2048 lanes on the bf16 decode GEMMs run the many-lane forms (2 x 2
     tiles per wave, 64 x 64 LDS blocks, and 128 x 128 LDS blocks for in_proj
     and FF1 from d_model 128, a partial last block at 2100 lanes): step
-    logits stay bit-identical to chunk logits, and a container of 2101
-    chunks (one decode batch) round-trips byte for byte."""
+    logits stay bit-identical to chunk logits, with the state streamed
+    (cache budget 0) and through the caches (every layer), and a container
+    of 2101 chunks (one decode batch) round-trips byte for byte."""
     torch = torch_dev
     w = make_weights(d, L, ds)
     lanes, T = 2100, 5
@@ -95,12 +96,17 @@ def test_bf16_many_lanes_step_equals_chunk_and_round_trip(torch_dev, make_weight
     c.forward_chunk(torch.from_numpy(tok).cuda(), lanes, T, d_log)
     torch.cuda.synchronize()
     got = d_log.cpu().numpy().reshape(lanes, T, 256)
-    c.reset_state(lanes)
     d_s = torch.zeros(lanes * 256, dtype=torch.float32, device="cuda")
-    for t in range(T):
-        c.step_batch(torch.from_numpy(np.ascontiguousarray(tok[:, t])).cuda(), lanes, d_s, True)
-        st = d_s.cpu().numpy().reshape(lanes, 256)
-        assert np.array_equal(st.view(np.uint32), got[:, t].view(np.uint32)), f"step {t}"
+    for budget, want_cached in [(0, 0), (1 << 40, L)]:
+        c.set_state_cache_budget(budget)
+        assert c.decode_plan(lanes)["cached_layers"] == want_cached
+        c.reset_state(lanes)
+        for t in range(T):
+            c.step_batch(torch.from_numpy(np.ascontiguousarray(tok[:, t])).cuda(), lanes, d_s, True)
+            st = d_s.cpu().numpy().reshape(lanes, 256)
+            assert np.array_equal(st.view(np.uint32), got[:, t].view(np.uint32)), \
+                f"budget {budget} step {t}"
+    c.set_state_cache_budget(-1)
     data = synth.gen_c3(21)[:2100 * 40 + 7]
     blob = c.compress(data, chunk_size=40)
     assert c.decompress(blob) == data
