@@ -199,14 +199,16 @@ template <int DS, int M>
 constexpr bool scan_fused_update() {
   return M == MATH_HW && (DS == 16 || BOA_SCAN_B16_FUSED_DS32);
 }
-template <int DS, int RB, int M = MATH_BF>
-__device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt_in,
-                                            const float* bc, int r, float u, float z) {
+// The channel's parameters come from P: wdt(j), na(n), bdt(), dd() (the
+// registers of a ScanCtx, or shared memory); h is updated in place.
+template <int DS, int RB, int M, class P>
+__device__ __forceinline__ float scan_token_p(float (&h)[DS], const P& p, const float* dt_in,
+                                              const float* bc, int r, float u, float z) {
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < RB; ++j)
-    if (j < r) acc = __builtin_fmaf(dt_in[j], sc.wdt[j], acc);
-  const float dt = softplus<M>(acc + sc.bdt);
+    if (j < r) acc = __builtin_fmaf(dt_in[j], p.wdt(j), acc);
+  const float dt = softplus<M>(acc + p.bdt());
   const float* Bv = bc;
   const float* Cv = bc + DS;
   float y = 0.0f;
@@ -214,22 +216,35 @@ __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt
     const float dtu = dt * u;
 #pragma unroll
     for (int n = 0; n < DS; ++n) {
-      const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
-      sc.h[n] = __builtin_fmaf(dA, sc.h[n], Bv[n] * dtu);
-      y = __builtin_fmaf(sc.h[n], Cv[n], y);
+      const float dA = exp2_neg_sel<M>(p.na(n) * dt);
+      h[n] = __builtin_fmaf(dA, h[n], Bv[n] * dtu);
+      y = __builtin_fmaf(h[n], Cv[n], y);
     }
   } else {
 #pragma unroll
     for (int n = 0; n < DS; ++n) {
-      const float dA = exp2_neg_sel<M>(sc.na[n] * dt);
+      const float dA = exp2_neg_sel<M>(p.na(n) * dt);
       const float dB = dt * Bv[n];
-      sc.h[n] = dA * sc.h[n] + dB * u;
-      y = y + sc.h[n] * Cv[n];
+      h[n] = dA * h[n] + dB * u;
+      y = y + h[n] * Cv[n];
     }
   }
-  y = y + sc.dd * u;
+  y = y + p.dd() * u;
   float sg = rcp_sel<M>(1.0f + exp_sel<M>(-z));
   return y * (z * sg);
+}
+template <int DS, int RB>
+struct ScanRegs {
+  const ScanCtx<DS, RB>& c;
+  __device__ __forceinline__ float wdt(int j) const { return c.wdt[j]; }
+  __device__ __forceinline__ float na(int n) const { return c.na[n]; }
+  __device__ __forceinline__ float bdt() const { return c.bdt; }
+  __device__ __forceinline__ float dd() const { return c.dd; }
+};
+template <int DS, int RB, int M = MATH_BF>
+__device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt_in,
+                                            const float* bc, int r, float u, float z) {
+  return scan_token_p<DS, RB, M>(sc.h, ScanRegs<DS, RB>{sc}, dt_in, bc, r, u, z);
 }
 
 }  // namespace boa

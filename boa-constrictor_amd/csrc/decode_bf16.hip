@@ -849,6 +849,28 @@ hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w
 // ------------------------------------------------------------------- scan
 // As the fp32 step scan (16 channels x 16 lanes per block, quad-layout state
 // and parameters), with bf16 32-blocked u, z, rows and y.
+// Scan parameters of the block's 16 channels in shared memory, in the quad
+// layout of na_q / wdt_q (float f of quad k of channel cl at (k 16 + cl) 4 +
+// f), then b_dt and D.
+template <int DS, int RB>
+struct ScanLds {
+  const float* p;
+  int cl;
+  __device__ __forceinline__ float na(int n) const { return p[((n >> 2) * 16 + cl) * 4 + (n & 3)]; }
+  __device__ __forceinline__ float wdt(int j) const {
+    return p[DS * 16 + ((j >> 2) * 16 + cl) * 4 + (j & 3)];
+  }
+  __device__ __forceinline__ float bdt() const { return p[(DS + RB) * 16 + cl]; }
+  __device__ __forceinline__ float dd() const { return p[(DS + RB) * 16 + 16 + cl]; }
+};
+
+// One thread per (lane, channel), a block of 16 lanes x 16 channels.  The
+// block's x_proj rows (as floats) and its channels' parameters go to shared
+// memory, so that a thread's registers hold little beyond its state (d_state
+// 32: 128 VGPRs with rows and parameters in registers, four waves per SIMD,
+// for a kernel bound by moving the state).  Every thread issues the same
+// number of row and parameter loads (the last ones repeat the first), then
+// its state, u and z loads, which stay in flight across the barrier.
 template <int DS, int RB, bool CACHED>
 __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const float* __restrict__ na_q,
                                                            const float* __restrict__ wdt_q,
@@ -857,62 +879,83 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
                                                            const uint16_t* __restrict__ rows,
                                                            float* ssm, uint16_t* yt, int M, int ld,
                                                            int ld_state, int r) {
-  constexpr int NB = (RB + 2 * DS + 31) / 32;
-  // the block's 16 lanes' x_proj rows (NB 32-blocked 32-feature blocks
-  // each), loaded once and read by the 16 channel threads of each lane
-  __shared__ u32x4 srow[16 * NB * 4];
-  const int cl = threadIdx.x & 15;
+  constexpr int NB = (RB + 2 * DS + 31) / 32;    // 32-feature blocks of an x_proj row
+  constexpr int RW = NB * 32;                    // floats of a row in shared memory
+  constexpr int NR = 16 * NB * 4;                // 16-byte row loads of the block
+  constexpr int NP = (DS + RB) * 4 + 8;          // 16-byte parameter loads
+  constexpr int PER = (NR + NP + 255) / 256;     // loads per thread
+  static_assert(PER * 256 - (NR + NP) <= NR + NP, "repeated loads fall in range");
+  __shared__ __align__(16) float rowf[16 * RW];
+  __shared__ __align__(16) float4 par[NP];
+  const int tid = threadIdx.x, cl = tid & 15, lm = tid >> 4;
   const int cb = blockIdx.y;
   const int c = cb * 16 + cl;
   const int m0 = blockIdx.x * 16;
-  for (int qi = threadIdx.x; qi < 16 * NB * 4; qi += 256) {
-    const int lm = qi / (NB * 4), kb = (qi / 4) % NB, q4 = qi % 4;
-    const int mq = min(m0 + lm, M - 1);
-    srow[qi] = reinterpret_cast<const u32x4*>(rows)[((size_t)kb * ld + mq) * 4 + q4];
+  const int m = m0 + lm, mc = min(m, M - 1);
+  const u32x4* R4 = reinterpret_cast<const u32x4*>(rows);
+  const u32x4* na4 = reinterpret_cast<const u32x4*>(na_q) + (size_t)cb * (DS / 4) * 16;
+  const u32x4* w4 = reinterpret_cast<const u32x4*>(wdt_q) + (size_t)cb * (RB / 4) * 16;
+  // 1. rows and parameters
+  u32x4 v[PER];
+  int slot[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    int q = tid + 256 * k;
+    q = q < NR + NP ? q : q - (NR + NP);
+    slot[k] = q;
+    const u32x4* src;
+    if (q < NR) {
+      const int rl = q / (NB * 4), kb = (q / 4) % NB, q4 = q % 4;
+      src = R4 + ((size_t)kb * ld + min(m0 + rl, M - 1)) * 4 + q4;
+    } else {
+      const int p = q - NR;
+      src = p < DS * 4 ? na4 + p
+          : p < (DS + RB) * 4 ? w4 + (p - DS * 4)
+          : reinterpret_cast<const u32x4*>((p - (DS + RB) * 4 < 4 ? Lw.b_dt : Lw.dd) + 16 * cb) +
+                ((p - (DS + RB) * 4) & 3);
+    }
+    v[k] = *src;
   }
-  __syncthreads();
-  const int lm = threadIdx.x >> 4;
-  const int m = m0 + lm;
-  if (m >= M) return;  // after the block's only barrier
-  ScanCtx<DS, RB> sc;
+  // 2. the state, u and z (lane mc), in flight across the barrier
+  float h[DS];
   float4* h4 = reinterpret_cast<float4*>(ssm);
-  const float4* na4 = reinterpret_cast<const float4*>(na_q);
-  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 hv =
-        state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl, CACHED);
-    sc.h[4 * n4] = hv.x; sc.h[4 * n4 + 1] = hv.y; sc.h[4 * n4 + 2] = hv.z; sc.h[4 * n4 + 3] = hv.w;
-    const float4 av = na4[(cb * (DS / 4) + n4) * 16 + cl];
-    sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
+    const float4 hv = state_ld4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + mc) * 16 + cl, CACHED);
+    h[4 * n4] = hv.x; h[4 * n4 + 1] = hv.y; h[4 * n4 + 2] = hv.z; h[4 * n4 + 3] = hv.w;
   }
+  const size_t cm = dblk32(c, mc, ld);
+  const uint16_t ub = cvt[cm], zb = zt[cm];
+  // 3. rows (bf16 pairs to floats: feature 2 e of a word in its low half) and
+  // parameters to shared memory
 #pragma unroll
-  for (int j4 = 0; j4 < RB / 4; ++j4) {
-    const float4 wv = w4[(cb * (RB / 4) + j4) * 16 + cl];
-    sc.wdt[4 * j4] = wv.x; sc.wdt[4 * j4 + 1] = wv.y; sc.wdt[4 * j4 + 2] = wv.z; sc.wdt[4 * j4 + 3] = wv.w;
-  }
-  sc.bdt = Lw.b_dt[c];
-  sc.dd = Lw.dd[c];
-  float row[NB * 32];
-#pragma unroll
-  for (int kb = 0; kb < NB; ++kb)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const u32x4 v = srow[(lm * NB + kb) * 4 + q];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        row[32 * kb + 8 * q + 2 * e] = u2f(v[e] << 16);
-        row[32 * kb + 8 * q + 2 * e + 1] = u2f(v[e] & 0xFFFF0000u);
-      }
+  for (int k = 0; k < PER; ++k) {
+    const int q = slot[k];
+    if (q < NR) {
+      const int rl = q / (NB * 4), kb = (q / 4) % NB, q4 = q % 4;
+      float* o = rowf + rl * RW + 32 * kb + 8 * q4;
+      reinterpret_cast<float4*>(o)[0] = make_float4(u2f(v[k][0] << 16), u2f(v[k][0] & 0xFFFF0000u),
+                                                    u2f(v[k][1] << 16), u2f(v[k][1] & 0xFFFF0000u));
+      reinterpret_cast<float4*>(o)[1] = make_float4(u2f(v[k][2] << 16), u2f(v[k][2] & 0xFFFF0000u),
+                                                    u2f(v[k][3] << 16), u2f(v[k][3] & 0xFFFF0000u));
+    } else {
+      par[q - NR] = make_float4(u2f(v[k][0]), u2f(v[k][1]), u2f(v[k][2]), u2f(v[k][3]));
     }
-  const size_t cm = dblk32(c, m, ld);
-  const float u = bf16_to_f32(cvt[cm]);
-  const float z = bf16_to_f32(zt[cm]);
-  yt[cm] = f32_to_bf16(scan_token<DS, RB, MATH_HW>(sc, row, row + RB, r, u, z));
+  }
+  // LDS barrier without the fence of __syncthreads, which would also wait
+  // for the state loads: this wave's shared-memory stores are done at
+  // lgkmcnt(0)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (m >= M) return;  // after the block's only barrier
+  const float* row = rowf + lm * RW;
+  const float y = scan_token_p<DS, RB, MATH_HW>(
+      h, ScanLds<DS, RB>{reinterpret_cast<const float*>(par), cl}, row, row + RB, r,
+      bf16_to_f32(ub), bf16_to_f32(zb));
+  yt[dblk32(c, m, ld)] = f32_to_bf16(y);
 #pragma unroll
   for (int n4 = 0; n4 < DS / 4; ++n4)
     state_st4(h4 + ((size_t)(cb * (DS / 4) + n4) * ld_state + m) * 16 + cl,
-              make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), CACHED);
+              make_float4(h[4 * n4], h[4 * n4 + 1], h[4 * n4 + 2], h[4 * n4 + 3]), CACHED);
 }
 
 hipError_t launch_dec_b16_scan(const Dims& D, const LayerW& Lw, const float* na_q,
