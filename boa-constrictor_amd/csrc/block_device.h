@@ -241,6 +241,34 @@ struct ScanRegs {
   __device__ __forceinline__ float bdt() const { return c.bdt; }
   __device__ __forceinline__ float dd() const { return c.dd; }
 };
+// Scan parameters of 16 channels in shared memory, in the quad layout of
+// the decode step's na_q / wdt_q (float f of quad k of channel cl at
+// (k 16 + cl) 4 + f), then b_dt and D of the 16 channels: scan_lds_floats
+// floats a 16-channel block.
+template <int DS, int RB>
+constexpr int scan_lds_floats() { return (DS + RB) * 16 + 32; }
+template <int DS, int RB>
+struct ScanLds {
+  const float* p;
+  int cl;
+  __device__ __forceinline__ float na(int n) const { return p[((n >> 2) * 16 + cl) * 4 + (n & 3)]; }
+  __device__ __forceinline__ float wdt(int j) const {
+    return p[DS * 16 + ((j >> 2) * 16 + cl) * 4 + (j & 3)];
+  }
+  __device__ __forceinline__ float bdt() const { return p[(DS + RB) * 16 + cl]; }
+  __device__ __forceinline__ float dd() const { return p[(DS + RB) * 16 + 16 + cl]; }
+};
+// Source of float4 k (< scan_lds_floats / 4) of 16-channel block c16's
+// parameters in that layout.
+template <int DS, int RB>
+__device__ __forceinline__ const float4* scan_lds_src(const LayerW& Lw, const float* na_q,
+                                                      const float* wdt_q, int c16, int k) {
+  if (k < DS * 4) return reinterpret_cast<const float4*>(na_q) + (size_t)c16 * (DS / 4) * 16 + k;
+  if (k < (DS + RB) * 4)
+    return reinterpret_cast<const float4*>(wdt_q) + (size_t)c16 * (RB / 4) * 16 + (k - DS * 4);
+  const int j = k - (DS + RB) * 4;  // 0-3 b_dt, 4-7 D
+  return reinterpret_cast<const float4*>((j < 4 ? Lw.b_dt : Lw.dd) + 16 * c16) + (j & 3);
+}
 template <int DS, int RB, int M = MATH_BF>
 __device__ __forceinline__ float scan_token(ScanCtx<DS, RB>& sc, const float* dt_in,
                                             const float* bc, int r, float u, float z) {

@@ -1029,15 +1029,18 @@ __global__ __launch_bounds__(256) void dec_scan_kernel(LayerW Lw, const float* _
 // ------------------------------------------------ x_proj fused with the scan
 // dec_xscan_kernel runs x_proj and the scan of one layer in one launch.  A
 // block of 1024 threads owns 16 lanes x 128 channels:
-//   1. every thread issues the loads of its two channels' SSM state;
-//   2. waves 0 .. NB-1 each run one 16-feature block of the lanes' x_proj
+//   1. waves 0 .. NB-1 each run one 16-feature block of the lanes' x_proj
 //      row (dt_in, B, C; K = di) as dec_gemm_kernel's wave does -- the same
 //      K-ordered fma chain, then + 0 as the bias-free epilogue -- and store
 //      it to LDS in natural feature order (position 4g + v of a lane's
-//      float4 is feature 4v + g of its block);
+//      float4 is feature 4v + g of its block), then issue the loads of
+//      their threads' SSM state, conv output and z;
+//   2. meanwhile the other waves copy the block's scan parameters to LDS and
+//      issue the same loads for their threads;
 //   3. after the block's only barrier, each thread runs the scan of its lane
-//      for two channels (c and c + 64) in turn, reading dt_in, B and C from
-//      LDS (the 16 channel threads of a lane read the same words).
+//      for two channels (c and c + 64) in turn, reading dt_in, B and C and
+//      the parameters from LDS (the 16 channel threads of a lane read the
+//      same row words, the 16 lanes of a channel the same parameters).
 // x_proj is recomputed by the di / 128 blocks of a 16-lane tile (4 at
 // d_model 256) instead of being stored and reloaded, which removes a launch
 // and the rows' round trip per layer; the bits are those of dec_gemm +
@@ -1064,12 +1067,10 @@ struct XscanPos {
   }
 };
 
-// The loads of the x_proj + scan that depend on no other block: both
-// channels' state and the first channel's scan parameters.
+// A thread's state of both channels (loaded ahead of the scan).
 template <int DS, int RB>
 struct XscanPre {
   float h0[DS], h1[DS];
-  ScanCtx<DS, RB> sc0;
 };
 template <int DS, int RB, int DI, bool CACHED>
 __device__ __forceinline__ void xscan_load_state(XscanPre<DS, RB>& pr, const XscanPos<DI>& ps,
@@ -1089,29 +1090,9 @@ __device__ __forceinline__ void xscan_load_state(XscanPre<DS, RB>& pr, const Xsc
     pr.h1[4 * n4] = hv.x; pr.h1[4 * n4 + 1] = hv.y; pr.h1[4 * n4 + 2] = hv.z; pr.h1[4 * n4 + 3] = hv.w;
   }
 }
-template <int DS, int RB, int DI>
-__device__ __forceinline__ void xscan_load_params(XscanPre<DS, RB>& pr, const XscanPos<DI>& ps,
-                                                  const LayerW& Lw, const float* na_q,
-                                                  const float* wdt_q) {
-  const int c16 = 8 * ps.cb + ps.q, c = 16 * c16 + ps.cl;
-  const float4* na4 = reinterpret_cast<const float4*>(na_q);
-  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
-  ScanCtx<DS, RB>& sc0 = pr.sc0;
-#pragma unroll
-  for (int n4 = 0; n4 < DS / 4; ++n4) {
-    const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + ps.cl];
-    sc0.na[4 * n4] = av.x; sc0.na[4 * n4 + 1] = av.y; sc0.na[4 * n4 + 2] = av.z; sc0.na[4 * n4 + 3] = av.w;
-  }
-#pragma unroll
-  for (int j4 = 0; j4 < RB / 4; ++j4) {
-    const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + ps.cl];
-    sc0.wdt[4 * j4] = wv4.x; sc0.wdt[4 * j4 + 1] = wv4.y; sc0.wdt[4 * j4 + 2] = wv4.z; sc0.wdt[4 * j4 + 3] = wv4.w;
-  }
-  sc0.bdt = Lw.b_dt[c];
-  sc0.dd = Lw.dd[c];
-}
-// The block's work for virtual block vb, its x_proj rows in LDS at rown;
-// pl receives the loads that depend on no other block.
+// The block's work for virtual block vb, its x_proj rows in LDS at rown and
+// its 128 channels' scan parameters at par (eight 16-channel blocks of
+// scan_lds_floats); pl holds a thread's state.
 template <int DS, int RB, int DI, bool CACHED>
 __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __restrict__ na_q,
                                                const float* __restrict__ wdt_q,
@@ -1119,7 +1100,8 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
                                                const float* __restrict__ zt,
                                                const float* __restrict__ cvt, float* ssm, float* yt,
                                                int M, int ld, int ld_state, int r, int vb,
-                                               float* rown, int tid, XscanPre<DS, RB>& pl) {
+                                               float* rown, float* par, int tid,
+                                               XscanPre<DS, RB>& pl) {
   constexpr int NB = (RB + 2 * DS + 15) / 16;  // 16-feature blocks of the x_proj row
   constexpr int RS = NB * 16 + 4;              // LDS row stride (floats, 16-byte aligned)
   static_assert(NB <= 16 && DI % 128 == 0, "one wave per x_proj feature block");
@@ -1127,25 +1109,26 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
   const int cb = ps.cb, m0 = ps.m0, cl = ps.cl, lm = ps.lm, q = ps.q, m = ps.m, mc = ps.mc;
   if (m0 >= M) return;  // the whole block, before the barrier
   float4* h4 = reinterpret_cast<float4*>(ssm);
-  // 1. both channels' state (16-channel blocks 8 cb + q and 8 cb + q + 4),
-  // in flight during x_proj (loading the second one only after the first
-  // channel's scan measured 18.2 against 16.6 us per launch at 1000 lanes)
-  xscan_load_state<DS, RB, DI, CACHED>(pl, ps, ssm, ld_state);
-  const float* h0 = pl.h0;
-  const float* h1 = pl.h1;
-  // the two channels' conv output and z (of lane mc) and the first channel's
-  // scan parameters, also in flight during x_proj (16.45 -> 16.2 us)
-  float uz[2][2];
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const size_t cmp = dblk(16 * (8 * cb + q + 4 * p) + cl, mc, ld);
-    uz[p][0] = cvt[cmp];
-    uz[p][1] = zt[cmp];
-  }
-  xscan_load_params<DS, RB, DI>(pl, ps, Lw, na_q, wdt_q);
-  const ScanCtx<DS, RB>& sc0 = pl.sc0;
-  // 2. x_proj: wave w < NB computes feature block w for lanes m0 .. m0 + 15
   const int wv = tid >> 6;
+  // 1. both channels' state (16-channel blocks 8 cb + q and 8 cb + q + 4)
+  // and their conv output and z (of lane mc).  The waves that run x_proj
+  // issue them after
+  // it: the vector memory counter completes in order, so an x_proj operand
+  // load issued behind them would wait for the state's HBM round trip
+  // (18.2 us per launch at 1000 lanes with the second channel's state
+  // loaded after the first channel's scan, 16.6 with both before x_proj,
+  // 16.0 with the x_proj waves' own after it).
+  float uz[2][2];
+  auto load_scan_operands = [&]() {
+    xscan_load_state<DS, RB, DI, CACHED>(pl, ps, ssm, ld_state);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const size_t cmp = dblk(16 * (8 * cb + q + 4 * p) + cl, mc, ld);
+      uz[p][0] = cvt[cmp];
+      uz[p][1] = zt[cmp];
+    }
+  };
+  // 2. x_proj: wave w < NB computes feature block w for lanes m0 .. m0 + 15
   if (wv < NB) {
     const int lane = tid & 63, i = lane & 15, g = lane >> 4;
     DecGemmArgs a{};
@@ -1155,44 +1138,54 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
 #pragma unroll
     for (int v = 0; v < 4; ++v)  // the bias-free epilogue of dec_gemm_kernel: acc + 0
       rown[i * RS + 16 * wv + 4 * v + g] = acc[0][0][v] + 0.0f;
+    load_scan_operands();
+  } else {
+    // the other waves copy the block's scan parameters to LDS (through
+    // registers: a copy straight to LDS makes the compiler wait for every
+    // load in flight before the scan's LDS reads), loaded ahead of their
+    // scan operands so that the copies' waits do not cover those (scan
+    // 129 -> 123 us per decode step at 1000 lanes against each thread
+    // loading its channels' parameters, the second channel's after the
+    // first channel's scan)
+    constexpr int S4 = scan_lds_floats<DS, RB>() / 4, TOT = 8 * S4;
+    constexpr int NT = (16 - NB) * 64, PER = (TOT + NT - 1) / NT;
+    static_assert(PER * NT - TOT <= TOT, "repeated copies fall in range");
+    float4 v[PER];
+    int at[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      int t = tid - NB * 64 + NT * k;
+      t = t < TOT ? t : t - TOT;
+      at[k] = t;
+      v[k] = *scan_lds_src<DS, RB>(Lw, na_q, wdt_q, 8 * cb + t / S4, t % S4);
+    }
+    load_scan_operands();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) reinterpret_cast<float4*>(par)[at[k]] = v[k];
   }
-  __syncthreads();
+  // the block's only barrier, without the fence of __syncthreads (which
+  // would wait for every load in flight): the LDS stores are done at
+  // lgkmcnt(0)
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (m >= M) return;  // after the block's only barrier
   const float* row = rown + lm * RS;
-  const float4* na4 = reinterpret_cast<const float4*>(na_q);
-  const float4* w4 = reinterpret_cast<const float4*>(wdt_q);
   // 3. channels c and c + 64 of the lane, one after the other
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int c16 = 8 * cb + q + 4 * p;
     const int c = 16 * c16 + cl;
-    ScanCtx<DS, RB> sc;
-    if (p == 0) {
-      sc = sc0;
-    } else {
-#pragma unroll
-      for (int n4 = 0; n4 < DS / 4; ++n4) {
-        const float4 av = na4[(c16 * (DS / 4) + n4) * 16 + cl];
-        sc.na[4 * n4] = av.x; sc.na[4 * n4 + 1] = av.y; sc.na[4 * n4 + 2] = av.z; sc.na[4 * n4 + 3] = av.w;
-      }
-#pragma unroll
-      for (int j4 = 0; j4 < RB / 4; ++j4) {
-        const float4 wv4 = w4[(c16 * (RB / 4) + j4) * 16 + cl];
-        sc.wdt[4 * j4] = wv4.x; sc.wdt[4 * j4 + 1] = wv4.y; sc.wdt[4 * j4 + 2] = wv4.z; sc.wdt[4 * j4 + 3] = wv4.w;
-      }
-      sc.bdt = Lw.b_dt[c];
-      sc.dd = Lw.dd[c];
-    }
-#pragma unroll
-    for (int n = 0; n < DS; ++n) sc.h[n] = p == 0 ? h0[n] : h1[n];
     const size_t cm = dblk(c, m, ld);
     const float u = uz[p][0];
     const float z = uz[p][1];
-    yt[cm] = scan_token<DS, RB, MATH_BR>(sc, row, row + RB, r, u, z);
+    float h[DS];
+#pragma unroll
+    for (int n = 0; n < DS; ++n) h[n] = p == 0 ? pl.h0[n] : pl.h1[n];
+    const ScanLds<DS, RB> sp{par + (q + 4 * p) * scan_lds_floats<DS, RB>(), cl};
+    yt[cm] = scan_token_p<DS, RB, MATH_BR>(h, sp, row, row + RB, r, u, z);
 #pragma unroll
     for (int n4 = 0; n4 < DS / 4; ++n4)
       state_st4(h4 + ((size_t)(c16 * (DS / 4) + n4) * ld_state + m) * 16 + cl,
-                make_float4(sc.h[4 * n4], sc.h[4 * n4 + 1], sc.h[4 * n4 + 2], sc.h[4 * n4 + 3]), CACHED);
+                make_float4(h[4 * n4], h[4 * n4 + 1], h[4 * n4 + 2], h[4 * n4 + 3]), CACHED);
   }
 }
 
@@ -1205,9 +1198,10 @@ __global__ __launch_bounds__(1024) void dec_xscan_kernel(LayerW Lw, const float*
                                                          float* ssm, float* yt, int M, int ld,
                                                          int ld_state, int r) {
   __shared__ __align__(16) float rown[xscan_lds_floats<DS, RB>()];
+  __shared__ __align__(16) float par[8 * scan_lds_floats<DS, RB>()];
   XscanPre<DS, RB> pl;
   dec_xscan_body<DS, RB, DI, CACHED>(Lw, na_q, wdt_q, w_x, ldw_x, zt, cvt, ssm, yt, M, ld,
-                                            ld_state, r, blockIdx.x, rown, threadIdx.x, pl);
+                                     ld_state, r, blockIdx.x, rown, par, threadIdx.x, pl);
 }
 
 bool dec_xscan_fits(const Dims& D) {

@@ -849,21 +849,6 @@ hipError_t launch_dec_b16_ln2(const uint16_t* src, uint16_t* xnt, const float* w
 // ------------------------------------------------------------------- scan
 // As the fp32 step scan (16 channels x 16 lanes per block, quad-layout state
 // and parameters), with bf16 32-blocked u, z, rows and y.
-// Scan parameters of the block's 16 channels in shared memory, in the quad
-// layout of na_q / wdt_q (float f of quad k of channel cl at (k 16 + cl) 4 +
-// f), then b_dt and D.
-template <int DS, int RB>
-struct ScanLds {
-  const float* p;
-  int cl;
-  __device__ __forceinline__ float na(int n) const { return p[((n >> 2) * 16 + cl) * 4 + (n & 3)]; }
-  __device__ __forceinline__ float wdt(int j) const {
-    return p[DS * 16 + ((j >> 2) * 16 + cl) * 4 + (j & 3)];
-  }
-  __device__ __forceinline__ float bdt() const { return p[(DS + RB) * 16 + cl]; }
-  __device__ __forceinline__ float dd() const { return p[(DS + RB) * 16 + 16 + cl]; }
-};
-
 // One thread per (lane, channel), a block of 16 lanes x 16 channels.  The
 // block's x_proj rows (as floats) and its channels' parameters go to shared
 // memory, so that a thread's registers hold little beyond its state (d_state
