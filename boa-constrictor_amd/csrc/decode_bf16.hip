@@ -451,20 +451,23 @@ __device__ __forceinline__ void t128_conv_epilogue(const DecB16Args& a, const fl
   }
 }
 
-// SC: in_proj's conv state cache policy (t128_conv_epilogue; 0 otherwise)
-template <int KS, bool CONV, bool F32, int SC>
+// SC: in_proj's conv state cache policy (t128_conv_epilogue; 0 otherwise).
+// BM x BN blocks (128 x 128, or 64 x 64 for the 256-wide outputs), four
+// waves of (BM / 2) x (BN / 2).
+template <int KS, bool CONV, bool F32, int SC, int BM = 128, int BN = 128>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void dec_b16_gemm_t128_kernel(DecB16Args a) {
+  static_assert(!CONV || BN == 128, "the conv epilogue walks 64-feature wave columns");
   constexpr int NR = T128_RING, PF = (NR - 1 < KS ? NR - 1 : KS);  // stages issued ahead
-  constexpr int BM = 128, TMW = 4;             // lanes per block, lane tiles per wave
-  constexpr int NQ = (BM + 128) / 16;          // 1 KB copies per stage
+  constexpr int TMW = BM / 32, TNW = BN / 32;  // lane and feature tiles per wave
+  constexpr int NQ = (BM + BN) / 16;           // 1 KB copies per stage
   constexpr int IPW = NQ / 4;                  // of them per wave
-  // [ring stage][X rows 0 .. BM-1, then W rows 0 .. 127][row * 4 + quarter]
-  __shared__ __align__(16) u32x4 sm[NR][(BM + 128) * 4];
+  // [ring stage][X rows 0 .. BM-1, then W rows 0 .. BN-1][row * 4 + quarter]
+  __shared__ __align__(16) u32x4 sm[NR][(BM + BN) * 4];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i = lane & 15, g = lane >> 4;
-  const int2 mn = t128_block(blockIdx.x, (a.M + BM - 1) / BM, (a.N + 127) / 128);
-  const int m0 = mn.x * BM, n0 = mn.y * 128;
+  const int2 mn = t128_block(blockIdx.x, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN);
+  const int m0 = mn.x * BM, n0 = mn.y * BN;
   const u32x4* X4 = reinterpret_cast<const u32x4*>(a.X);
   const u32x4* W4 = reinterpret_cast<const u32x4*>(a.W);
   // DMA of k-step st: wave wv issues copies IPW wv .. IPW wv + IPW - 1 of
@@ -488,11 +491,11 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
     }
   };
   const int wm = wv >> 1, wn = wv & 1;
-  floatx4 acc[TMW][4];
+  floatx4 acc[TMW][TNW];
 #pragma unroll
   for (int tm = 0; tm < TMW; ++tm)
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) acc[tm][tn] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int tn = 0; tn < TNW; ++tn) acc[tm][tn] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < PF; ++st) issue(st);
 #pragma unroll 1
@@ -507,15 +510,21 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
     u32x4 xf[4], wf[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int rx = (BM / 2) * wm + 16 * t + i, rw = 64 * wn + 16 * t + i;
-      xf[t] = lds_read128(&sm[buf][rx * 4 + (g ^ ((rx >> 2) & 3))]);
-      wf[t] = lds_read128(&sm[buf][BM * 4 + rw * 4 + (g ^ ((rw >> 2) & 3))]);
+      if (t < TMW) {
+        const int rx = (BM / 2) * wm + 16 * t + i;
+        xf[t] = lds_read128(&sm[buf][rx * 4 + (g ^ ((rx >> 2) & 3))]);
+      }
+      if (t < TNW) {
+        const int rw = (BN / 2) * wn + 16 * t + i;
+        wf[t] = lds_read128(&sm[buf][BM * 4 + rw * 4 + (g ^ ((rw >> 2) & 3))]);
+      }
     }
-    lds_wait8(xf[0], xf[1], xf[2], xf[3], wf[0], wf[1], wf[2], wf[3]);
+    if constexpr (TMW == 4 && TNW == 4) lds_wait8(xf[0], xf[1], xf[2], xf[3], wf[0], wf[1], wf[2], wf[3]);
+    else lds_wait4(xf[0], xf[1], wf[0], wf[1]);
 #pragma unroll
     for (int tm = 0; tm < TMW; ++tm)
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn)
+      for (int tn = 0; tn < TNW; ++tn)
         acc[tm][tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8, wf[tn]), __builtin_bit_cast(bf16x8, xf[tm]), acc[tm][tn], 0,
             0, 0);
@@ -537,7 +546,7 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
   };
   ColOps col[2];
   auto load_col = [&](int tn, ColOps& o) {
-    const int nb = min(n0 + 64 * wn + 16 * tn + 4 * g, a.N - 4);  // N % 4 == 0
+    const int nb = min(n0 + (BN / 2) * wn + 16 * tn + 4 * g, a.N - 4);  // N % 4 == 0
     o.bias = a.bias ? *reinterpret_cast<const float4*>(a.bias + nb) : make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (F32) {
       if (a.res) {
@@ -552,10 +561,10 @@ void dec_b16_gemm_t128_kernel(DecB16Args a) {
   };
   load_col(0, col[0]);
 #pragma unroll
-  for (int tn = 0; tn < 4; ++tn) {
-    if (tn + 1 < 4) load_col(tn + 1, col[(tn + 1) & 1]);
+  for (int tn = 0; tn < TNW; ++tn) {
+    if (tn + 1 < TNW) load_col(tn + 1, col[(tn + 1) & 1]);
     const ColOps& c = col[tn & 1];
-    const int nb = n0 + 64 * wn + 16 * tn + 4 * g;
+    const int nb = n0 + (BN / 2) * wn + 16 * tn + 4 * g;
     const float bb[4] = {c.bias.x, c.bias.y, c.bias.z, c.bias.w};
 #pragma unroll
     for (int tm = 0; tm < TMW; ++tm) {
@@ -607,18 +616,20 @@ hipError_t dec_b16_lds_launch(const DecB16Args& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <bool CONV, bool F32, int SC = 0>
+template <bool CONV, bool F32, int SC = 0, int BM = 128, int BN = 128>
 hipError_t dec_b16_t128_launch(const DecB16Args& a, hipStream_t s) {
-  const dim3 grid(((a.M + 127) / 128) * ((a.N + 127) / 128)), block(256);
+  const dim3 grid(((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN)), block(256);
+#define BOA_T128(KSv) BOA_LAUNCH((dec_b16_gemm_t128_kernel<KSv, CONV, F32, SC, BM, BN>), grid, block, 0, s, a)
   switch (a.K) {
-    case 64: BOA_LAUNCH((dec_b16_gemm_t128_kernel<2, CONV, F32, SC>), grid, block, 0, s, a); break;
-    case 128: BOA_LAUNCH((dec_b16_gemm_t128_kernel<4, CONV, F32, SC>), grid, block, 0, s, a); break;
-    case 256: BOA_LAUNCH((dec_b16_gemm_t128_kernel<8, CONV, F32, SC>), grid, block, 0, s, a); break;
-    case 512: BOA_LAUNCH((dec_b16_gemm_t128_kernel<16, CONV, F32, SC>), grid, block, 0, s, a); break;
-    case 1024: BOA_LAUNCH((dec_b16_gemm_t128_kernel<32, CONV, F32, SC>), grid, block, 0, s, a); break;
-    case 2048: BOA_LAUNCH((dec_b16_gemm_t128_kernel<64, CONV, F32, SC>), grid, block, 0, s, a); break;
+    case 64: BOA_T128(2); break;
+    case 128: BOA_T128(4); break;
+    case 256: BOA_T128(8); break;
+    case 512: BOA_T128(16); break;
+    case 1024: BOA_T128(32); break;
+    case 2048: BOA_T128(64); break;
     default: return hipErrorInvalidValue;
   }
+#undef BOA_T128
   return hipGetLastError();
 }
 
@@ -651,6 +662,10 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   //   1.05 -> 1.11 MB/s, then out_proj and FF2 4.24 -> 3.84 ms, 1.153 ->
   //   1.187 MB/s; 64-lane blocks for the 256-wide out_proj and FF2 of C3
   //   were slower, 708 -> 774 us);
+  // - fp32 outputs (+ residual) under 512 wide with K >= 512 (C3's out_proj
+  //   and FF2): the same form in 64 x 64 blocks (C3 probe decode GEMMs 644
+  //   -> 635 us per step against the 64 x 64 register-staged blocks; two to
+  //   eight waves per SIMD measured even);
   // - the other GEMMs: 2 x 2 tiles per wave for K <= 256 (C3 decode 3.76 ->
   //   4.40 MB/s against one tile per wave; 4 x 4, 2 x 1 and 1 x 2 were
   //   slower) and the 64 x 64 LDS-tiled blocks for K >= 512 (4.40 -> 4.54
@@ -663,6 +678,8 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
       return a.state_cached ? dec_b16_t128_launch<true, false, 1>(a, s)
                             : dec_b16_t128_launch<true, false, 0>(a, s);
     }
+    if (a.out_mode == DEC_OUT_F32 && a.N % 64 == 0 && a.K >= 512)
+      return dec_b16_t128_launch<false, true, 0, 64, 64>(a, s);
     if (a.K >= 512) return dec_b16_lds_launch(a, s);
     return a.conv_di > 0 ? dec_b16_blk_launch<2, 2, true>(a, s) : dec_b16_blk_launch<2, 2, false>(a, s);
   }
