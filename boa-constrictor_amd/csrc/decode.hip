@@ -1112,12 +1112,11 @@ __device__ __forceinline__ void dec_xscan_body(const LayerW& Lw, const float* __
   const int wv = tid >> 6;
   // 1. both channels' state (16-channel blocks 8 cb + q and 8 cb + q + 4)
   // and their conv output and z (of lane mc).  The waves that run x_proj
-  // issue them after
-  // it: the vector memory counter completes in order, so an x_proj operand
-  // load issued behind them would wait for the state's HBM round trip
-  // (18.2 us per launch at 1000 lanes with the second channel's state
-  // loaded after the first channel's scan, 16.6 with both before x_proj,
-  // 16.0 with the x_proj waves' own after it).
+  // issue them after it: the vector memory counter completes in order, so
+  // an x_proj operand load issued behind them would wait for the state's
+  // HBM round trip (18.2 us per launch at 1000 lanes with the second
+  // channel's state loaded after the first channel's scan, 16.6 with both
+  // before x_proj, 16.1 with the x_proj waves' own after it).
   float uz[2][2];
   auto load_scan_operands = [&]() {
     xscan_load_state<DS, RB, DI, CACHED>(pl, ps, ssm, ld_state);

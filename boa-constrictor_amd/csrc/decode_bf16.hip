@@ -884,7 +884,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   constexpr int NB = (RB + 2 * DS + 31) / 32;    // 32-feature blocks of an x_proj row
   constexpr int RW = NB * 32;                    // floats of a row in shared memory
   constexpr int NR = 16 * NB * 4;                // 16-byte row loads of the block
-  constexpr int NP = (DS + RB) * 4 + 8;          // 16-byte parameter loads
+  constexpr int NP = scan_lds_floats<DS, RB>() / 4;  // 16-byte parameter loads
   constexpr int PER = (NR + NP + 255) / 256;     // loads per thread
   static_assert(PER * 256 - (NR + NP) <= NR + NP, "repeated loads fall in range");
   __shared__ __align__(16) float rowf[16 * RW];
@@ -895,8 +895,6 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
   const int m0 = blockIdx.x * 16;
   const int m = m0 + lm, mc = min(m, M - 1);
   const u32x4* R4 = reinterpret_cast<const u32x4*>(rows);
-  const u32x4* na4 = reinterpret_cast<const u32x4*>(na_q) + (size_t)cb * (DS / 4) * 16;
-  const u32x4* w4 = reinterpret_cast<const u32x4*>(wdt_q) + (size_t)cb * (RB / 4) * 16;
   // 1. rows and parameters
   u32x4 v[PER];
   int slot[PER];
@@ -910,11 +908,7 @@ __global__ __launch_bounds__(256) void dec_b16_scan_kernel(LayerW Lw, const floa
       const int rl = q / (NB * 4), kb = (q / 4) % NB, q4 = q % 4;
       src = R4 + ((size_t)kb * ld + min(m0 + rl, M - 1)) * 4 + q4;
     } else {
-      const int p = q - NR;
-      src = p < DS * 4 ? na4 + p
-          : p < (DS + RB) * 4 ? w4 + (p - DS * 4)
-          : reinterpret_cast<const u32x4*>((p - (DS + RB) * 4 < 4 ? Lw.b_dt : Lw.dd) + 16 * cb) +
-                ((p - (DS + RB) * 4) & 3);
+      src = reinterpret_cast<const u32x4*>(scan_lds_src<DS, RB>(Lw, na_q, wdt_q, cb, q - NR));
     }
     v[k] = *src;
   }
