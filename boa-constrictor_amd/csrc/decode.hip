@@ -527,16 +527,21 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
   // 16-k block q = 4 it + tid / 256 (row r / 4, quarter r % 4)
   const int r = tid & 255, ml = r >> 2, a4 = r & 3;
   const int m = min(m0 + ml, a.M - 1);  // rows past M are normalised, never stored
-  float4 xr[SQ];
+  stream_f4 xr[SQ];  // a vector type: an array of float4 structs went through scratch
   const float4* W4 = reinterpret_cast<const float4*>(a.W);
   const float* erow = EMB ? emb + (size_t)tok[m] * d : nullptr;
 #pragma unroll
   for (int it = 0; it < SQ; ++it) {
     const int q = 4 * it + (tid >> 8);
-    xr[it] = EMB ? *reinterpret_cast<const float4*>(erow + 16 * q + 4 * a4)
-                 : reinterpret_cast<const float4*>(a.Xt)[((size_t)q * a.ldx + m) * 4 + a4];
+    xr[it] = EMB ? *reinterpret_cast<const stream_f4*>(erow + 16 * q + 4 * a4)
+                 : reinterpret_cast<const stream_f4*>(a.Xt)[((size_t)q * a.ldx + m) * 4 + a4];
   }
-  for (int k = tid; k < d; k += 1024) { lwb[k] = lw[k]; lwb[d + k] = lb[k]; }
+  static_assert(d <= 1024, "one LayerNorm parameter per thread");
+  const int kp = min(tid, d - 1);
+  const float lwv = lw[kp], lbv = lb[kp];
+  // threads past d store parameter d - 1 again (the same value, no branch)
+  lwb[kp] = lwv;
+  lwb[d + kp] = lbv;
 #pragma unroll
   for (int it = 0; it < SQ; ++it) {
     const int q = 4 * it + (tid >> 8);
@@ -546,7 +551,7 @@ __device__ __forceinline__ void dec_ln_gemm_body(const DecGemmArgs& a, const flo
 #pragma unroll
       for (int e = 0; e < 4; ++e) row[dperm(4 * a4 + e)] = e4[e];
     } else {
-      reinterpret_cast<float4*>(row)[a4] = xr[it];
+      reinterpret_cast<stream_f4*>(row)[a4] = xr[it];
     }
   }
   // the weight rows go straight to LDS (global_load_lds_dwordx4: a wave's 64
