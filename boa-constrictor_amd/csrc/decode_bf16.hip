@@ -662,10 +662,13 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   //   1.05 -> 1.11 MB/s, then out_proj and FF2 4.24 -> 3.84 ms, 1.153 ->
   //   1.187 MB/s; 64-lane blocks for the 256-wide out_proj and FF2 of C3
   //   were slower, 708 -> 774 us);
-  // - fp32 outputs (+ residual) under 512 wide with K >= 512 (C3's out_proj
-  //   and FF2): the same form in 64 x 64 blocks (C3 probe decode GEMMs 644
-  //   -> 635 us per step against the 64 x 64 register-staged blocks; two to
-  //   eight waves per SIMD measured even);
+  // - outputs under 512 wide with K >= 512 (C3's FF2, fp32 + residual; its
+  //   out_proj and x_proj, bf16; C5's x_proj): the same form in 64 x 64
+  //   blocks (C3 probe decode GEMMs 644 -> 635 us per step for FF2, then
+  //   632 -> 616 with out_proj and x_proj, against the 64 x 64
+  //   register-staged blocks; two to eight waves per SIMD measured even);
+  //   x_proj's 48 or 96 columns fill the last block in part (the weight
+  //   rows past N read the last row, the stores test n < N);
   // - the other GEMMs: 2 x 2 tiles per wave for K <= 256 (C3 decode 3.76 ->
   //   4.40 MB/s against one tile per wave; 4 x 4, 2 x 1 and 1 x 2 were
   //   slower) and the 64 x 64 LDS-tiled blocks for K >= 512 (4.40 -> 4.54
@@ -680,6 +683,8 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
     }
     if (a.out_mode == DEC_OUT_F32 && a.N % 64 == 0 && a.K >= 512)
       return dec_b16_t128_launch<false, true, 0, 64, 64>(a, s);
+    if (a.out_mode == DEC_OUT_B16 && a.conv_di == 0 && a.N % 16 == 0 && a.K >= 512)
+      return dec_b16_t128_launch<false, false, 0, 64, 64>(a, s);
     if (a.K >= 512) return dec_b16_lds_launch(a, s);
     return a.conv_di > 0 ? dec_b16_blk_launch<2, 2, true>(a, s) : dec_b16_blk_launch<2, 2, false>(a, s);
   }
