@@ -384,6 +384,8 @@ hipError_t dec_gemm_cfg(const DecGemmArgs& a, int cfg, hipStream_t s) {
 // lanes the other K >= 256 shapes (out_proj, FF2, the heads) share their
 // weight fragments through LDS (at 1000 lanes 127 -> 110 us of these GEMMs
 // per decode step, three stages in flight; two measured 0.5 us slower).
+// At 4096 lanes the shared-weight form was slower for FF1 and for out_proj
+// and FF2 (decode GEMMs 991 -> 1014 and 1006 us per step).
 hipError_t dec_gemm(const DecGemmArgs& a, hipStream_t s) {
   int cfg = 4;
   if (a.K <= 256 && a.N >= 1024) cfg = 10;
