@@ -793,6 +793,7 @@ hipError_t step_range_b16(boa_ctx* c, int lane0, int lanes, hipStream_t s, int* 
     DecB16Args a{};
     a.X = X; a.ldx = ld; a.W = W; a.ldw = (int)round_up(N, 16); a.C = C; a.ldc = ld;
     a.out_mode = mode; a.bias = bias; a.M = lanes; a.N = N; a.K = K; a.act = act;
+    a.n_cus = c->n_cus;
     return a;
   };
   auto run = [&](const DecB16Args& a) {

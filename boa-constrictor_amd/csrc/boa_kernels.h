@@ -293,6 +293,7 @@ struct DecB16Args {
   float* conv_state; int ld_state;
   const float* conv_w; const float* conv_b; uint16_t* conv_out;
   int state_cached;             // conv state through the caches (1) or streamed (0)
+  int n_cus;                    // the device's compute units (0: 256), for the block shape
 };
 hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s);
 hipError_t launch_dec_b16_weight(const float* w, int ldw_in, int n_src, uint16_t* out, int K,

@@ -661,7 +661,10 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   //   us per step, decompress 4.88 -> 5.15 MB/s; C5 probe 5.58 -> 4.73 ms,
   //   1.05 -> 1.11 MB/s, then out_proj and FF2 4.24 -> 3.84 ms, 1.153 ->
   //   1.187 MB/s; 64-lane blocks for the 256-wide out_proj and FF2 of C3
-  //   were slower, 708 -> 774 us);
+  //   were slower, 708 -> 774 us), in 64 x 128 blocks where 128 x 128 ones
+  //   would leave under two per CU (C5's 512-wide out_proj, FF2 and head.1
+  //   at 8192 lanes: decode GEMMs 2174 -> 2108 us per step; the same for
+  //   its 2048-wide FF1, 1024 blocks, was slower);
   // - outputs under 512 wide with K >= 512 (C3's FF2, fp32 + residual; its
   //   out_proj and x_proj, bf16; C5's x_proj): the same form in 64 x 64
   //   blocks (C3 probe decode GEMMs 644 -> 635 us per step for FF2, then
@@ -676,8 +679,15 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   if (a.M >= 2048) {
     if ((a.out_mode == DEC_OUT_B16 || a.out_mode == DEC_OUT_F32) && a.N >= 512 &&
         a.conv_di % 128 == 0 && (a.conv_di == 0 || a.bias)) {
-      if (a.out_mode == DEC_OUT_F32) return dec_b16_t128_launch<false, true>(a, s);
-      if (a.conv_di == 0) return dec_b16_t128_launch<false, false>(a, s);
+      // fewer than two 128 x 128 blocks per CU: 64 x 128 blocks
+      const int cus = a.n_cus > 0 ? a.n_cus : 256;
+      const bool rows64 = (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128) < 2 * (int64_t)cus;
+      if (a.out_mode == DEC_OUT_F32)
+        return rows64 ? dec_b16_t128_launch<false, true, 0, 64, 128>(a, s)
+                      : dec_b16_t128_launch<false, true>(a, s);
+      if (a.conv_di == 0)
+        return rows64 ? dec_b16_t128_launch<false, false, 0, 64, 128>(a, s)
+                      : dec_b16_t128_launch<false, false>(a, s);
       return a.state_cached ? dec_b16_t128_launch<true, false, 1>(a, s)
                             : dec_b16_t128_launch<true, false, 0>(a, s);
     }
