@@ -666,10 +666,11 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
   //   at 8192 lanes: decode GEMMs 2174 -> 2108 us per step; the same for
   //   its 2048-wide FF1, 1024 blocks, was slower);
   // - outputs under 512 wide with K >= 512 (C3's FF2, fp32 + residual; its
-  //   out_proj and x_proj, bf16; C5's x_proj): the same form in 64 x 64
-  //   blocks (C3 probe decode GEMMs 644 -> 635 us per step for FF2, then
-  //   632 -> 616 with out_proj and x_proj, against the 64 x 64
-  //   register-staged blocks; two to eight waves per SIMD measured even);
+  //   out_proj and x_proj, bf16; C5's x_proj), and bf16 ones with K = 256
+  //   (C3's head.1): the same form in 64 x 64 blocks (C3 probe decode GEMMs
+  //   644 -> 635 us per step for FF2, then 632 -> 616 with out_proj and
+  //   x_proj, 626 -> 619 with head.1, against the 64 x 64 register-staged
+  //   and the 2 x 2-tile blocks; two to eight waves per SIMD measured even);
   //   x_proj's 48 or 96 columns fill the last block in part (the weight
   //   rows past N read the last row, the stores test n < N);
   // - the other GEMMs: 2 x 2 tiles per wave for K <= 256 (C3 decode 3.76 ->
@@ -693,7 +694,7 @@ hipError_t dec_b16_gemm(const DecB16Args& a, hipStream_t s) {
     }
     if (a.out_mode == DEC_OUT_F32 && a.N % 64 == 0 && a.K >= 512)
       return dec_b16_t128_launch<false, true, 0, 64, 64>(a, s);
-    if (a.out_mode == DEC_OUT_B16 && a.conv_di == 0 && a.N % 16 == 0 && a.K >= 512)
+    if (a.out_mode == DEC_OUT_B16 && a.conv_di == 0 && a.N % 16 == 0 && a.K >= 256)
       return dec_b16_t128_launch<false, false, 0, 64, 64>(a, s);
     if (a.K >= 512) return dec_b16_lds_launch(a, s);
     return a.conv_di > 0 ? dec_b16_blk_launch<2, 2, true>(a, s) : dec_b16_blk_launch<2, 2, false>(a, s);
